@@ -1,0 +1,153 @@
+/*
+ * lloom_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul path.
+ *
+ * This is the drop-in boundary a `QStorage::Hip` arm of lloom-tensor binds
+ * through a thin `lloom-hip-sys` crate (extern "C" declarations of exactly
+ * these functions).  Plain pointers and sizes only: every buffer argument
+ * named `*_dev` is device memory owned by the caller; `stream` is a
+ * hipStream_t (NULL = the context's own stream).
+ *
+ * Type ids are GGUF's (GgmlDType::to_u32, lloom-tensor/src/quantized/mod.rs
+ * :539-568): F32 = 0, F16 = 1, Q8_0 = 8, Q4K = 12, Q6K = 14, Q8K = 15.
+ * Weights are stored exactly as GGUF lays them out, [n, k] row-major rows of
+ * blocks (mod.rs:1915 "self is transposed so n is first then k"), with a tail
+ * pad (lloom_hip_weight_bytes) so vector loads past the last block stay in
+ * bounds, as the CUDA arm pads (quantized/cuda.rs:29-38).
+ *
+ * Every function returns 0 on success or a LLOOM_HIP_E* code; the message of
+ * the last failure on the calling thread is lloom_hip_last_error().  Bad
+ * arguments are refused by name, never downgraded (quantized/route.rs:1-10).
+ *
+ * Threading: one context serves one stream at a time (the reference issues
+ * every forward from one scheduler thread, lloom-engine/src/batch.rs:3-6).
+ * The context's workspace is reused by consecutive calls in stream order.
+ */
+#ifndef LLOOM_HIP_H
+#define LLOOM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    LLOOM_HIP_OK = 0,
+    LLOOM_HIP_EINVAL = 1,      /* null pointer, negative or zero size        */
+    LLOOM_HIP_EDTYPE = 2,      /* dtype not supported by this entry point   */
+    LLOOM_HIP_ESHAPE = 3,      /* k not a multiple of the block, mismatch   */
+    LLOOM_HIP_EEXPERT = 4,     /* an expert id >= n_experts                  */
+    LLOOM_HIP_EHIP = 5,        /* a HIP runtime call failed                 */
+    LLOOM_HIP_ENOMEM = 6,      /* device allocation failed                  */
+    LLOOM_HIP_EDEVICE = 7      /* no gfx950 device at that ordinal          */
+};
+
+enum {
+    LLOOM_HIP_F32 = 0,
+    LLOOM_HIP_F16 = 1,
+    LLOOM_HIP_Q8_0 = 8,
+    LLOOM_HIP_Q4K = 12,
+    LLOOM_HIP_Q6K = 14,
+    LLOOM_HIP_Q8K = 15
+};
+
+typedef struct lloom_hip_ctx lloom_hip_ctx;
+
+/* Message of the last failure on this thread ("" if none). */
+const char* lloom_hip_last_error(void);
+
+/* Library version string. */
+const char* lloom_hip_version(void);
+
+/* --------------------------------------------------------------- context --
+ * Replaces CudaDevice::new (lloom-tensor/src/cuda_backend/device.rs:59-68)
+ * for the quantized arm: binds a device ordinal, creates the context stream
+ * and the grow-only workspace (quantized/fast_mmvq.rs:49-80). */
+int lloom_hip_ctx_create(int device, lloom_hip_ctx** out);
+int lloom_hip_ctx_destroy(lloom_hip_ctx* ctx);
+/* The context stream (hipStream_t), for callers that share it. */
+void* lloom_hip_ctx_stream(lloom_hip_ctx* ctx);
+/* Decode/GEMM route knob: rows <= mv_rows_max take the fused matvec,
+ * more rows the MFMA GEMM (default 16, range 1..16).  The reference's knobs
+ * are MMVQ_MAX_BATCH (fast_mmvq.rs:38) and qmv.mm_from (tuning.rs:1413). */
+int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows);
+/* Wait for the context stream; report a device-side error (an out-of-range
+ * expert id seen by a routed matmul) recorded since the last check. */
+int lloom_hip_ctx_sync(lloom_hip_ctx* ctx);
+
+/* ---------------------------------------------------------------- memory --
+ * Device buffers for callers without a tensor runtime (the Rust HipStorage).
+ * QCudaStorage::zeros / load_quantized (quantized/cuda.rs:624-637, 1005-1024). */
+int lloom_hip_alloc(lloom_hip_ctx* ctx, size_t bytes, void** out_dev);
+int lloom_hip_free(lloom_hip_ctx* ctx, void* dev);
+int lloom_hip_memcpy_h2d(lloom_hip_ctx* ctx, void* dst_dev, const void* src, size_t bytes,
+                         void* stream);
+int lloom_hip_memcpy_d2h(lloom_hip_ctx* ctx, void* dst, const void* src_dev, size_t bytes,
+                         void* stream);
+
+/* Bytes of the packed blocks of an [n, k] weight (no pad), and the bytes to
+ * allocate for it (with the tail pad).  k must be a multiple of the block. */
+int lloom_hip_weight_bytes(int ggml_type, int64_t n, int64_t k, size_t* packed_bytes,
+                           size_t* alloc_bytes);
+
+/* -------------------------------------------------------------- quantize --
+ * QTensor::quantize (mod.rs:919-938) -> QStorage::quantize (:257-267) for a
+ * device f32 source: BlockQ8_0/Q4K/Q6K/Q8K::from_float (k_quants.rs:738-767,
+ * 1622-1680, 2174-2244, 2400-2438), bit for bit, on the GPU.  elems must be
+ * a multiple of the block size. */
+int lloom_hip_quantize(lloom_hip_ctx* ctx, int ggml_type, const float* src_dev, int64_t elems,
+                       void* dst_dev, void* stream);
+
+/* Activation quantization of an [m, k] f32 matrix to the weight's VecDotType
+ * (Q8_0 for Q8_0 weights, Q8K for Q4K/Q6K), as k_quants::matmul does before
+ * its dots (k_quants.rs:2477-2508).  Bit-exact with from_float.  The CUDA arm
+ * quantizes to Q8_1 instead (quantized/cuda.rs:48-103). */
+int lloom_hip_quantize_act(lloom_hip_ctx* ctx, int vec_dot_type, const float* x_dev, int64_t m,
+                           int64_t k, void* out_dev, void* stream);
+
+/* ------------------------------------------------------------ dequantize --
+ * QTensor::dequantize / dequantize_f16 (mod.rs:1065-1086), to_float of
+ * k_quants.rs:720-736, 1747-1774, 2327-2358, 2440-2451; out_dtype F32 or F16
+ * (f16 = RNE of the f32 value, as Tensor::to_dtype does).  Bit-exact. */
+int lloom_hip_dequantize(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t elems,
+                         void* y_dev, int out_dtype, void* stream);
+
+/* ---------------------------------------------------------------- matmul --
+ * QMatMul::forward -> CustomOp1 for QTensor (mod.rs:1901-2020, 2022-2025):
+ * y[m, n] = x[m, k] . W[n, k]^T with W packed (ggml_type Q8_0/Q4K/Q6K) and
+ * x f32.  Replaces QCudaStorage::fwd (quantized/cuda.rs:862-894).  Each call
+ * quantizes x to the VecDotType exactly as the CPU arm does; the dots then
+ * run in integer arithmetic with f32 scales, within 1e-3 * max|y row| of the
+ * CPU result.  x_dtype / y_dtype: F32 only in this version (F16 is refused
+ * by name: LLOOM_HIP_EDTYPE). */
+int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                      const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype,
+                      void* stream);
+
+/* ------------------------------------------------------- routed experts --
+ * QTensor::indexed_moe_forward{,_with,_as} (mod.rs:1560-1645), CPU arm
+ * matmul_t_indexed (mod.rs:766-810): W [n_experts, n, k] packed, x f32
+ * [batch, in_dim1, k] with in_dim1 in {1, topk}, ids u32 [batch, topk],
+ * y f32 [batch, topk, n]; plane (b, t) = x[b, t or 0] . W[ids[b, t]]^T.
+ * The dots are f32 over dequantized weight rows, as the CPU arm computes
+ * them (no activation quantization).  An id >= n_experts yields a zero plane
+ * and LLOOM_HIP_EEXPERT from this call (it synchronizes the stream to read
+ * the device flag) unless strict is 0, in which case the next
+ * lloom_hip_ctx_sync reports it. */
+int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n_experts,
+                         int64_t n, int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1,
+                         const uint32_t* ids_dev, int64_t topk, float* y_dev, int strict,
+                         void* stream);
+
+/* ------------------------------------------------------- synthetic data --
+ * The benchmark/test input generator (not part of the reference): SplitMix64
+ * seeding xoshiro256**, Box-Muller normals N(mean, std) written as f32 into a
+ * host buffer.  Deterministic for a seed on every host. */
+int lloom_hip_synth_normal(uint64_t seed, float mean, float std, float* out, int64_t count);
+int lloom_hip_synth_uniform(uint64_t seed, float lo, float hi, float* out, int64_t count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,311 @@
+// api.hip -- the C ABI (include/lloom_hip.h): argument checks, the context
+// (device, stream, grow-only workspace) and dispatch to the kernels.
+//
+// The argument checks mirror the CPU arm's refusals, by name:
+//   k not a multiple of the block     mod.rs:775-780, check_shape (mod.rs:900-907)
+//   x last dim != weight k            CustomOp1::cpu_fwd (mod.rs:1920-1923)
+//   MoE shapes                        indexed_moe_forward_as (mod.rs:1616-1623)
+//   expert id out of range            matmul_t_indexed (mod.rs:796-798)
+//   unsupported dtype                 QStorage::from_data (mod.rs:206-220)
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/lloom_hip.h"
+#include "kernels.hpp"
+#include "kq_common.hpp"
+
+using namespace lloom;
+
+struct lloom_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;  // grow-only workspace
+    size_t ws_bytes = 0;
+    int* flags = nullptr;  // [0] sticky expert-id error
+    int mv_rows_max = 16;
+    std::mutex mu;
+};
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_OK(expr)                                                                         \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess) return fail(LLOOM_HIP_EHIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+static hipStream_t pick_stream(lloom_hip_ctx* ctx, void* stream) {
+    return stream ? (hipStream_t)stream : ctx->stream;
+}
+
+static bool is_weight_type(int t) { return t == T_Q8_0 || t == T_Q4K || t == T_Q6K; }
+
+static const char* type_name(int t) {
+    switch (t) {
+        case T_F32: return "F32";
+        case T_F16: return "F16";
+        case T_Q8_0: return "Q8_0";
+        case T_Q4K: return "Q4K";
+        case T_Q6K: return "Q6K";
+        case T_Q8K: return "Q8K";
+    }
+    return "unknown";
+}
+
+// Workspace of at least `bytes`, 256-byte aligned; grows, never shrinks
+// (the CUDA arm's per-device workspace, quantized/fast_mmvq.rs:49-80).
+static int ensure_ws(lloom_hip_ctx* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->ws_bytes) {
+        if (ctx->ws) {
+            HIP_OK(hipStreamSynchronize(ctx->stream));
+            HIP_OK(hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        size_t want = (bytes + 0xFFFFF) & ~(size_t)0xFFFFF;
+        if (hipMalloc(&ctx->ws, want) != hipSuccess)
+            return fail(LLOOM_HIP_ENOMEM, "workspace allocation of %zu bytes failed", want);
+        ctx->ws_bytes = want;
+    }
+    *out = ctx->ws;
+    return LLOOM_HIP_OK;
+}
+
+extern "C" {
+
+const char* lloom_hip_last_error(void) { return g_err.c_str(); }
+
+const char* lloom_hip_version(void) { return "lloom-hip 0.1 (gfx950)"; }
+
+int lloom_hip_ctx_create(int device, lloom_hip_ctx** out) {
+    if (!out) return fail(LLOOM_HIP_EINVAL, "ctx_create: out is null");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count)
+        return fail(LLOOM_HIP_EDEVICE, "ctx_create: no HIP device %d (%d visible)", device, count);
+    hipDeviceProp_t prop;
+    HIP_OK(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(LLOOM_HIP_EDEVICE, "ctx_create: device %d is %s, this library is built for gfx950", device,
+                    prop.gcnArchName);
+    HIP_OK(hipSetDevice(device));
+    lloom_hip_ctx* c = new lloom_hip_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fail(LLOOM_HIP_EHIP, "ctx_create: stream creation failed");
+    }
+    if (hipMalloc(&c->flags, 256) != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return fail(LLOOM_HIP_ENOMEM, "ctx_create: flag allocation failed");
+    }
+    (void)hipMemset(c->flags, 0, 256);
+    (void)hipDeviceSynchronize();
+    *out = c;
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_ctx_destroy(lloom_hip_ctx* ctx) {
+    if (!ctx) return LLOOM_HIP_OK;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->flags) (void)hipFree(ctx->flags);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return LLOOM_HIP_OK;
+}
+
+void* lloom_hip_ctx_stream(lloom_hip_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows) {
+    if (!ctx) return fail(LLOOM_HIP_EINVAL, "set_mv_rows_max: null context");
+    if (rows < 1 || rows > 16) return fail(LLOOM_HIP_EINVAL, "set_mv_rows_max: %d is outside 1..16", rows);
+    ctx->mv_rows_max = rows;
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_ctx_sync(lloom_hip_ctx* ctx) {
+    if (!ctx) return fail(LLOOM_HIP_EINVAL, "ctx_sync: null context");
+    HIP_OK(hipSetDevice(ctx->device));
+    HIP_OK(hipStreamSynchronize(ctx->stream));
+    int flag = 0;
+    HIP_OK(hipMemcpy(&flag, ctx->flags, sizeof(int), hipMemcpyDeviceToHost));
+    if (flag) {
+        int zero = 0;
+        HIP_OK(hipMemcpy(ctx->flags, &zero, sizeof(int), hipMemcpyHostToDevice));
+        return fail(LLOOM_HIP_EEXPERT, "a routed matmul saw an expert id out of range for its experts");
+    }
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_alloc(lloom_hip_ctx* ctx, size_t bytes, void** out_dev) {
+    if (!ctx || !out_dev) return fail(LLOOM_HIP_EINVAL, "alloc: null argument");
+    HIP_OK(hipSetDevice(ctx->device));
+    if (hipMalloc(out_dev, bytes ? bytes : 1) != hipSuccess)
+        return fail(LLOOM_HIP_ENOMEM, "alloc: %zu bytes failed", bytes);
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_free(lloom_hip_ctx* ctx, void* dev) {
+    if (!ctx) return fail(LLOOM_HIP_EINVAL, "free: null context");
+    if (dev) HIP_OK(hipFree(dev));
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_memcpy_h2d(lloom_hip_ctx* ctx, void* dst_dev, const void* src, size_t bytes, void* stream) {
+    if (!ctx || (!dst_dev && bytes) || (!src && bytes)) return fail(LLOOM_HIP_EINVAL, "memcpy_h2d: null argument");
+    hipStream_t s = pick_stream(ctx, stream);
+    HIP_OK(hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, s));
+    HIP_OK(hipStreamSynchronize(s));
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_memcpy_d2h(lloom_hip_ctx* ctx, void* dst, const void* src_dev, size_t bytes, void* stream) {
+    if (!ctx || (!dst && bytes) || (!src_dev && bytes)) return fail(LLOOM_HIP_EINVAL, "memcpy_d2h: null argument");
+    hipStream_t s = pick_stream(ctx, stream);
+    HIP_OK(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, s));
+    HIP_OK(hipStreamSynchronize(s));
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_weight_bytes(int ggml_type, int64_t n, int64_t k, size_t* packed_bytes, size_t* alloc_bytes) {
+    int be = block_elems(ggml_type);
+    if (!be) return fail(LLOOM_HIP_EDTYPE, "weight_bytes: dtype %s (%d) is not a block type", type_name(ggml_type), ggml_type);
+    if (n < 0 || k < 0) return fail(LLOOM_HIP_EINVAL, "weight_bytes: negative shape");
+    if (k % be) return fail(LLOOM_HIP_ESHAPE, "weight_bytes: k %lld is not divisible by block size %d", (long long)k, be);
+    size_t b = (size_t)n * (size_t)(k / be) * (size_t)block_bytes(ggml_type);
+    if (packed_bytes) *packed_bytes = b;
+    if (alloc_bytes) *alloc_bytes = b + WEIGHT_TAIL_PAD;
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_quantize(lloom_hip_ctx* ctx, int ggml_type, const float* src_dev, int64_t elems, void* dst_dev,
+                       void* stream) {
+    if (!ctx || !src_dev || !dst_dev) return fail(LLOOM_HIP_EINVAL, "quantize: null argument");
+    int be = block_elems(ggml_type);
+    if (!be) return fail(LLOOM_HIP_EDTYPE, "quantize: %s (%d) is not supported on the HIP quantized path", type_name(ggml_type), ggml_type);
+    if (elems <= 0 || elems % be)
+        return fail(LLOOM_HIP_ESHAPE, "quantize: tensor size %lld is not divisible by block size %d", (long long)elems, be);
+    if ((uintptr_t)src_dev % 16 || (uintptr_t)dst_dev % 4)
+        return fail(LLOOM_HIP_EINVAL, "quantize: src must be 16-byte and dst 4-byte aligned");
+    HIP_OK(hipSetDevice(ctx->device));
+    HIP_OK(launch_quantize_weights(ggml_type, src_dev, dst_dev, elems, pick_stream(ctx, stream)));
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_quantize_act(lloom_hip_ctx* ctx, int vec_dot_type, const float* x_dev, int64_t m, int64_t k,
+                           void* out_dev, void* stream) {
+    if (!ctx || !x_dev || !out_dev) return fail(LLOOM_HIP_EINVAL, "quantize_act: null argument");
+    if (vec_dot_type != T_Q8_0 && vec_dot_type != T_Q8K)
+        return fail(LLOOM_HIP_EDTYPE, "quantize_act: %s (%d) is not a vec-dot type (Q8_0 or Q8K)", type_name(vec_dot_type), vec_dot_type);
+    int be = block_elems(vec_dot_type);
+    if (m <= 0 || k <= 0) return fail(LLOOM_HIP_EINVAL, "quantize_act: empty shape (%lld, %lld)", (long long)m, (long long)k);
+    if (k % be) return fail(LLOOM_HIP_ESHAPE, "quantize_act: k %lld is not divisible by block size %d", (long long)k, be);
+    if ((uintptr_t)x_dev % 16 || (uintptr_t)out_dev % 4)
+        return fail(LLOOM_HIP_EINVAL, "quantize_act: x must be 16-byte and out 4-byte aligned");
+    HIP_OK(hipSetDevice(ctx->device));
+    HIP_OK(launch_quantize_act(vec_dot_type, x_dev, out_dev, m * k, pick_stream(ctx, stream)));
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_dequantize(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t elems, void* y_dev,
+                         int out_dtype, void* stream) {
+    if (!ctx || !w_dev || !y_dev) return fail(LLOOM_HIP_EINVAL, "dequantize: null argument");
+    int be = block_elems(ggml_type);
+    if (!be) return fail(LLOOM_HIP_EDTYPE, "dequantize: %s (%d) is not supported on the HIP quantized path", type_name(ggml_type), ggml_type);
+    if (out_dtype != T_F32 && out_dtype != T_F16)
+        return fail(LLOOM_HIP_EDTYPE, "dequantize: output dtype %s (%d) must be F32 or F16", type_name(out_dtype), out_dtype);
+    if (elems <= 0 || elems % be)
+        return fail(LLOOM_HIP_ESHAPE, "dequantize: %lld elements is not divisible by block size %d", (long long)elems, be);
+    if ((uintptr_t)w_dev % 4) return fail(LLOOM_HIP_EINVAL, "dequantize: weight must be 4-byte aligned");
+    HIP_OK(hipSetDevice(ctx->device));
+    HIP_OK(launch_dequantize(ggml_type, w_dev, y_dev, out_dtype, elems, pick_stream(ctx, stream)));
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                      const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, void* stream) {
+    if (!ctx || !w_dev || !x_dev || !y_dev) return fail(LLOOM_HIP_EINVAL, "qmatmul: null argument");
+    if (!is_weight_type(ggml_type))
+        return fail(LLOOM_HIP_EDTYPE, "qmatmul: weight dtype %s (%d) is not supported on the HIP quantized path (Q8_0, Q4K, Q6K)", type_name(ggml_type), ggml_type);
+    if (x_dtype != T_F32 || y_dtype != T_F32)
+        return fail(LLOOM_HIP_EDTYPE, "qmatmul: activation dtypes %s -> %s: only F32 -> F32 is supported", type_name(x_dtype), type_name(y_dtype));
+    int be = block_elems(ggml_type);
+    if (n <= 0 || k <= 0 || m <= 0)
+        return fail(LLOOM_HIP_EINVAL, "qmatmul: empty shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+    if (k % be) return fail(LLOOM_HIP_ESHAPE, "qmatmul: k %lld is not divisible by block size %d", (long long)k, be);
+    if (n > INT32_MAX || k > INT32_MAX || m > INT32_MAX) return fail(LLOOM_HIP_ESHAPE, "qmatmul: dimension exceeds 2^31");
+    if ((uintptr_t)w_dev % (ggml_type == T_Q4K ? 16 : 4))
+        return fail(LLOOM_HIP_EINVAL, "qmatmul: weight pointer is not %d-byte aligned", ggml_type == T_Q4K ? 16 : 4);
+    if ((uintptr_t)x_dev % 16) return fail(LLOOM_HIP_EINVAL, "qmatmul: x must be 16-byte aligned");
+    HIP_OK(hipSetDevice(ctx->device));
+    hipStream_t s = pick_stream(ctx, stream);
+    if (m <= ctx->mv_rows_max) {
+        HIP_OK(launch_matvec(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, s));
+        return LLOOM_HIP_OK;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    void* qbuf = nullptr;
+    size_t need = gemm_workspace_bytes(ggml_type, k, m);
+    if (need) {
+        int rc = ensure_ws(ctx, need, &qbuf);
+        if (rc) return rc;
+    }
+    HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, qbuf, s));
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n_experts, int64_t n,
+                         int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1, const uint32_t* ids_dev,
+                         int64_t topk, float* y_dev, int strict, void* stream) {
+    if (!ctx || !w_dev || !x_dev || !ids_dev || !y_dev) return fail(LLOOM_HIP_EINVAL, "moe_matmul: null argument");
+    if (!is_weight_type(ggml_type))
+        return fail(LLOOM_HIP_EDTYPE, "moe_matmul: weight dtype %s (%d) is not supported on the HIP quantized path", type_name(ggml_type), ggml_type);
+    int be = block_elems(ggml_type);
+    if (n_experts <= 0 || n <= 0 || k <= 0 || batch <= 0 || topk <= 0)
+        return fail(LLOOM_HIP_EINVAL, "moe_matmul: empty shape");
+    if (k % be) return fail(LLOOM_HIP_ESHAPE, "routed matmul k %lld is not divisible by block size %d", (long long)k, be);
+    if (in_dim1 != 1 && in_dim1 != topk)
+        return fail(LLOOM_HIP_ESHAPE, "indexed_moe_forward: x dim 1 (%lld) must be 1 or topk (%lld)", (long long)in_dim1, (long long)topk);
+    if (batch * topk > (1 << 24) || n_experts > (1 << 20) || n > INT32_MAX || k > INT32_MAX)
+        return fail(LLOOM_HIP_ESHAPE, "moe_matmul: shape too large");
+    if ((uintptr_t)w_dev % (ggml_type == T_Q4K ? 16 : 4) || (uintptr_t)x_dev % 16)
+        return fail(LLOOM_HIP_EINVAL, "moe_matmul: misaligned weight or x pointer");
+    HIP_OK(hipSetDevice(ctx->device));
+    hipStream_t s = pick_stream(ctx, stream);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    void* ws = nullptr;
+    int rc = ensure_ws(ctx, moe_workspace_ints(n_experts, batch * topk) * sizeof(int), &ws);
+    if (rc) return rc;
+    HIP_OK(launch_moe(ggml_type, w_dev, n_experts, n, k, x_dev, batch, in_dim1, ids_dev, topk, y_dev, (int*)ws,
+                      ctx->flags, s));
+    if (strict) {
+        int flag = 0;
+        HIP_OK(hipMemcpyAsync(&flag, ws, sizeof(int), hipMemcpyDeviceToHost, s));
+        HIP_OK(hipStreamSynchronize(s));
+        if (flag) {
+            int zero = 0;
+            HIP_OK(hipMemcpy(ctx->flags, &zero, sizeof(int), hipMemcpyHostToDevice));
+            return fail(LLOOM_HIP_EEXPERT, "expert id is out of range for %lld experts", (long long)n_experts);
+        }
+    }
+    return LLOOM_HIP_OK;
+}
+
+}  // extern "C"

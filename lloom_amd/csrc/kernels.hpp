@@ -1,0 +1,30 @@
+// kernels.hpp -- launchers of the gfx950 kernels (host side of each .hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace lloom {
+
+// quant.hip
+hipError_t launch_quantize_act(int vec_dot_type, const float* x, void* out, int64_t elems, hipStream_t s);
+hipError_t launch_quantize_weights(int type, const float* x, void* out, int64_t elems, hipStream_t s);
+hipError_t launch_dequantize(int type, const void* w, void* y, int out_dtype, int64_t elems, hipStream_t s);
+
+// matvec.hip: m <= 16
+hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
+                         hipStream_t s);
+
+// gemm.hip: any m, int8 MFMA; qbuf is workspace for the quantized x
+hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
+                       void* qbuf, hipStream_t s);
+size_t gemm_workspace_bytes(int type, int64_t k, int64_t m);
+
+// moe.hip
+size_t moe_workspace_ints(int64_t n_experts, int64_t planes);
+hipError_t launch_moe(int type, const void* w, int64_t n_experts, int64_t n, int64_t k, const float* x,
+                      int64_t batch, int64_t in_dim1, const uint32_t* ids, int64_t topk, float* y, int* ws,
+                      int* sticky, hipStream_t s);
+
+}  // namespace lloom

@@ -1,0 +1,114 @@
+// kq_common.hpp -- block layouts and device helpers shared by the gfx950
+// kernels of the quantized-matmul path.
+//
+// Block layouts are GGUF's, as lloom-tensor declares them
+// (lloom-tensor/src/quantized/k_quants.rs:154-159, 216-223, 254-261,
+// 264-270): the kernels read the packed bytes exactly as a GGUF file stores
+// them, so QStorage::from_data is a plain upload.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lloom {
+
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+
+constexpr int T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4K = 12, T_Q6K = 14, T_Q8K = 15;
+
+constexpr int Q8_0_BYTES = 34;   // f16 d, i8 qs[32]
+constexpr int Q4K_BYTES = 144;   // f16 d, f16 dmin, u8 scales[12], u8 qs[128]
+constexpr int Q6K_BYTES = 210;   // u8 ql[128], u8 qh[64], i8 scales[16], f16 d
+constexpr int Q8K_BYTES = 292;   // f32 d, i8 qs[256], i16 bsums[16]
+
+// Offsets inside a Q6K block.
+constexpr int Q6K_QH = 128, Q6K_SC = 192, Q6K_D = 208;
+// Offsets inside a Q8K block.
+constexpr int Q8K_QS = 4, Q8K_BS = 260;
+
+// Tail pad after a weight buffer: realigning loads read at most 3 bytes
+// past a block, the fused kernels never more than one 16-byte vector.
+constexpr size_t WEIGHT_TAIL_PAD = 512;
+
+__host__ __device__ inline int block_elems(int t) {
+    return t == T_Q8_0 ? QK8_0 : (t == T_Q4K || t == T_Q6K || t == T_Q8K) ? QK_K : 0;
+}
+__host__ __device__ inline int block_bytes(int t) {
+    return t == T_Q8_0 ? Q8_0_BYTES
+         : t == T_Q4K  ? Q4K_BYTES
+         : t == T_Q6K  ? Q6K_BYTES
+         : t == T_Q8K  ? Q8K_BYTES
+                       : 0;
+}
+
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
+
+// ------------------------------------------------------------ f16 bits --
+// f16 -> f32 is exact; f32 -> f16 is IEEE round-to-nearest-even, which is
+// what half::f16::from_f32 (F16C on x86) does.
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+// ------------------------------------------------- Rust cast semantics --
+// f32::round is half away from zero (llvm.round, not rint).
+__device__ __forceinline__ float round_away(float v) { return __builtin_roundf(v); }
+// `f32 as i32`: saturating, NaN -> 0.
+__device__ __forceinline__ int32_t sat_i32(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483647.0f) return 2147483647;
+    if (v <= -2147483648.0f) return (int32_t)(-2147483647 - 1);
+    return (int32_t)v;
+}
+// `f32 as i8`: saturating, NaN -> 0.
+__device__ __forceinline__ int32_t sat_i8(float v) {
+    if (v != v) return 0;
+    if (v >= 127.0f) return 127;
+    if (v <= -128.0f) return -128;
+    return (int32_t)v;
+}
+__device__ __forceinline__ int32_t nearest_int(float v) { return sat_i32(round_away(v)); }
+__device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// ------------------------------------------------------------- loads --
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t i) { return (w >> (8u * i)) & 0xffu; }
+
+// 16 bytes starting at a 2-byte-aligned address: five dword loads from the
+// 4-byte floor and a byte realignment (v_alignbyte_b32).  GGUF's 34- and
+// 210-byte blocks put every other block at an address = 2 (mod 4).
+__device__ __forceinline__ uint4 load16_a2(const uint8_t* p) {
+    uintptr_t a = (uintptr_t)p;
+    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+    uint32_t s = (uint32_t)(a & 3u);
+    uint4 v0 = *(const uint4*)q;  // 4-byte aligned dwordx4
+    uint32_t v4 = q[4];
+    uint4 r;
+    r.x = __builtin_amdgcn_alignbyte(v0.y, v0.x, s);
+    r.y = __builtin_amdgcn_alignbyte(v0.z, v0.y, s);
+    r.z = __builtin_amdgcn_alignbyte(v0.w, v0.z, s);
+    r.w = __builtin_amdgcn_alignbyte(v4, v0.w, s);
+    return r;
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Full-wave butterfly sum (wave64).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+#endif
+
+}  // namespace lloom

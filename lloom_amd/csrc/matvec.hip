@@ -1,0 +1,342 @@
+// matvec.hip -- decode-shaped quantized matmul (m <= 16 activation rows).
+//
+// y[m, n] = x[m, k] . W[n, k]^T with W packed Q8_0 / Q4_K / Q6_K, the CPU
+// arm's arithmetic (k_quants::matmul, k_quants.rs:2455-2641): x is quantized
+// to the VecDotType (Q8_0 or Q8_K, bit-exact), each dot is an exact integer
+// sum per block combined with f32 scales.
+//
+// MI355X layout of the work:
+//  * a 256-thread workgroup = 4 wave64s; each wave owns R consecutive weight
+//    rows, each lane one "task" (a 16-byte qs vector of a Q4_K superblock,
+//    a 64-element quarter of a Q6_K superblock, or a 34-byte Q8_0 block) per
+//    row, so a wave streams a row as one contiguous, coalesced sweep;
+//  * the weight loads of a K-chunk are issued first, then the workgroup
+//    quantizes the chunk of x into LDS (every block exactly as from_float),
+//    so the HBM latency of the weights hides under the quantization;
+//  * the dots are v_dot4_i32_i8 on 4 int8 lanes at a time; the Q4_K min term
+//    uses the Q8_K bsums, the Q6_K "-32" uses them too;
+//  * each lane accumulates f32 partials for its rows and activation rows,
+//    reduced across the wave at the end.
+// The float summation order differs from the CPU's (lane partials), which
+// is why parity is to a tolerance; every integer sum is exact.
+#include "kq_common.hpp"
+#include "kq_quant.hpp"
+#include "kernels.hpp"
+
+namespace lloom {
+
+constexpr int MV_WAVES = 4;
+constexpr int MV_THREADS = 64 * MV_WAVES;
+
+template <int TYPE>
+struct MvTraits;
+template <>
+struct MvTraits<T_Q4K> {
+    static constexpr int BE = 256, BB = Q4K_BYTES, P = 8, VT = T_Q8K;
+};
+template <>
+struct MvTraits<T_Q6K> {
+    static constexpr int BE = 256, BB = Q6K_BYTES, P = 4, VT = T_Q8K;
+};
+template <>
+struct MvTraits<T_Q8_0> {
+    static constexpr int BE = 32, BB = Q8_0_BYTES, P = 1, VT = T_Q8_0;
+};
+
+// Weight bytes a lane holds for one task.
+struct TaskData {
+    uint4 a, b, c, s;
+    uint32_t e;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void load_task(const uint8_t* __restrict__ row, int blk, int p, TaskData& t) {
+    if constexpr (TYPE == T_Q4K) {
+        const uint8_t* b = row + (size_t)blk * Q4K_BYTES;
+        t.s = *(const uint4*)b;                 // d, dmin, scales[12]
+        t.a = *(const uint4*)(b + 16 + 16 * p);  // qs[16p .. 16p+16)
+    } else if constexpr (TYPE == T_Q6K) {
+        const uint8_t* b = row + (size_t)blk * Q6K_BYTES;
+        int h = p >> 1, lq = (p & 1) * 16;
+        t.a = load16_a2(b + 64 * h + lq);
+        t.b = load16_a2(b + 64 * h + 32 + lq);
+        t.c = load16_a2(b + Q6K_QH + 32 * h + lq);
+        t.s = load16_a2(b + Q6K_SC);
+        t.e = *(const uint16_t*)(b + Q6K_D);
+    } else {
+        const uint8_t* b = row + (size_t)blk * Q8_0_BYTES;
+        uintptr_t a = (uintptr_t)b;
+        const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+        t.a = *(const uint4*)q;
+        t.b = *(const uint4*)(q + 4);
+        t.e = q[8];
+        t.c.x = (uint32_t)(a & 3u);  // 0 or 2
+    }
+}
+
+// Byte i (0..3) of the 4-dword group as a variable index.
+__device__ __forceinline__ uint32_t dw_sel(const uint4& v, uint32_t i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <int TYPE, int MB>
+__device__ __forceinline__ void compute_task(const TaskData& t, int p, int blk_local, int m, int KC,
+                                             const int8_t* __restrict__ lqs, const float* __restrict__ ld,
+                                             const int* __restrict__ lbs, int nbc, float* acc) {
+    if constexpr (TYPE == T_Q4K) {
+        const float d = f16_to_f32(t.s.x & 0xffffu);
+        const float dmin = f16_to_f32(t.s.x >> 16);
+        const int j = p >> 1, half = p & 1;
+        // get_scale_min_k4 (utils.rs:50-60) for sub-blocks 2j and 2j+1
+        int sc0, m0, sc1, m1;
+        if (j < 2) {
+            sc0 = byte_of(t.s.y, 2 * j) & 63;
+            m0 = byte_of(t.s.z, 2 * j) & 63;
+            sc1 = byte_of(t.s.y, 2 * j + 1) & 63;
+            m1 = byte_of(t.s.z, 2 * j + 1) & 63;
+        } else {
+            uint32_t i0 = 2 * j - 4, i1 = 2 * j - 3;
+            sc0 = (byte_of(t.s.w, i0) & 0xF) | ((byte_of(t.s.y, i0) >> 6) << 4);
+            m0 = (byte_of(t.s.w, i0) >> 4) | ((byte_of(t.s.z, i0) >> 6) << 4);
+            sc1 = (byte_of(t.s.w, i1) & 0xF) | ((byte_of(t.s.y, i1) >> 6) << 4);
+            m1 = (byte_of(t.s.w, i1) >> 4) | ((byte_of(t.s.z, i1) >> 6) << 4);
+        }
+        const uint32_t lo0 = t.a.x & 0x0F0F0F0Fu, lo1 = t.a.y & 0x0F0F0F0Fu, lo2 = t.a.z & 0x0F0F0F0Fu,
+                       lo3 = t.a.w & 0x0F0F0F0Fu;
+        const uint32_t hi0 = (t.a.x >> 4) & 0x0F0F0F0Fu, hi1 = (t.a.y >> 4) & 0x0F0F0F0Fu,
+                       hi2 = (t.a.z >> 4) & 0x0F0F0F0Fu, hi3 = (t.a.w >> 4) & 0x0F0F0F0Fu;
+        const int eoff = blk_local * 256 + 64 * j + 16 * half;
+#pragma unroll
+        for (int mi = 0; mi < MB; mi++) {
+            if (mi < m) {
+                const int8_t* xq = lqs + mi * KC + eoff;
+                uint4 xl = *(const uint4*)xq;
+                uint4 xh = *(const uint4*)(xq + 32);
+                int sl = dot4(lo0, xl.x, 0);
+                sl = dot4(lo1, xl.y, sl);
+                sl = dot4(lo2, xl.z, sl);
+                sl = dot4(lo3, xl.w, sl);
+                int sh = dot4(hi0, xh.x, 0);
+                sh = dot4(hi1, xh.y, sh);
+                sh = dot4(hi2, xh.z, sh);
+                sh = dot4(hi3, xh.w, sh);
+                const int* bs = lbs + (mi * nbc + blk_local) * 16 + 4 * j + half;
+                int S = sc0 * sl + sc1 * sh;
+                int Mn = m0 * bs[0] + m1 * bs[2];
+                float dy = ld[mi * nbc + blk_local];
+                acc[mi] += dy * ((float)S * d - (float)Mn * dmin);
+            }
+        }
+    } else if constexpr (TYPE == T_Q6K) {
+        const float d = f16_to_f32(t.e);
+        const int h = p >> 1, odd = p & 1;
+        // q6 bytes of the 4 groups g (elements 128h + 32g + 16*odd + 0..15)
+        uint32_t q[4][4];
+        const uint32_t A[4] = {t.a.x, t.a.y, t.a.z, t.a.w};
+        const uint32_t B[4] = {t.b.x, t.b.y, t.b.z, t.b.w};
+        const uint32_t C[4] = {t.c.x, t.c.y, t.c.z, t.c.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            q[0][i] = (A[i] & 0x0F0F0F0Fu) | ((C[i] & 0x03030303u) << 4);
+            q[1][i] = (B[i] & 0x0F0F0F0Fu) | (((C[i] >> 2) & 0x03030303u) << 4);
+            q[2][i] = ((A[i] >> 4) & 0x0F0F0F0Fu) | (((C[i] >> 4) & 0x03030303u) << 4);
+            q[3][i] = ((B[i] >> 4) & 0x0F0F0F0Fu) | (((C[i] >> 6) & 0x03030303u) << 4);
+        }
+        // scales[8h + 2g + odd]: dword 2h (g < 2) or 2h + 1, byte (2g + odd) & 3
+        int sc[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t w = dw_sel(t.s, 2 * h + (g >> 1));
+            sc[g] = (int)(int8_t)byte_of(w, (2 * g + odd) & 3);
+        }
+#pragma unroll
+        for (int mi = 0; mi < MB; mi++) {
+            if (mi < m) {
+                int tot = 0;
+                const int8_t* xb = lqs + mi * KC + blk_local * 256 + 128 * h + 16 * odd;
+                const int* bs = lbs + (mi * nbc + blk_local) * 16 + 8 * h + odd;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    uint4 xv = *(const uint4*)(xb + 32 * g);
+                    int s = dot4(q[g][0], xv.x, 0);
+                    s = dot4(q[g][1], xv.y, s);
+                    s = dot4(q[g][2], xv.z, s);
+                    s = dot4(q[g][3], xv.w, s);
+                    tot += sc[g] * (s - 32 * bs[2 * g]);
+                }
+                float dy = ld[mi * nbc + blk_local];
+                acc[mi] += (d * dy) * (float)tot;
+            }
+        }
+    } else {
+        const uint32_t s = t.c.x;
+        const float dx = f16_to_f32(s == 0 ? (t.a.x & 0xffffu) : (t.a.x >> 16));
+        const uint32_t W[9] = {t.a.x, t.a.y, t.a.z, t.a.w, t.b.x, t.b.y, t.b.z, t.b.w, t.e};
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = s == 0 ? __builtin_amdgcn_alignbyte(W[i + 1], W[i], 2) : W[i + 1];
+#pragma unroll
+        for (int mi = 0; mi < MB; mi++) {
+            if (mi < m) {
+                const int8_t* xb = lqs + mi * KC + blk_local * 32;
+                uint4 x0 = *(const uint4*)xb;
+                uint4 x1 = *(const uint4*)(xb + 16);
+                int sum = dot4(w[0], x0.x, 0);
+                sum = dot4(w[1], x0.y, sum);
+                sum = dot4(w[2], x0.z, sum);
+                sum = dot4(w[3], x0.w, sum);
+                sum = dot4(w[4], x1.x, sum);
+                sum = dot4(w[5], x1.y, sum);
+                sum = dot4(w[6], x1.z, sum);
+                sum = dot4(w[7], x1.w, sum);
+                acc[mi] += (float)sum * (dx * ld[mi * nbc + blk_local]);
+            }
+        }
+    }
+}
+
+// Quantize x[:, kc0 : kc0 + KC] into LDS (qs, per-block d, Q8_K bsums).
+template <int VT>
+__device__ __forceinline__ void fill_lds(const float* __restrict__ x, int64_t K, int kc0, int KC, int m,
+                                         int8_t* lqs, float* ld, int* lbs) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if constexpr (VT == T_Q8K) {
+        const int nbc = KC / 256;
+        for (int b = wave; b < m * nbc; b += MV_WAVES) {
+            int mi = b / nbc, sb = b - mi * nbc;
+            float4 v = *(const float4*)(x + mi * K + kc0 + sb * 256 + 4 * lane);
+            float d;
+            int bs;
+            uint32_t q = q8k_block_wave(v, lane, &d, &bs);
+            *(uint32_t*)(lqs + mi * KC + sb * 256 + 4 * lane) = q;
+            if ((lane & 3) == 0) lbs[b * 16 + (lane >> 2)] = bs;
+            if (lane == 0) ld[b] = d;
+        }
+    } else {
+        const int nbc = KC / 32;
+        const int total = m * nbc;
+        for (int b0 = wave * 8; b0 < total; b0 += 8 * MV_WAVES) {
+            int b = b0 + (lane >> 3), sub = lane & 7;
+            bool ok = b < total;
+            int mi = ok ? b / nbc : 0, bl = ok ? b - mi * nbc : 0;
+            float4 v = ok ? *(const float4*)(x + mi * K + kc0 + bl * 32 + 4 * sub) : make_float4(0, 0, 0, 0);
+            uint16_t d16;
+            uint32_t q = q8_0_block_8lanes(v, &d16);
+            if (ok) {
+                *(uint32_t*)(lqs + mi * KC + bl * 32 + 4 * sub) = q;
+                if (sub == 0) ld[b] = f16_to_f32(d16);
+            }
+        }
+    }
+}
+
+template <int TYPE, int MB, int R>
+__global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                        float* __restrict__ Y, int n, int K, int m, int KC) {
+    using Tr = MvTraits<TYPE>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * MV_WAVES + wave) * R;
+    const int64_t rowbytes = (int64_t)(K / Tr::BE) * Tr::BB;
+    const int nbc = KC / Tr::BE;
+    int8_t* lqs = (int8_t*)smem;
+    float* ld = (float*)(smem + m * KC);
+    int* lbs = (int*)(ld + m * nbc);
+
+    float acc[R][MB];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int mi = 0; mi < MB; mi++) acc[r][mi] = 0.0f;
+
+    const int T = nbc * Tr::P;  // tasks per row per chunk
+    for (int kc0 = 0; kc0 < K; kc0 += KC) {
+        const int blk0 = kc0 / Tr::BE;
+        // first round of weight loads before the activation prologue
+        TaskData td[R];
+        int ti = lane;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int row = row0 + r;
+            if (ti < T && row < n) load_task<TYPE>(W + row * rowbytes, blk0 + ti / Tr::P, ti % Tr::P, td[r]);
+        }
+        __syncthreads();
+        fill_lds<Tr::VT>(X, K, kc0, KC, m, lqs, ld, lbs);
+        __syncthreads();
+        for (; ti < T; ti += 64) {
+            if (ti != lane) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    int row = row0 + r;
+                    if (row < n) load_task<TYPE>(W + row * rowbytes, blk0 + ti / Tr::P, ti % Tr::P, td[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (row0 + r < n)
+                    compute_task<TYPE, MB>(td[r], ti % Tr::P, ti / Tr::P, m, KC, lqs, ld, lbs, nbc, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int row = row0 + r;
+#pragma unroll
+        for (int mi = 0; mi < MB; mi++) {
+            if (mi < m) {
+                float v = wave_sum(acc[r][mi]);
+                if (lane == 0 && row < n) Y[(int64_t)mi * n + row] = v;
+            }
+        }
+    }
+}
+
+// Chunk of K staged in LDS at a time: all of K when it fits the budget.
+static int pick_kc(int type, int64_t K, int m) {
+    const int be = type == T_Q8_0 ? 32 : 256;
+    const int64_t budget = 32768;  // bytes of int8 activations per chunk
+    int64_t kc = budget / m;
+    kc -= kc % 256;
+    if (kc < be) kc = be;
+    if (kc >= K) return (int)K;
+    while (K % kc) kc -= be;  // chunks tile K exactly
+    return (int)kc;
+}
+
+static size_t lds_bytes(int type, int KC, int m) {
+    const int be = type == T_Q8_0 ? 32 : 256;
+    size_t b = (size_t)m * KC + (size_t)m * (KC / be) * 4;
+    if (type != T_Q8_0) b += (size_t)m * (KC / 16) * 4;
+    return b;
+}
+
+template <int TYPE, int MB>
+static hipError_t launch_mb(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
+    constexpr int R = 2;
+    int KC = pick_kc(TYPE, K, m);
+    size_t shm = lds_bytes(TYPE, KC, m);
+    dim3 grid((n + MV_WAVES * R - 1) / (MV_WAVES * R));
+    hipLaunchKernelGGL((k_matvec<TYPE, MB, R>), grid, dim3(MV_THREADS), shm, s, (const uint8_t*)w, x, y, n, K, m,
+                       KC);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+static hipError_t launch_type(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
+    if (m <= 1) return launch_mb<TYPE, 1>(w, x, y, n, K, m, s);
+    if (m <= 2) return launch_mb<TYPE, 2>(w, x, y, n, K, m, s);
+    if (m <= 4) return launch_mb<TYPE, 4>(w, x, y, n, K, m, s);
+    if (m <= 8) return launch_mb<TYPE, 8>(w, x, y, n, K, m, s);
+    return launch_mb<TYPE, 16>(w, x, y, n, K, m, s);
+}
+
+hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
+                         hipStream_t s) {
+    switch (type) {
+        case T_Q4K: return launch_type<T_Q4K>(w, x, y, (int)n, (int)k, (int)m, s);
+        case T_Q6K: return launch_type<T_Q6K>(w, x, y, (int)n, (int)k, (int)m, s);
+        case T_Q8_0: return launch_type<T_Q8_0>(w, x, y, (int)n, (int)k, (int)m, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace lloom

@@ -1,0 +1,256 @@
+"""Host mirror of lloom-tensor's quantized surface on the HIP arm.
+
+Names, argument meaning and refusals follow lloom-tensor/src/quantized/mod.rs:
+  GgmlDType            mod.rs:404-437, ids mod.rs:505-568
+  QTensor.quantize     mod.rs:919-938   (QStorage::quantize on the device)
+  QTensor.from_data    mod.rs:136-223   (QStorage::from_data: an upload)
+  QTensor.dequantize   mod.rs:1065-1086 (and dequantize_f16)
+  QTensor.indexed_moe_forward{,_with,_as}  mod.rs:1560-1645
+  QMatMul.from_qtensor / forward          mod.rs:1698-1729, 2022-2025
+  MoeArm               mod.rs:2290-2310
+Tensors are torch tensors on the GPU (device memory and streams only); the
+arithmetic is the C ABI's.
+"""
+import ctypes
+import enum
+import threading
+
+import numpy as np
+import torch
+
+from .lib import LloomHipError, check, lib
+
+
+class GgmlDType(enum.IntEnum):
+    F32 = 0
+    F16 = 1
+    Q8_0 = 8
+    Q4K = 12
+    Q6K = 14
+    Q8K = 15
+
+    def block_size(self):
+        return {GgmlDType.F32: 1, GgmlDType.F16: 1, GgmlDType.Q8_0: 32}.get(self, 256)
+
+    def type_size(self):
+        return {GgmlDType.F32: 4, GgmlDType.F16: 2, GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144,
+                GgmlDType.Q6K: 210, GgmlDType.Q8K: 292}[self]
+
+    def vec_dot_type(self):
+        return GgmlDType.Q8_0 if self == GgmlDType.Q8_0 else GgmlDType.Q8K
+
+
+class MoeArm(enum.Enum):
+    """The kernel family of a routed matmul (mod.rs:2290-2310).  The HIP arm
+    has one kernel (f32 dots, as the CPU arm) and, like the CPU and CUDA
+    arms, ignores it; it is kept so callers pass it unchanged."""
+    MatVec = 0
+    Gemm = 1
+
+    @staticmethod
+    def for_rows(rows, mm_from=64):
+        return MoeArm.Gemm if mm_from > 0 and rows >= mm_from else MoeArm.MatVec
+
+
+# ------------------------------------------------------------- context --
+
+_ctx_lock = threading.Lock()
+_ctxs = {}
+
+
+def _ctx(device_index):
+    with _ctx_lock:
+        c = _ctxs.get(device_index)
+        if c is None:
+            p = ctypes.c_void_p()
+            check(lib().lloom_hip_ctx_create(device_index, ctypes.byref(p)))
+            c = p.value
+            _ctxs[device_index] = c
+        return c
+
+
+def _dev_index(t):
+    if not t.is_cuda:
+        raise LloomHipError(1, "tensor is not on a HIP device")
+    return t.device.index if t.device.index is not None else torch.cuda.current_device()
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def set_mv_rows_max(rows, device=0):
+    check(lib().lloom_hip_ctx_set_mv_rows_max(_ctx(device), rows))
+
+
+# ------------------------------------------------------------ QTensor ---
+
+def _padded_bytes(dtype, n_rows, k):
+    packed, alloc = ctypes.c_size_t(), ctypes.c_size_t()
+    check(lib().lloom_hip_weight_bytes(int(dtype), n_rows, k, ctypes.byref(packed), ctypes.byref(alloc)))
+    return packed.value, alloc.value
+
+
+class QTensor:
+    """Packed GGUF blocks in device memory with a logical shape whose last
+    dimension is k (a multiple of the block size)."""
+
+    def __init__(self, storage, shape, dtype):
+        self.storage = storage  # torch.uint8 on the GPU, with the tail pad
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = GgmlDType(dtype)
+
+    # QTensor::quantize (mod.rs:919-938); check_shape (mod.rs:900-907)
+    @staticmethod
+    def quantize(src, dtype):
+        dtype = GgmlDType(dtype)
+        if dtype in (GgmlDType.F32, GgmlDType.F16):
+            raise LloomHipError(2, f"{dtype.name} is not a block type on the HIP quantized path")
+        shape = tuple(src.shape)
+        bs = dtype.block_size()
+        if len(shape) == 0 or shape[-1] % bs:
+            raise LloomHipError(3, f"quantized tensor must have their last dim divisible by block size {shape} {bs}")
+        src = src.to(torch.float32).contiguous()
+        elems = src.numel()
+        packed, alloc = _padded_bytes(dtype, elems // shape[-1], shape[-1])
+        storage = torch.zeros(alloc, dtype=torch.uint8, device=src.device)
+        check(lib().lloom_hip_quantize(_ctx(_dev_index(src)), int(dtype), _ptr(src), elems, _ptr(storage),
+                                       _stream(src)))
+        return QTensor(storage, shape, dtype)
+
+    # QStorage::from_data (mod.rs:136-223): raw GGUF bytes, uploaded as is
+    @staticmethod
+    def from_data(data, shape, dtype, device="cuda"):
+        dtype = GgmlDType(dtype)
+        shape = tuple(shape)
+        buf = np.frombuffer(bytes(data) if not isinstance(data, np.ndarray) else data.tobytes(), dtype=np.uint8)
+        packed, alloc = _padded_bytes(dtype, int(np.prod(shape[:-1])), shape[-1])
+        if buf.size != packed:
+            raise LloomHipError(3, f"{buf.size} bytes do not hold a {dtype.name} tensor of shape {shape} ({packed} bytes)")
+        storage = torch.zeros(alloc, dtype=torch.uint8, device=device)
+        storage[:packed].copy_(torch.from_numpy(buf.copy()))
+        return QTensor(storage, shape, dtype)
+
+    def packed_bytes(self):
+        return _padded_bytes(self.dtype, int(np.prod(self.shape[:-1])), self.shape[-1])[0]
+
+    def data(self):
+        """The packed GGUF bytes (numpy uint8)."""
+        return self.storage[:self.packed_bytes()].cpu().numpy()
+
+    def elem_count(self):
+        return int(np.prod(self.shape))
+
+    def _dequant(self, out_dtype, torch_dtype):
+        y = torch.empty(self.shape, dtype=torch_dtype, device=self.storage.device)
+        check(lib().lloom_hip_dequantize(_ctx(_dev_index(self.storage)), int(self.dtype), _ptr(self.storage),
+                                         self.elem_count(), _ptr(y), out_dtype, _stream(self.storage)))
+        return y
+
+    def dequantize(self):
+        return self._dequant(0, torch.float32)
+
+    def dequantize_f16(self):
+        return self._dequant(1, torch.float16)
+
+    # indexed_moe_forward{,_with,_as} (mod.rs:1560-1645); the arm is ignored
+    def indexed_moe_forward(self, x, ids, arm=None, strict=True):
+        if len(self.shape) != 3:
+            raise LloomHipError(3, f"indexed_moe_forward: weight {self.shape} is not [experts, n, k]")
+        n_experts, n, k = self.shape
+        if x.dim() != 3 or ids.dim() != 2:
+            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
+        batch, in_dim1, k_in = x.shape
+        batch_ids, topk = ids.shape
+        if k_in != k or batch != batch_ids or (in_dim1 != 1 and in_dim1 != topk):
+            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
+        x = x.to(torch.float32).contiguous()
+        ids = ids.to(torch.int32).contiguous()
+        y = torch.empty((batch, topk, n), dtype=torch.float32, device=x.device)
+        check(lib().lloom_hip_moe_matmul(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage), n_experts, n,
+                                         k, _ptr(x), batch, in_dim1, _ptr(ids), topk, _ptr(y), 1 if strict else 0,
+                                         _stream(x)))
+        return y
+
+    indexed_moe_forward_with = indexed_moe_forward
+
+    def indexed_moe_forward_pair(self, up, x, ids, arm=None):
+        """Gate and up of one routed layer: two calls (mod.rs:1472-1475 off Metal)."""
+        return self.indexed_moe_forward(x, ids, arm), up.indexed_moe_forward(x, ids, arm)
+
+    def __repr__(self):
+        return f"QTensor[{list(self.shape)}; {self.dtype.name}]"
+
+
+# ------------------------------------------------------------ QMatMul ---
+
+class QMatMul:
+    """QMatMul::QTensor (mod.rs:1698-1729): forward(x) = x . W^T with W
+    packed.  x is [.., k] f32 (rank >= 2, contiguous); the result is [.., n]."""
+
+    def __init__(self, qtensor):
+        if len(qtensor.shape) != 2:
+            raise LloomHipError(3, f"QMatMul weight must be [n, k], got {qtensor.shape}")
+        self.qtensor = qtensor
+
+    @staticmethod
+    def from_qtensor(qtensor):
+        return QMatMul(qtensor)
+
+    def forward(self, xs):
+        n, k = self.qtensor.shape
+        if xs.dim() < 2:
+            raise LloomHipError(3, f"input tensor has only one dimension {tuple(xs.shape)}")
+        if xs.shape[-1] != k:
+            raise LloomHipError(3, f"input tensor {tuple(xs.shape)} incompatible with {self.qtensor.shape}")
+        if xs.dtype != torch.float32:
+            raise LloomHipError(2, f"Expected f32 activations, got {xs.dtype}")
+        if not xs.is_contiguous():
+            raise LloomHipError(1, f"input tensor is not contiguous {tuple(xs.shape)}")
+        m = xs.numel() // k
+        y = torch.empty(tuple(xs.shape[:-1]) + (n,), dtype=torch.float32, device=xs.device)
+        check(lib().lloom_hip_qmatmul(_ctx(_dev_index(xs)), int(self.qtensor.dtype), _ptr(self.qtensor.storage), n,
+                                      k, _ptr(xs), 0, m, _ptr(y), 0, _stream(xs)))
+        return y
+
+    __call__ = forward
+
+
+# ---------------------------------------------------------- functions ---
+
+def quantize_act(x, vec_dot_dtype):
+    """[m, k] f32 -> packed Q8_0 / Q8K blocks (uint8), as k_quants::matmul
+    quantizes its lhs (k_quants.rs:2477-2508)."""
+    vec_dot_dtype = GgmlDType(vec_dot_dtype)
+    x = x.contiguous()
+    m, k = x.shape
+    bs = vec_dot_dtype.block_size()
+    nbytes = m * (k // bs) * vec_dot_dtype.type_size() if k % bs == 0 else 0
+    out = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    check(lib().lloom_hip_quantize_act(_ctx(_dev_index(x)), int(vec_dot_dtype), _ptr(x), m, k, _ptr(out),
+                                       _stream(x)))
+    return out[:nbytes]
+
+
+def dequantize(blocks, dtype, elems, out_f16=False):
+    y = torch.empty(elems, dtype=torch.float16 if out_f16 else torch.float32, device=blocks.device)
+    check(lib().lloom_hip_dequantize(_ctx(_dev_index(blocks)), int(GgmlDType(dtype)), _ptr(blocks), elems, _ptr(y),
+                                     1 if out_f16 else 0, _stream(blocks)))
+    return y
+
+
+def synth_normal(seed, count, mean=0.0, std=1.0):
+    """Deterministic N(mean, std) f32 (SplitMix64 -> xoshiro256**, Box-Muller)."""
+    out = np.empty(count, dtype=np.float32)
+    check(lib().lloom_hip_synth_normal(seed, mean, std, out.ctypes.data_as(ctypes.c_void_p), count))
+    return out
+
+
+def synth_uniform(seed, count, lo=0.0, hi=1.0):
+    out = np.empty(count, dtype=np.float32)
+    check(lib().lloom_hip_synth_uniform(seed, lo, hi, out.ctypes.data_as(ctypes.c_void_p), count))
+    return out

@@ -1,0 +1,294 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle.
+
+Bars: quantizers and dequantizers bit-exact; matmul max|d| <= 1e-3 * max|y row|
+(the tolerance BASELINE.json's north_star states); routed experts also mean
+relative error < 1e-4 against a dense f32 reference
+(lloom-tensor/tests/moe_routed_metal.rs:148-154, 244-327).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MATMUL_TOL = 1e-3  # max|got - want| <= MATMUL_TOL * max|want row|
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import lloom_amd
+
+    lloom_amd.lib()
+    return lloom_amd
+
+
+DEV = "cuda:0"
+
+
+def _cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def assert_rows_close(got, want, tol=MATMUL_TOL, what=""):
+    got = np.asarray(got, dtype=np.float64).reshape(-1, want.shape[-1])
+    want = np.asarray(want, dtype=np.float64).reshape(-1, want.shape[-1])
+    bound = tol * np.abs(want).max(axis=1, keepdims=True) + 1e-30
+    err = np.abs(got - want)
+    bad = err > bound
+    assert not bad.any(), f"{what}: {bad.sum()} outputs out of tolerance, worst ratio {(err / bound).max():.3g}"
+
+
+def ggml_like(n, offset=0.0):
+    i = np.arange(n, dtype=np.float32)
+    return (np.float32(0.1) + np.float32(2.0) * np.cos(i + np.float32(offset))).astype(np.float32)
+
+
+def edge_inputs(k, rows=4, seed=0):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[0, :256] = 0.0  # an all-zero block
+    x[1, :32] = 7.25  # constant block
+    x[1, 40] = -3.0   # tie on |x| with a later +3.0
+    x[1, 41] = 3.0
+    x[2] *= np.float32(1e-38)  # subnormal range
+    x[3, ::7] *= 1000.0  # outliers
+    return x
+
+
+# ------------------------------------------------------------ quantize ---
+
+@pytest.mark.parametrize("vt", [O.Q8_0, O.Q8K])
+def test_quantize_act_bit_exact(L, vt):
+    for x in [edge_inputs(1024), L.synth_normal(5, 9 * 2048).reshape(9, 2048)]:
+        got = L.quantize_act(_cuda(x), vt).cpu().numpy()
+        want = np.concatenate([O.quantize(vt, r) for r in x])
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+def test_weight_quantize_bit_exact(L, dt):
+    cases = [
+        L.synth_normal(7, 64 * 2048, 0.0, 0.02).reshape(64, 2048),
+        ggml_like(4096).reshape(2, 2048),
+        (np.arange(1024, dtype=np.float32) - 512.0).reshape(1, 1024) * np.float32(0.5 / 512),
+        edge_inputs(1024, seed=1),
+        np.zeros((1, 512), np.float32),
+        np.full((1, 256), 0.375, np.float32),
+    ]
+    for w in cases:
+        qt = L.QTensor.quantize(_cuda(w), dt)
+        got = qt.data()
+        want = O.quantize(dt, w.ravel())
+        assert np.array_equal(got, want), f"{dt}: {np.sum(got != want)} bytes differ for shape {w.shape}"
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K, O.Q8K])
+def test_dequantize_bit_exact(L, dt):
+    w = L.synth_normal(9, 16 * 1024, 0.0, 0.5).astype(np.float32)
+    q = O.quantize(dt, w)
+    blocks = _cuda(np.concatenate([q, np.zeros(512, np.uint8)]))
+    got = L.dequantize(blocks, dt, w.size).cpu().numpy()
+    want = O.dequantize(dt, q, w.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    got16 = L.dequantize(blocks, dt, w.size, out_f16=True).cpu().numpy()
+    assert np.array_equal(got16.view(np.uint16), O.dequantize_f16(dt, q, w.size).view(np.uint16))
+
+
+def test_qtensor_dequantize_f16_is_rne_of_f32(L):
+    """dequantize_f16 == f16(dequantize) exactly (quantized_tests.rs:867-873)."""
+    w = _cuda(ggml_like(4096).reshape(16, 256))
+    for dt in (L.GgmlDType.Q4K, L.GgmlDType.Q6K, L.GgmlDType.Q8_0):
+        qt = L.QTensor.quantize(w, dt)
+        a = qt.dequantize().half().cpu().numpy().view(np.uint16)
+        b = qt.dequantize_f16().cpu().numpy().view(np.uint16)
+        assert np.array_equal(a, b)
+
+
+# -------------------------------------------------------------- matmul ---
+
+def _qmm(L, dt, w, x):
+    qt = L.QTensor.quantize(_cuda(w), dt)
+    y = L.QMatMul.from_qtensor(qt).forward(_cuda(x)).cpu().numpy()
+    return y, qt.data()
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 8, 13, 16, 17, 33])
+def test_qmatmul_matches_oracle(L, dt, m):
+    rng = np.random.default_rng(100 + m)
+    for n, k in [(1, 256), (7, 768), (65, 2048), (130, 512)]:
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y, q = _qmm(L, dt, w, x)
+        assert_rows_close(y, O.matmul(dt, x, q, n), what=f"dt={dt} m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+def test_qmatmul_closed_form_inputs(L, dt):
+    """The reference's closed-form GEMM inputs (quantized_tests.rs:1769-1903)."""
+    for m in [2, 17, 33]:
+        for n in [1, 2, 3, 4, 7, 65]:
+            for k in [256, 768]:
+                lhs = (((np.arange(m * k) * 17 % 211).astype(np.float32) - 103) / 73).astype(np.float32).reshape(m, k)
+                wts = (((np.arange(n * k) * 31 % 173).astype(np.float32) - 87) / 61).astype(np.float32).reshape(n, k)
+                y, q = _qmm(L, dt, wts, lhs)
+                assert_rows_close(y, O.matmul(dt, lhs, q, n), what=f"closed form dt={dt} {m},{n},{k}")
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+def test_decode_rows_batch_invariant(L, dt):
+    """Within the decode route every activation row is computed alone, so a
+    row's output does not depend on its batch (qmm_batch,
+    quantized_tests.rs:239-275, exact on the CPU arm)."""
+    rng = np.random.default_rng(3)
+    n, k = 96, 1024
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((16, k)).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), dt)
+    mm = L.QMatMul.from_qtensor(qt)
+    full = mm.forward(_cuda(x)).cpu().numpy()
+    for m in (1, 2, 5, 8):
+        part = mm.forward(_cuda(x[:m])).cpu().numpy()
+        assert np.array_equal(part.view(np.uint32), full[:m].view(np.uint32))
+
+
+def test_qmatmul_rank3_input(L):
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((40, 512)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((2, 3, 512)).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), L.GgmlDType.Q4K)
+    y = L.QMatMul.from_qtensor(qt).forward(_cuda(x)).cpu().numpy()
+    assert y.shape == (2, 3, 40)
+    assert_rows_close(y.reshape(6, 40), O.matmul(O.Q4K, x.reshape(6, 512), qt.data(), 40))
+
+
+# BASELINE.json configs at their full shapes (the decode ones whole, the
+# prefill one on a column subset the oracle finishes quickly).
+def test_baseline_c1_q8_0_decode(L):
+    w = L.synth_normal(0, 8192 * 2048, 0.0, 0.02).reshape(8192, 2048)
+    x = L.synth_normal(1000, 2048).reshape(1, 2048)
+    y, q = _qmm(L, O.Q8_0, w, x)
+    assert_rows_close(y, O.matmul(O.Q8_0, x, q, 8192), what="C1")
+
+
+@pytest.mark.parametrize("b", [1, 2, 4, 8, 16])
+def test_baseline_c2_q4k_decode_sweep(L, b):
+    w = L.synth_normal(1, 6144 * 2048, 0.0, 0.02).reshape(6144, 2048)
+    x = L.synth_normal(1001 + b, b * 2048).reshape(b, 2048)
+    y, q = _qmm(L, O.Q4K, w, x)
+    assert_rows_close(y, O.matmul(O.Q4K, x, q, 6144), what=f"C2 b={b}")
+
+
+@pytest.mark.parametrize("m", [64, 512])
+def test_baseline_c3_q4k_prefill_subset(L, m):
+    n, k = 8192, 2048
+    w = L.synth_normal(2, n * k, 0.0, 0.02).reshape(n, k)
+    x = L.synth_normal(2002 + m, m * k).reshape(m, k)
+    y, q = _qmm(L, O.Q4K, w, x)
+    cols = np.arange(0, n, 61)
+    rowbytes = (k // 256) * 144
+    qsub = np.concatenate([q[c * rowbytes:(c + 1) * rowbytes] for c in cols])
+    rows = np.arange(0, m, 7) if m > 64 else np.arange(m)
+    want = O.matmul(O.Q4K, x[rows], qsub, len(cols))
+    assert_rows_close(y[np.ix_(rows, cols)], want, what=f"C3 m={m}")
+
+
+def test_baseline_c4_q6k_down_proj(L):
+    w = L.synth_normal(3, 2048 * 8192, 0.0, 0.02).reshape(2048, 8192)
+    x = L.synth_normal(3003, 4 * 8192).reshape(4, 8192)
+    y, q = _qmm(L, O.Q6K, w, x)
+    assert_rows_close(y, O.matmul(O.Q6K, x, q, 2048), what="C4 down")
+
+
+# -------------------------------------------------------- routed experts ---
+
+def _moe_case(L, dt, n_experts, n, k, batch, topk, in_dim1, seed, ids=None):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n_experts, n, k)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((batch, in_dim1, k)).astype(np.float32)
+    if ids is None:
+        ids = rng.integers(0, n_experts, (batch, topk)).astype(np.uint32)
+        ids[0, :] = ids[0, 0]  # the same expert in several slots
+        if batch > 1:
+            ids[1, 0] = ids[0, 0]  # and across the batch
+    qt = L.QTensor.quantize(_cuda(w), dt)
+    got = qt.indexed_moe_forward(_cuda(x), _cuda(ids.astype(np.int32))).cpu().numpy()
+    q = qt.data()
+    want = O.matmul_indexed(dt, q, n_experts, n, k, x, ids)
+    dense = O.dequantize(dt, q, w.size).reshape(n_experts, n, k).astype(np.float64)
+    ref = np.empty((batch, topk, n))
+    for b in range(batch):
+        for t in range(topk):
+            ref[b, t] = dense[ids[b, t]] @ x[b, 0 if in_dim1 == 1 else t].astype(np.float64)
+    return got, want, ref
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+@pytest.mark.parametrize("in_dim1_is_topk", [False, True])
+@pytest.mark.parametrize("n", [40, 37])
+def test_moe_matches_oracle_and_dense(L, dt, in_dim1_is_topk, n):
+    topk = 4
+    got, want, ref = _moe_case(L, dt, 8, n, 512, 5, topk, topk if in_dim1_is_topk else 1, seed=n)
+    assert_rows_close(got, want, what="moe vs oracle")
+    rel = np.mean(np.abs(ref - got) / (np.abs(ref) + 1e-4))
+    assert rel < 1e-4, rel
+
+
+def test_moe_short_rows_and_many_experts(L):
+    """k = 768 (the down projection's), 64 experts top-10."""
+    got, want, ref = _moe_case(L, O.Q4K, 64, 48, 768, 6, 10, 10, seed=9)
+    assert_rows_close(got, want, what="moe k=768")
+
+
+def test_moe_run_to_run_identical(L):
+    a, _, _ = _moe_case(L, O.Q4K, 16, 64, 1024, 8, 4, 1, seed=5)
+    b, _, _ = _moe_case(L, O.Q4K, 16, 64, 1024, 8, 4, 1, seed=5)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_moe_out_of_range_expert_is_refused(L):
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((4, 8, 256)) * 0.05).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), L.GgmlDType.Q4K)
+    x = _cuda(rng.standard_normal((2, 1, 256)).astype(np.float32))
+    bad = _cuda(np.array([[0, 4], [1, 2]], dtype=np.int32))
+    with pytest.raises(L.LloomHipError) as e:
+        qt.indexed_moe_forward(x, bad)
+    assert e.value.name == "EEXPERT"
+    # deferred: the call returns, the next sync reports, then it is cleared
+    y = qt.indexed_moe_forward(x, bad, strict=False)
+    assert np.all(y[0, 1].cpu().numpy() == 0)
+    from lloom_amd.quantized import _ctx
+    from lloom_amd.lib import lib
+
+    assert lib().lloom_hip_ctx_sync(_ctx(0)) == 4
+    assert lib().lloom_hip_ctx_sync(_ctx(0)) == 0
+    good = qt.indexed_moe_forward(x, _cuda(np.array([[0, 3], [1, 2]], dtype=np.int32)))
+    assert np.isfinite(good.cpu().numpy()).all()
+
+
+# ------------------------------------------------------------- refusals ---
+
+def test_refusals_are_named(L):
+    w = _cuda(np.zeros((4, 256), np.float32))
+    with pytest.raises(L.LloomHipError) as e:
+        L.QTensor.quantize(_cuda(np.zeros((4, 100), np.float32)), L.GgmlDType.Q4K)
+    assert e.value.name == "ESHAPE"
+    qt = L.QTensor.quantize(w, L.GgmlDType.Q4K)
+    with pytest.raises(L.LloomHipError) as e:
+        L.QMatMul.from_qtensor(qt).forward(_cuda(np.zeros((2, 512), np.float32)))
+    assert e.value.name == "ESHAPE"
+    with pytest.raises(L.LloomHipError) as e:
+        L.QMatMul.from_qtensor(qt).forward(_cuda(np.zeros((2, 256), np.float16)))
+    assert e.value.name == "EDTYPE"
+    from lloom_amd.quantized import _ctx, _ptr, _stream
+    from lloom_amd.lib import lib
+
+    x = _cuda(np.zeros((1, 256), np.float32))
+    y = torch.empty((1, 4), device=DEV)
+    rc = lib().lloom_hip_qmatmul(_ctx(0), 15, _ptr(qt.storage), 4, 256, _ptr(x), 0, 1, _ptr(y), 0, _stream(x))
+    assert rc == 2 and b"Q8K" in lib().lloom_hip_last_error()
