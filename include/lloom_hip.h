@@ -4,8 +4,9 @@
  * This is the drop-in boundary a `QStorage::Hip` arm of lloom-tensor binds
  * through a thin `lloom-hip-sys` crate (extern "C" declarations of exactly
  * these functions).  Plain pointers and sizes only: every buffer argument
- * named `*_dev` is device memory owned by the caller; `stream` is a
- * hipStream_t (NULL = the context's own stream).
+ * named `*_dev` is device memory owned by the caller; `stream` is the
+ * hipStream_t every launch of the call is queued on, used as given (NULL is
+ * HIP's null stream; lloom_hip_ctx_stream() returns the context's own).
  *
  * Type ids are GGUF's (GgmlDType::to_u32, lloom-tensor/src/quantized/mod.rs
  * :539-568): F32 = 0, F16 = 1, Q8_0 = 8, Q4K = 12, Q6K = 14, Q8K = 15.
@@ -72,8 +73,8 @@ void* lloom_hip_ctx_stream(lloom_hip_ctx* ctx);
  * more rows the MFMA GEMM (default 16, range 1..16).  The reference's knobs
  * are MMVQ_MAX_BATCH (fast_mmvq.rs:38) and qmv.mm_from (tuning.rs:1413). */
 int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows);
-/* Wait for the context stream; report a device-side error (an out-of-range
- * expert id seen by a routed matmul) recorded since the last check. */
+/* Wait for the device; report a device-side error (an out-of-range expert
+ * id seen by a routed matmul) recorded since the last check, and clear it. */
 int lloom_hip_ctx_sync(lloom_hip_ctx* ctx);
 
 /* ---------------------------------------------------------------- memory --

@@ -49,8 +49,11 @@ static int fail(int code, const char* fmt, ...) {
         if (e_ != hipSuccess) return fail(LLOOM_HIP_EHIP, "%s: %s", #expr, hipGetErrorString(e_)); \
     } while (0)
 
+// The caller's stream, verbatim: NULL is HIP's null stream (torch's default
+// stream handle is 0), never silently another stream.
 static hipStream_t pick_stream(lloom_hip_ctx* ctx, void* stream) {
-    return stream ? (hipStream_t)stream : ctx->stream;
+    (void)ctx;
+    return (hipStream_t)stream;
 }
 
 static bool is_weight_type(int t) { return t == T_Q8_0 || t == T_Q4K || t == T_Q6K; }
@@ -72,7 +75,8 @@ static const char* type_name(int t) {
 static int ensure_ws(lloom_hip_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->ws_bytes) {
         if (ctx->ws) {
-            HIP_OK(hipStreamSynchronize(ctx->stream));
+            // earlier calls may still read it on any stream
+            HIP_OK(hipDeviceSynchronize());
             HIP_OK(hipFree(ctx->ws));
             ctx->ws = nullptr;
             ctx->ws_bytes = 0;
@@ -143,7 +147,7 @@ int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows) {
 int lloom_hip_ctx_sync(lloom_hip_ctx* ctx) {
     if (!ctx) return fail(LLOOM_HIP_EINVAL, "ctx_sync: null context");
     HIP_OK(hipSetDevice(ctx->device));
-    HIP_OK(hipStreamSynchronize(ctx->stream));
+    HIP_OK(hipDeviceSynchronize());
     int flag = 0;
     HIP_OK(hipMemcpy(&flag, ctx->flags, sizeof(int), hipMemcpyDeviceToHost));
     if (flag) {

@@ -52,6 +52,9 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
     return (float)h;
 }
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    // The barrier keeps the f32 value: without it the compiler folds a
+    // preceding multiply into v_fma_mix (one rounding, -0 turned into +0).
+    asm volatile("" : "+v"(f));
     _Float16 h = (_Float16)f;
     return __builtin_bit_cast(uint16_t, h);
 }
