@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-matmul path (BASELINE.json's metric).
+
+Headline (`value`): the Q4_K decode matvec batch sweep of BASELINE.json
+x f32 [B, 2048] ~N(0,1) for B in {1,2,4,8,16}, W [6144, 2048]
+~N(0,0.02) quantized to Q4_K.  One "step" is one pass of the sweep (five
+qmatmul calls, each on the next of R distinct weight copies, R * 7.08 MB >=
+512 MB so the 256 MB Infinity Cache cannot hold them).  `value` is the
+algorithmic bytes of the timed steps (weights + x f32 + y f32, as BASELINE.md
+counts them) divided by the timed region, in GB/s.  The launches of the
+timed steps are replayed from one HIP graph (decode launches are a few
+microseconds each; the graph keeps host launch overhead out), bracketed by
+HIP events on the stream they run on.
+
+`details` adds the other BASELINE configs (C1 Q8_0 decode, C3 Q4_K prefill
+TFLOP/s, C4 decoder-layer decode, C5 routed experts) measured the same way,
+and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
+(oracle/kq_cpubase.c) on the same weights on a bounded sample.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
+I8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POP/s
+ROTATE_BYTES = 512 << 20   # distinct weight bytes cycled through per config
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-details", action="store_true", help="only the headline config")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    return ap.parse_args()
+
+
+class Rotation:
+    """R copies of one packed weight in one device buffer (distinct memory)."""
+
+    def __init__(self, qt, copies):
+        import torch
+
+        from lloom_amd import QTensor
+
+        size = qt.storage.numel()
+        stride = (size + 255) // 256 * 256
+        self.buf = torch.empty(stride * copies, dtype=torch.uint8, device=qt.storage.device)
+        self.tensors = []
+        for i in range(copies):
+            view = self.buf[i * stride:i * stride + size]
+            view.copy_(qt.storage)
+            self.tensors.append(QTensor(view, qt.shape, qt.dtype))
+
+    def __len__(self):
+        return len(self.tensors)
+
+
+def copies_for(packed_bytes):
+    return max(2, math.ceil(ROTATE_BYTES / packed_bytes))
+
+
+def time_graph(fn_list, reps, warmup):
+    """Capture fn_list (a list of zero-arg launch callables) into one graph,
+    replay it `warmup` times, then time `reps` replays with events.
+    Returns seconds per replay."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in fn_list:  # eager warm-up (allocations, code objects)
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fn_list:
+            f()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / reps
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one "
+                                   "MI355X; the multi-GPU layout is described in DESIGN.md"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import lloom_amd as L
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    lib = L.lib()  # raises if the HIP library is not built
+
+    def cu(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+    # ---------------------------------------------------- headline: C2 ---
+    n, k = 6144, 2048
+    Bs = [1, 2, 4, 8, 16]
+    w = L.synth_normal(1, n * k, 0.0, 0.02)
+    qt = L.QTensor.quantize(cu(w).view(n, k), L.GgmlDType.Q4K)
+    wbytes = qt.packed_bytes()
+    rot = Rotation(qt, copies_for(wbytes))
+    xs = {b: cu(L.synth_normal(1000 + b, b * k)).view(b, k) for b in Bs}
+    ys = {b: torch.empty((b, n), device=dev) for b in Bs}
+    algo = {b: wbytes + b * k * 4 + b * n * 4 for b in Bs}
+
+    counter = [0]
+
+    def launch(b, qtensor):
+        return lambda: L.QMatMul(qtensor).forward_into(xs[b], ys[b])
+
+    sweep = []
+    for step in range(args.steps):
+        for b in Bs:
+            sweep.append(launch(b, rot.tensors[counter[0] % len(rot)]))
+            counter[0] += 1
+    torch.cuda.synchronize()
+    t_step = time_graph(sweep, 1, args.warmup) / args.steps
+    step_bytes = sum(algo.values())
+    value = step_bytes / t_step / 1e9
+
+    # per-B kernel figures (same method, one B per graph)
+    per_b = {}
+    for b in Bs:
+        fns = [launch(b, rot.tensors[i % len(rot)]) for i in range(len(rot))]
+        t = time_graph(fns, 3, 1) / len(fns)
+        per_b[str(b)] = {"us": round(t * 1e6, 3), "GB/s": round(algo[b] / t / 1e9, 1),
+                         "hbm_frac": round(algo[b] / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+    details = {"c2_q4k_decode_per_batch": per_b, "rotation_copies": len(rot),
+               "rotation_bytes": len(rot) * wbytes}
+    del rot
+    torch.cuda.empty_cache()
+
+    if not args.no_details:
+        details.update(run_details(L, cu, np, torch, dev, args))
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(L, qt, xs, n, k, Bs, algo, args.cpu_seconds)
+
+    line = {
+        "metric": "Q4_K/Q8_0 QMatMul decode GB/s (% HBM peak) + prefill TFLOP/s (% i8 MFMA)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4k-weights/q8k-activations (int8 dot4, f32 scales)",
+        "data": "synthetic (SplitMix64/xoshiro256** Box-Muller, seeded), random-init weights",
+        "config": {"workload": "C2 Q4_K decode matvec sweep, W [6144,2048] Q4_K, x f32 [B,2048], "
+                               "B in {1,2,4,8,16}; one step = the 5 calls",
+                   "n": n, "k": k, "batches": Bs},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "details": details,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def run_details(L, cu, np, torch, dev, args):
+    out = {}
+    # C1 Q8_0 decode
+    n, k = 8192, 2048
+    qt = L.QTensor.quantize(cu(L.synth_normal(0, n * k, 0.0, 0.02)).view(n, k), L.GgmlDType.Q8_0)
+    rot = Rotation(qt, copies_for(qt.packed_bytes()))
+    x = cu(L.synth_normal(1000, k)).view(1, k)
+    y = torch.empty((1, n), device=dev)
+    t = time_graph([(lambda q=q: L.QMatMul(q).forward_into(x, y)) for q in rot.tensors], 3, 1) / len(rot)
+    b = qt.packed_bytes() + k * 4 + n * 4
+    out["c1_q8_0_decode"] = {"us": round(t * 1e6, 3), "GB/s": round(b / t / 1e9, 1),
+                             "hbm_frac": round(b / t / 1e9 / 8000.0, 4)}
+    del rot
+    # C3 Q4_K prefill
+    n, k = 8192, 2048
+    qt = L.QTensor.quantize(cu(L.synth_normal(2, n * k, 0.0, 0.02)).view(n, k), L.GgmlDType.Q4K)
+    c3 = {}
+    for m in (64, 512, 2048):
+        x = cu(L.synth_normal(2000 + m, m * k)).view(m, k)
+        y = torch.empty((m, n), device=dev)
+        reps = 10 if m < 2048 else 4
+        t = time_graph([lambda: L.QMatMul(qt).forward_into(x, y)], reps, 1)
+        ops = 2.0 * m * n * k
+        c3[str(m)] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 2),
+                      "mfma_frac": round(ops / t / 1e12 / I8_PEAK_TOPS, 4)}
+    out["c3_q4k_prefill"] = c3
+    # C4 decoder layer decode (q,k,v,o,gate,up in Q4_K; down in Q6_K)
+    shapes = [("q", 2048, 2048, 12), ("k", 512, 2048, 12), ("v", 512, 2048, 12), ("o", 2048, 2048, 12),
+              ("gate", 8192, 2048, 12), ("up", 8192, 2048, 12), ("down", 2048, 8192, 14)]
+    layers = []
+    total = 0
+    for i, (name, nn, kk, dt) in enumerate(shapes):
+        q = L.QTensor.quantize(cu(L.synth_normal(30 + i, nn * kk, 0.0, 0.02)).view(nn, kk), dt)
+        layers.append((q, nn, kk))
+        total += q.packed_bytes()
+    ncopy = copies_for(total)
+    copies = [[Rotation(q, 1).tensors[0] for (q, _, _) in layers] for _ in range(ncopy)]
+    c4 = {}
+    for bsz in (1, 4, 16):
+        xin = {kk: cu(L.synth_normal(300 + kk, bsz * kk)).view(bsz, kk) for kk in (2048, 8192)}
+        yout = {nn: torch.empty((bsz, nn), device=dev) for nn in (512, 2048, 8192)}
+        fns = []
+        for c in copies:
+            for (q, nn, kk), qc in zip(layers, c):
+                fns.append(lambda qc=qc, nn=nn, kk=kk: L.QMatMul(qc).forward_into(xin[kk], yout[nn]))
+        t = time_graph(fns, 3, 1) / ncopy
+        byts = total + sum(bsz * (kk + nn) * 4 for (_, nn, kk) in layers)
+        c4[str(bsz)] = {"us_per_layer": round(t * 1e6, 2), "GB/s": round(byts / t / 1e9, 1),
+                        "hbm_frac": round(byts / t / 1e9 / 8000.0, 4)}
+    out["c4_layer_decode"] = c4
+    del copies, layers
+    torch.cuda.empty_cache()
+    # C5 routed experts: 128 experts, gate/up [768, 2048], down [2048, 768], Q4_K
+    E, ff, hid, T, topk = 128, 768, 2048, 32, 8
+    gate = L.QTensor.quantize(cu(L.synth_normal(40, E * ff * hid, 0.0, 0.02)).view(E, ff, hid), 12)
+    up = L.QTensor.quantize(cu(L.synth_normal(41, E * ff * hid, 0.0, 0.02)).view(E, ff, hid), 12)
+    down = L.QTensor.quantize(cu(L.synth_normal(42, E * hid * ff, 0.0, 0.02)).view(E, hid, ff), 12)
+    logits = L.synth_uniform(4, T * E).reshape(T, E)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :topk].astype(np.int32)
+    ids_t = cu(ids)
+    x = cu(L.synth_normal(4000, T * hid)).view(T, 1, hid)
+    h = cu(L.synth_normal(4001, T * topk * ff)).view(T, topk, ff)
+    yg = torch.empty((T, topk, ff), device=dev)
+    yu = torch.empty((T, topk, ff), device=dev)
+    yd = torch.empty((T, topk, hid), device=dev)
+
+    def moe():
+        gate.indexed_moe_forward_into(x, ids_t, yg)
+        up.indexed_moe_forward_into(x, ids_t, yu)
+        down.indexed_moe_forward_into(h, ids_t, yd)
+
+    t = time_graph([moe], 5, 1)
+    distinct = len(np.unique(ids))
+    byts = distinct * (gate.packed_bytes() + up.packed_bytes() + down.packed_bytes()) // E
+    byts += (T * hid + T * topk * ff) * 4 + (2 * T * topk * ff + T * topk * hid) * 4
+    out["c5_moe_experts"] = {"us": round(t * 1e6, 2), "distinct_experts": distinct,
+                             "unique_expert_bytes": int(byts), "GB/s": round(byts / t / 1e9, 1),
+                             "hbm_frac": round(byts / t / 1e9 / 8000.0, 4),
+                             "note": "gate+up+down, 3 routed calls; working set fits the 256 MB MALL"}
+    return out
+
+
+def cpu_baseline(L, qt, xs, n, k, Bs, algo, budget_s):
+    """The C++ restatement of lloom-tensor's CPU QMatMul (AVX2 vec_dots and the
+    barrier-pool driver, oracle/kq_cpubase.c) on the same Q4_K bytes."""
+    import numpy as np
+
+    path = os.path.join(ROOT, "oracle", "libkq_cpubase.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    lib.cpb_matmul.argtypes = [ctypes.c_int, sz, sz, sz, vp, vp, vp]
+    lib.cpb_pool_init.argtypes = [ctypes.c_int]
+    phys = lib.cpb_physical_cores()
+    threads = lib.cpb_pool_init(max(1, min(phys, 16)))
+    w = np.ascontiguousarray(qt.data())
+    xh = {b: np.ascontiguousarray(xs[b].cpu().numpy()) for b in Bs}
+    yh = {b: np.empty((b, n), np.float32) for b in Bs}
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    for b in Bs:  # warm-up
+        lib.cpb_matmul(12, b, k, n, p(xh[b]), p(w), p(yh[b]))
+    iters, t0 = 0, time.perf_counter()
+    while True:
+        for b in Bs:
+            lib.cpb_matmul(12, b, k, n, p(xh[b]), p(w), p(yh[b]))
+        iters += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or iters >= 2000:
+            break
+    gbs = iters * sum(algo.values()) / el / 1e9
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "sample": f"C2 sweep B in {{1,2,4,8,16}} x {iters} iterations ({el:.1f} s), same Q4_K bytes, "
+                      f"restatement of lloom-tensor CPU QMatMul (AVX2, barrier pool); "
+                      f"physical cores {phys}, nproc {os.cpu_count()}, {cpu_model}"}
+
+
+if __name__ == "__main__":
+    main()

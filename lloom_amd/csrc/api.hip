@@ -260,18 +260,18 @@ int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int6
     if ((uintptr_t)x_dev % 16) return fail(LLOOM_HIP_EINVAL, "qmatmul: x must be 16-byte aligned");
     HIP_OK(hipSetDevice(ctx->device));
     hipStream_t s = pick_stream(ctx, stream);
-    if (m <= ctx->mv_rows_max) {
-        HIP_OK(launch_matvec(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, s));
-        return LLOOM_HIP_OK;
-    }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    void* qbuf = nullptr;
-    size_t need = gemm_workspace_bytes(ggml_type, k, m);
+    const bool decode = m <= ctx->mv_rows_max;
+    void* ws = nullptr;
+    size_t need = decode ? matvec_workspace_bytes(ggml_type, k, m) : gemm_workspace_bytes(ggml_type, k, m);
     if (need) {
-        int rc = ensure_ws(ctx, need, &qbuf);
+        int rc = ensure_ws(ctx, need, &ws);
         if (rc) return rc;
     }
-    HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, qbuf, s));
+    if (decode)
+        HIP_OK(launch_matvec(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, s));
+    else
+        HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, s));
     return LLOOM_HIP_OK;
 }
 

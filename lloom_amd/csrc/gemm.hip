@@ -6,8 +6,8 @@
 namespace lloom {
 
 size_t gemm_workspace_bytes(int type, int64_t k, int64_t m) {
-    (void)type; (void)k; (void)m;
-    return 0;
+    (void)m;
+    return matvec_workspace_bytes(type, k, 16);
 }
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
@@ -15,7 +15,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
     (void)qbuf;
     for (int64_t r = 0; r < m; r += 16) {
         int64_t mm = m - r < 16 ? m - r : 16;
-        hipError_t e = launch_matvec(type, w, x + r * k, y + r * n, n, k, mm, s);
+        hipError_t e = launch_matvec(type, w, x + r * k, y + r * n, n, k, mm, qbuf, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -12,9 +12,19 @@ hipError_t launch_quantize_act(int vec_dot_type, const float* x, void* out, int6
 hipError_t launch_quantize_weights(int type, const float* x, void* out, int64_t elems, hipStream_t s);
 hipError_t launch_dequantize(int type, const void* w, void* y, int out_dtype, int64_t elems, hipStream_t s);
 
-// matvec.hip: m <= 16
+// quant.hip: Q8_K activations in the split layout the MFMA kernels read:
+// qs int8 [m][k] then d f32 [k/256][16] (m padded to 16), 256-byte aligned.
+size_t split_q8k_bytes(int64_t k, int64_t m);
+void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d);
+hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s);
+
+// matvec.hip: m <= 16.  Rows up to MV_DOT_MAX_ROWS take the fused dot4
+// kernel; Q4_K with more rows takes the MFMA kernel on a workspace of
+// matvec_workspace_bytes.
+constexpr int MV_DOT_MAX_ROWS = 4;
+size_t matvec_workspace_bytes(int type, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                         hipStream_t s);
+                         void* ws, hipStream_t s);
 
 // gemm.hip: any m, int8 MFMA; qbuf is workspace for the quantized x
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,

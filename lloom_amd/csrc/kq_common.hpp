@@ -105,11 +105,60 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// Full-wave butterfly sum (wave64).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+// ---------------------------------------------- cross-lane exchanges --
+// DPP and permlane moves (pure VALU, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+constexpr int DPP_XOR1 = 0xb1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4e;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <-> 7-i within 8
+constexpr int DPP_ROW_MIRROR = 0x140;   // lane i <-> 15-i within 16
+
+// The value held by the partner 16-lane row (rows 0<->1, 2<->3) and by
+// the partner 32-lane half, via v_permlane16_swap / v_permlane32_swap of a
+// register with itself.  Selecting by lane parity gives the partner both
+// when the compiler keeps the two operands in separate registers (the pair
+// then holds even rows in .x and odd rows in .y) and when it gives both one
+// register (then both results hold the rows swapped).
+__device__ __forceinline__ float partner16(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                              false, false);
+    return __builtin_bit_cast(float, ((__lane_id() >> 4) & 1) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float partner32(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                              false, false);
+    return __builtin_bit_cast(float, (__lane_id() >> 5) ? r[0] : r[1]);
+}
+
+// Sum over the 16 lanes of each row, the result in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<DPP_XOR1>(v);
+    v += dpp<DPP_XOR2>(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    v += dpp<DPP_ROW_MIRROR>(v);
     return v;
+}
+// Full-wave (wave64) sum, the result in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += partner16(v);
+    return v + partner32(v);
+}
+// Full-wave max (NaN-ignoring, as fmaxf), the result in every lane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = __builtin_fmaxf(v, dpp<DPP_XOR1>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_XOR2>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_ROW_MIRROR>(v));
+    v = __builtin_fmaxf(v, partner16(v));
+    return __builtin_fmaxf(v, partner32(v));
 }
 
 #endif

@@ -207,7 +207,7 @@ __device__ __forceinline__ void fill_lds(const float* __restrict__ x, int64_t K,
             float4 v = *(const float4*)(x + mi * K + kc0 + sb * 256 + 4 * lane);
             float d;
             int bs;
-            uint32_t q = q8k_block_wave(v, lane, &d, &bs);
+            uint32_t q = q8k_block_wave(v, &d, &bs);
             *(uint32_t*)(lqs + mi * KC + sb * 256 + 4 * lane) = q;
             if ((lane & 3) == 0) lbs[b * 16 + (lane >> 2)] = bs;
             if (lane == 0) ld[b] = d;
@@ -255,10 +255,13 @@ __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict
         // first round of weight loads before the activation prologue
         TaskData td[R];
         int ti = lane;
+        // rows past n and tasks past T load a valid block (row n-1, task 0)
+        // and are never accumulated: no branch around the loads
+        const int t0 = ti < T ? ti : 0;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            int row = row0 + r;
-            if (ti < T && row < n) load_task<TYPE>(W + row * rowbytes, blk0 + ti / Tr::P, ti % Tr::P, td[r]);
+            int row = min(row0 + r, n - 1);
+            load_task<TYPE>(W + row * rowbytes, blk0 + t0 / Tr::P, t0 % Tr::P, td[r]);
         }
         __syncthreads();
         fill_lds<Tr::VT>(X, K, kc0, KC, m, lqs, ld, lbs);
@@ -267,8 +270,8 @@ __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict
             if (ti != lane) {
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    int row = row0 + r;
-                    if (row < n) load_task<TYPE>(W + row * rowbytes, blk0 + ti / Tr::P, ti % Tr::P, td[r]);
+                    int row = min(row0 + r, n - 1);
+                    load_task<TYPE>(W + row * rowbytes, blk0 + ti / Tr::P, ti % Tr::P, td[r]);
                 }
             }
 #pragma unroll
@@ -286,6 +289,98 @@ __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict
                 float v = wave_sum(acc[r][mi]);
                 if (lane == 0 && row < n) Y[(int64_t)mi * n + row] = v;
             }
+        }
+    }
+}
+
+// --------------------------------------------- Q4_K decode on int8 MFMA --
+// For 5..16 activation rows the dot4 kernel turns ALU-bound; this one puts
+// the per-sub-block dot on v_mfma_i32_16x16x32_i8.  A wave owns 16 weight
+// rows; the workgroup's KS waves split the superblocks of K and add their
+// partials through LDS.  Operands (k within one 32-element sub-block j):
+//   A (activations): lane l holds x_q8[m = l%16][32j + 8(l/16) + 0..7]
+//   B (weights):     lane l holds q4[n = l%16][32j + 8(l/16) + 0..7]
+//   D:               lane l holds D[m = 4(l/16) + t][n = l%16], t = 0..3
+// so the lane's four outputs all belong to its own weight row and the row's
+// sub-block scale is a lane-local integer: acc += sc[j] * D_j.  The Q4_K min
+// term sum_j m[j] * sum_{k in j} x_k is a second MFMA chain against the 6-bit
+// mins broadcast to all 8 bytes, accumulated over the superblock in the
+// MFMA's own C operand.  Activations come pre-quantized (Q8_K, bit-exact)
+// in the split layout of k_quantize_split_q8k: qs [m][K], d [K/256][16].
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+template <int KS>
+__global__ __launch_bounds__(64 * KS) void k_mv_mfma_q4k(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                         const float* __restrict__ xd, float* __restrict__ Y, int n,
+                                                         int K, int m) {
+    __shared__ float4 part[KS][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int nrow = blockIdx.x * 16 + c16;
+    const int nload = min(nrow, n - 1);
+    const int nsb = K >> 8;
+    const uint8_t* wrow = W + (int64_t)nload * nsb * Q4K_BYTES;
+    const bool arow_ok = c16 < m;
+    const int8_t* xrow = xq + (int64_t)(arow_ok ? c16 : 0) * K;
+    float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sb = wave; sb < nsb; sb += KS) {
+        const uint8_t* b = wrow + sb * Q4K_BYTES;
+        const uint4 hdr = *(const uint4*)b;
+        uint2 q[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[c] = *(const uint2*)(b + 16 + 32 * c + 8 * g);
+        long a[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = arow_ok ? *(const long*)(xrow + sb * 256 + 32 * j + 8 * g) : 0l;
+        const float4 dy = *(const float4*)(xd + sb * 16 + 4 * g);
+        const float d = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
+        v4i accs = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int sc, mn;
+            if (j < 4) {
+                sc = byte_of(hdr.y, j) & 63;
+                mn = byte_of(hdr.z, j) & 63;
+            } else {
+                sc = (byte_of(hdr.w, j - 4) & 0xF) | ((byte_of(hdr.y, j - 4) >> 6) << 4);
+                mn = (byte_of(hdr.w, j - 4) >> 4) | ((byte_of(hdr.z, j - 4) >> 6) << 4);
+            }
+            const int c = j >> 1, sh = (j & 1) * 4;
+            const uint32_t lo = (q[c].x >> sh) & 0x0F0F0F0Fu, hi = (q[c].y >> sh) & 0x0F0F0F0Fu;
+            const long bw = (long)(((uint64_t)hi << 32) | lo);
+            const v4i zero = {0, 0, 0, 0};
+            const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
+            const uint32_t mrep = (uint32_t)mn * 0x01010101u;
+            const long bm = (long)(((uint64_t)mrep << 32) | mrep);
+            accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bm, accm, 0, 0, 0);
+            accs[0] += sc * dj[0];
+            accs[1] += sc * dj[1];
+            accs[2] += sc * dj[2];
+            accs[3] += sc * dj[3];
+        }
+        out[0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
+        out[1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
+        out[2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
+        out[3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
+    }
+    if (KS > 1) {
+        part[wave][lane] = make_float4(out[0], out[1], out[2], out[3]);
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int w = 1; w < KS; w++) {
+            float4 p = part[w][lane];
+            out[0] += p.x;
+            out[1] += p.y;
+            out[2] += p.z;
+            out[3] += p.w;
+        }
+    }
+    if (nrow < n) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int mi = 4 * g + t;
+            if (mi < m) Y[(int64_t)mi * n + nrow] = out[t];
         }
     }
 }
@@ -329,8 +424,24 @@ static hipError_t launch_type(const void* w, const float* x, float* y, int n, in
     return launch_mb<TYPE, 16>(w, x, y, n, K, m, s);
 }
 
+size_t matvec_workspace_bytes(int type, int64_t k, int64_t m) {
+    if (type != T_Q4K || m <= MV_DOT_MAX_ROWS) return 0;
+    return split_q8k_bytes(k, m);
+}
+
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                         hipStream_t s) {
+                         void* ws, hipStream_t s) {
+    if (type == T_Q4K && m > MV_DOT_MAX_ROWS) {
+        int8_t* xq;
+        float* xd;
+        split_q8k_ptrs(ws, k, m, &xq, &xd);
+        hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
+        if (e != hipSuccess) return e;
+        constexpr int KS = 4;
+        hipLaunchKernelGGL(k_mv_mfma_q4k<KS>, dim3((unsigned)((n + 15) / 16)), dim3(64 * KS), 0, s,
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
+        return hipGetLastError();
+    }
     switch (type) {
         case T_Q4K: return launch_type<T_Q4K>(w, x, y, (int)n, (int)k, (int)m, s);
         case T_Q6K: return launch_type<T_Q6K>(w, x, y, (int)n, (int)k, (int)m, s);

@@ -26,11 +26,46 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
     float4 v = *(const float4*)(x + blk * 256 + 4 * lane);
     float d;
     int bs;
-    uint32_t q = q8k_block_wave(v, lane, &d, &bs);
+    uint32_t q = q8k_block_wave(v, &d, &bs);
     uint8_t* b = out + blk * Q8K_BYTES;
     *(uint32_t*)(b + Q8K_QS + 4 * lane) = q;
     if ((lane & 3) == 0) *(int16_t*)(b + Q8K_BS + 2 * (lane >> 2)) = (int16_t)bs;
     if (lane == 0) *(float*)b = d;
+}
+
+// Q8_K into the split layout (qs [m][k], d [k/256][16]) read by the MFMA
+// kernels.  One block per wave; the values are those of k_quantize_q8k.
+__global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restrict__ x, int8_t* __restrict__ qs,
+                                                            float* __restrict__ dt, int m, int k) {
+    const int lane = threadIdx.x & 63;
+    const int nsb = k >> 8;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= (int64_t)m * nsb) return;
+    const int mi = (int)(blk / nsb), sb = (int)(blk - (int64_t)mi * nsb);
+    const float4 v = *(const float4*)(x + (int64_t)mi * k + sb * 256 + 4 * lane);
+    float d;
+    int bs;
+    const uint32_t q = q8k_block_wave(v, &d, &bs);
+    *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + 4 * lane) = q;
+    if (lane == 0) dt[sb * 16 + mi] = d;
+}
+
+size_t split_q8k_bytes(int64_t k, int64_t m) {
+    size_t qb = ((size_t)m * k + 255) & ~(size_t)255;
+    return qb + (size_t)(k / 256) * 16 * sizeof(float);
+}
+
+void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d) {
+    size_t qb = ((size_t)m * k + 255) & ~(size_t)255;
+    *qs = (int8_t*)base;
+    *d = (float*)((uint8_t*)base + qb);
+}
+
+hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s) {
+    const int64_t nb = m * (k / 256);
+    hipLaunchKernelGGL(k_quantize_split_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, qs, d, (int)m,
+                       (int)k);
+    return hipGetLastError();
 }
 
 // Q8_0: one 32-element block per 8 lanes (f16 d, i8 qs[32]); the 34-byte

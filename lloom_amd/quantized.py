@@ -178,6 +178,17 @@ class QTensor:
 
     indexed_moe_forward_with = indexed_moe_forward
 
+    def indexed_moe_forward_into(self, x, ids, y):
+        """indexed_moe_forward into a preallocated contiguous f32 y
+        [batch, topk, n]; non-strict (no stream sync), so it can be captured
+        in a graph; lloom_hip_ctx_sync reports a bad id afterwards."""
+        n_experts, n, k = self.shape
+        batch, in_dim1, _ = x.shape
+        topk = ids.shape[1]
+        check(lib().lloom_hip_moe_matmul(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage), n_experts, n,
+                                         k, _ptr(x), batch, in_dim1, _ptr(ids), topk, _ptr(y), 0, _stream(x)))
+        return y
+
     def indexed_moe_forward_pair(self, up, x, ids, arm=None):
         """Gate and up of one routed layer: two calls (mod.rs:1472-1475 off Metal)."""
         return self.indexed_moe_forward(x, ids, arm), up.indexed_moe_forward(x, ids, arm)
@@ -218,6 +229,15 @@ class QMatMul:
         return y
 
     __call__ = forward
+
+    def forward_into(self, xs, y):
+        """forward into a preallocated contiguous f32 y [m, n] (xs [m, k] f32
+        contiguous): no allocation, so it can be captured in a graph."""
+        n, k = self.qtensor.shape
+        m = xs.numel() // k
+        check(lib().lloom_hip_qmatmul(_ctx(_dev_index(xs)), int(self.qtensor.dtype), _ptr(self.qtensor.storage), n,
+                                      k, _ptr(xs), 0, m, _ptr(y), 0, _stream(xs)))
+        return y
 
 
 # ---------------------------------------------------------- functions ---

@@ -69,6 +69,17 @@ def test_quantize_act_bit_exact(L, vt):
         assert np.array_equal(got, want)
 
 
+def test_quantize_act_q8k_max_at_every_position(L):
+    """The block max is a cross-lane reduction: put it at each of the 256
+    positions (and a tie after it) and check the exact bytes."""
+    x = np.full((256, 256), 0.5, np.float32)
+    for i in range(256):
+        x[i, i] = -3.0
+        x[i, (i + 97) % 256] = 3.0  # same |x|: the first index must win
+    got = L.quantize_act(_cuda(x), O.Q8K).cpu().numpy()
+    assert np.array_equal(got, np.concatenate([O.quantize(O.Q8K, r) for r in x]))
+
+
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
 def test_weight_quantize_bit_exact(L, dt):
     cases = [
@@ -141,19 +152,24 @@ def test_qmatmul_closed_form_inputs(L, dt):
 
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
 def test_decode_rows_batch_invariant(L, dt):
-    """Within the decode route every activation row is computed alone, so a
+    """Within one decode kernel every activation row is computed alone, so a
     row's output does not depend on its batch (qmm_batch,
-    quantized_tests.rs:239-275, exact on the CPU arm)."""
+    quantized_tests.rs:239-275, exact on the CPU arm).  Q4_K with 5..16 rows
+    runs the MFMA kernel, 1..4 the dot4 kernel: each group is checked
+    against its own full batch (across the two kernels only the tolerance
+    holds, as on the reference's CUDA and Metal arms)."""
     rng = np.random.default_rng(3)
     n, k = 96, 1024
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     x = rng.standard_normal((16, k)).astype(np.float32)
     qt = L.QTensor.quantize(_cuda(w), dt)
     mm = L.QMatMul.from_qtensor(qt)
-    full = mm.forward(_cuda(x)).cpu().numpy()
-    for m in (1, 2, 5, 8):
-        part = mm.forward(_cuda(x[:m])).cpu().numpy()
-        assert np.array_equal(part.view(np.uint32), full[:m].view(np.uint32))
+    groups = [(4, (1, 2, 3)), (16, (5, 8, 13))] if dt == O.Q4K else [(16, (1, 2, 5, 8))]
+    for full_m, ms in groups:
+        full = mm.forward(_cuda(x[:full_m])).cpu().numpy()
+        for m in ms:
+            part = mm.forward(_cuda(x[:m])).cpu().numpy()
+            assert np.array_equal(part.view(np.uint32), full[:m].view(np.uint32)), (full_m, m)
 
 
 def test_qmatmul_rank3_input(L):
