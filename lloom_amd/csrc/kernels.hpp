@@ -21,7 +21,7 @@ hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_
 // matvec.hip: m <= 16.  Rows up to MV_DOT_MAX_ROWS take the fused dot4
 // kernel; Q4_K with more rows takes the MFMA kernel on a workspace of
 // matvec_workspace_bytes.
-constexpr int MV_DOT_MAX_ROWS = 4;
+constexpr int MV_DOT_MAX_ROWS = 2;
 size_t matvec_workspace_bytes(int type, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, hipStream_t s);

@@ -195,42 +195,79 @@ __device__ __forceinline__ void compute_task(const TaskData& t, int p, int blk_l
     }
 }
 
-// Quantize x[:, kc0 : kc0 + KC] into LDS (qs, per-block d, Q8_K bsums).
-template <int VT>
-__device__ __forceinline__ void fill_lds(const float* __restrict__ x, int64_t K, int kc0, int KC, int m,
-                                         int8_t* lqs, float* ld, int* lbs) {
+// Activation prologue, split in two so the x loads are issued before the
+// weight loads (vmcnt retires loads in order: waiting for x must not mean
+// waiting for the weights).  A wave quantizes up to XN blocks per chunk
+// (XN <= XQ); the loads are unconditional (a block past the end reloads
+// block 0) so no load sits under a branch.
+constexpr int XQ = 8;
+
+template <int VT, int XN>
+__device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int64_t K, int kc0, int KC, int m,
+                                           float4 (&xv)[XN]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if constexpr (VT == T_Q8K) {
-        const int nbc = KC / 256;
-        for (int b = wave; b < m * nbc; b += MV_WAVES) {
-            int mi = b / nbc, sb = b - mi * nbc;
-            float4 v = *(const float4*)(x + mi * K + kc0 + sb * 256 + 4 * lane);
-            float d;
-            int bs;
-            uint32_t q = q8k_block_wave(v, &d, &bs);
-            *(uint32_t*)(lqs + mi * KC + sb * 256 + 4 * lane) = q;
-            if ((lane & 3) == 0) lbs[b * 16 + (lane >> 2)] = bs;
-            if (lane == 0) ld[b] = d;
+        const int nbc = KC / 256, total = m * nbc;
+#pragma unroll
+        for (int i = 0; i < XN; i++) {
+            const int b = wave + MV_WAVES * i;
+            const int bb = b < total ? b : 0;
+            const int mi = bb / nbc, sb = bb - mi * nbc;
+            xv[i] = *(const float4*)(x + mi * K + kc0 + sb * 256 + 4 * lane);
         }
     } else {
-        const int nbc = KC / 32;
-        const int total = m * nbc;
-        for (int b0 = wave * 8; b0 < total; b0 += 8 * MV_WAVES) {
-            int b = b0 + (lane >> 3), sub = lane & 7;
-            bool ok = b < total;
-            int mi = ok ? b / nbc : 0, bl = ok ? b - mi * nbc : 0;
-            float4 v = ok ? *(const float4*)(x + mi * K + kc0 + bl * 32 + 4 * sub) : make_float4(0, 0, 0, 0);
-            uint16_t d16;
-            uint32_t q = q8_0_block_8lanes(v, &d16);
-            if (ok) {
-                *(uint32_t*)(lqs + mi * KC + bl * 32 + 4 * sub) = q;
-                if (sub == 0) ld[b] = f16_to_f32(d16);
+        const int nbc = KC / 32, total = m * nbc;
+#pragma unroll
+        for (int i = 0; i < XN; i++) {
+            const int b = wave * 8 + 8 * MV_WAVES * i + (lane >> 3);
+            const int bb = b < total ? b : 0;
+            const int mi = bb / nbc, bl = bb - mi * nbc;
+            xv[i] = *(const float4*)(x + mi * K + kc0 + bl * 32 + 4 * (lane & 7));
+        }
+    }
+}
+
+// Quantize the prefetched blocks (every block exactly as from_float) into
+// LDS: qs [m][KC], d [m][KC / block], Q8_K bsums [m][KC / 16].
+template <int VT, int XN>
+__device__ __forceinline__ void quantize_lds(const float4 (&xv)[XN], int KC, int m, int8_t* lqs, float* ld,
+                                             int* lbs) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if constexpr (VT == T_Q8K) {
+        const int nbc = KC / 256, total = m * nbc;
+#pragma unroll
+        for (int i = 0; i < XN; i++) {
+            const int b = wave + MV_WAVES * i;
+            if (b < total) {  // wave-uniform
+                const int mi = b / nbc, sb = b - mi * nbc;
+                float d;
+                int bs;
+                const uint32_t q = q8k_block_wave(xv[i], &d, &bs);
+                *(uint32_t*)(lqs + mi * KC + sb * 256 + 4 * lane) = q;
+                if ((lane & 3) == 0) lbs[b * 16 + (lane >> 2)] = bs;
+                if (lane == 0) ld[b] = d;
+            }
+        }
+    } else {
+        const int nbc = KC / 32, total = m * nbc;
+#pragma unroll
+        for (int i = 0; i < XN; i++) {
+            const int b0 = wave * 8 + 8 * MV_WAVES * i;
+            if (b0 < total) {  // wave-uniform; the 8-lane groups stay whole
+                const int b = b0 + (lane >> 3), sub = lane & 7;
+                uint16_t d16;
+                const uint32_t q = q8_0_block_8lanes(xv[i], &d16);
+                if (b < total) {
+                    const int mi = b / nbc, bl = b - mi * nbc;
+                    *(uint32_t*)(lqs + mi * KC + bl * 32 + 4 * sub) = q;
+                    if (sub == 0) ld[b] = f16_to_f32(d16);
+                }
             }
         }
     }
 }
 
-template <int TYPE, int MB, int R>
+template <int TYPE, int MB, int R, int XN>
 __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                         float* __restrict__ Y, int n, int K, int m, int KC) {
     using Tr = MvTraits<TYPE>;
@@ -252,25 +289,26 @@ __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict
     const int T = nbc * Tr::P;  // tasks per row per chunk
     for (int kc0 = 0; kc0 < K; kc0 += KC) {
         const int blk0 = kc0 / Tr::BE;
-        // first round of weight loads before the activation prologue
+        if (kc0) __syncthreads();  // the previous chunk's readers are done with LDS
+        float4 xv[XN];
+        prefetch_x<Tr::VT, XN>(X, K, kc0, KC, m, xv);
+        // first round of weight loads; rows past n and tasks past T load a
+        // valid block (row n-1, task 0) and are never accumulated
         TaskData td[R];
         int ti = lane;
-        // rows past n and tasks past T load a valid block (row n-1, task 0)
-        // and are never accumulated: no branch around the loads
         const int t0 = ti < T ? ti : 0;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            int row = min(row0 + r, n - 1);
+            const int row = min(row0 + r, n - 1);
             load_task<TYPE>(W + row * rowbytes, blk0 + t0 / Tr::P, t0 % Tr::P, td[r]);
         }
-        __syncthreads();
-        fill_lds<Tr::VT>(X, K, kc0, KC, m, lqs, ld, lbs);
+        quantize_lds<Tr::VT, XN>(xv, KC, m, lqs, ld, lbs);
         __syncthreads();
         for (; ti < T; ti += 64) {
             if (ti != lane) {
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    int row = min(row0 + r, n - 1);
+                    const int row = min(row0 + r, n - 1);
                     load_task<TYPE>(W + row * rowbytes, blk0 + ti / Tr::P, ti % Tr::P, td[r]);
                 }
             }
@@ -282,11 +320,11 @@ __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict
     }
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        int row = row0 + r;
+        const int row = row0 + r;
 #pragma unroll
         for (int mi = 0; mi < MB; mi++) {
             if (mi < m) {
-                float v = wave_sum(acc[r][mi]);
+                const float v = wave_sum(acc[r][mi]);
                 if (lane == 0 && row < n) Y[(int64_t)mi * n + row] = v;
             }
         }
@@ -294,103 +332,133 @@ __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict
 }
 
 // --------------------------------------------- Q4_K decode on int8 MFMA --
-// For 5..16 activation rows the dot4 kernel turns ALU-bound; this one puts
-// the per-sub-block dot on v_mfma_i32_16x16x32_i8.  A wave owns 16 weight
-// rows; the workgroup's KS waves split the superblocks of K and add their
-// partials through LDS.  Operands (k within one 32-element sub-block j):
-//   A (activations): lane l holds x_q8[m = l%16][32j + 8(l/16) + 0..7]
-//   B (weights):     lane l holds q4[n = l%16][32j + 8(l/16) + 0..7]
-//   D:               lane l holds D[m = 4(l/16) + t][n = l%16], t = 0..3
+// For more activation rows the dot4 kernel turns ALU-bound; this one puts
+// the per-sub-block dot on v_mfma_i32_16x16x32_i8.  A workgroup owns 16*NT
+// weight rows (NT tiles of 16); its KS waves split the superblocks of K and
+// add their partials through LDS.  Operands (k within one 32-element
+// sub-block j, g = lane / 16):
+//   A (activations): lane l holds x_q8[m = l%16][32j + 8g + 0..7]
+//   B (weights):     lane l holds q4[n = l%16][32j + 8g + 0..7]
+//   D:               lane l holds D[m = 4g + t][n = l%16], t = 0..3
 // so the lane's four outputs all belong to its own weight row and the row's
 // sub-block scale is a lane-local integer: acc += sc[j] * D_j.  The Q4_K min
 // term sum_j m[j] * sum_{k in j} x_k is a second MFMA chain against the 6-bit
 // mins broadcast to all 8 bytes, accumulated over the superblock in the
 // MFMA's own C operand.  Activations come pre-quantized (Q8_K, bit-exact)
-// in the split layout of k_quantize_split_q8k: qs [m][K], d [K/256][16].
+// from k_quantize_split_q8k, laid out so a lane's 64 bytes of a superblock
+// (its 8 bytes of each sub-block) are contiguous: one A tile serves NT weight
+// tiles.
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-template <int KS>
+template <int KS, int NT>
 __global__ __launch_bounds__(64 * KS) void k_mv_mfma_q4k(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                          const float* __restrict__ xd, float* __restrict__ Y, int n,
                                                          int K, int m) {
-    __shared__ float4 part[KS][64];
+    __shared__ float4 part[KS > 1 ? KS - 1 : 1][NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int nrow = blockIdx.x * 16 + c16;
-    const int nload = min(nrow, n - 1);
     const int nsb = K >> 8;
-    const uint8_t* wrow = W + (int64_t)nload * nsb * Q4K_BYTES;
-    const bool arow_ok = c16 < m;
-    const int8_t* xrow = xq + (int64_t)(arow_ok ? c16 : 0) * K;
-    float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int sb = wave; sb < nsb; sb += KS) {
-        const uint8_t* b = wrow + sb * Q4K_BYTES;
-        const uint4 hdr = *(const uint4*)b;
-        uint2 q[4];
+    const int64_t rowbytes = (int64_t)nsb * Q4K_BYTES;
+    const uint8_t* wrow[NT];
 #pragma unroll
-        for (int c = 0; c < 4; c++) q[c] = *(const uint2*)(b + 16 + 32 * c + 8 * g);
+    for (int t = 0; t < NT; t++) wrow[t] = W + (int64_t)min(blockIdx.x * 16 * NT + 16 * t + c16, n - 1) * rowbytes;
+    const bool arow_ok = c16 < m;
+    const int8_t* xrow = xq + (int64_t)(arow_ok ? c16 : 0) * K + 64 * g;
+    float out[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++) out[t][0] = out[t][1] = out[t][2] = out[t][3] = 0.0f;
+    for (int sb = wave; sb < nsb; sb += KS) {
+        uint4 hdr[NT];
+        uint2 q[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const uint8_t* b = wrow[t] + sb * Q4K_BYTES;
+            hdr[t] = *(const uint4*)b;
+#pragma unroll
+            for (int c = 0; c < 4; c++) q[t][c] = *(const uint2*)(b + 16 + 32 * c + 8 * g);
+        }
+        // unconditional loads (row clamped above), zeroed by select: a load
+        // under a divergent branch makes the compiler serialize them
+        uint4 av[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) av[i] = *(const uint4*)(xrow + sb * 256 + 16 * i);
+        const float4 dy = *(const float4*)(xd + sb * 16 + 4 * g);
         long a[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) a[j] = arow_ok ? *(const long*)(xrow + sb * 256 + 32 * j + 8 * g) : 0l;
-        const float4 dy = *(const float4*)(xd + sb * 16 + 4 * g);
-        const float d = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
-        v4i accs = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int sc, mn;
-            if (j < 4) {
-                sc = byte_of(hdr.y, j) & 63;
-                mn = byte_of(hdr.z, j) & 63;
-            } else {
-                sc = (byte_of(hdr.w, j - 4) & 0xF) | ((byte_of(hdr.y, j - 4) >> 6) << 4);
-                mn = (byte_of(hdr.w, j - 4) >> 4) | ((byte_of(hdr.z, j - 4) >> 6) << 4);
-            }
-            const int c = j >> 1, sh = (j & 1) * 4;
-            const uint32_t lo = (q[c].x >> sh) & 0x0F0F0F0Fu, hi = (q[c].y >> sh) & 0x0F0F0F0Fu;
-            const long bw = (long)(((uint64_t)hi << 32) | lo);
-            const v4i zero = {0, 0, 0, 0};
-            const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
-            const uint32_t mrep = (uint32_t)mn * 0x01010101u;
-            const long bm = (long)(((uint64_t)mrep << 32) | mrep);
-            accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bm, accm, 0, 0, 0);
-            accs[0] += sc * dj[0];
-            accs[1] += sc * dj[1];
-            accs[2] += sc * dj[2];
-            accs[3] += sc * dj[3];
+        for (int i = 0; i < 4; i++) {
+            a[2 * i] = arow_ok ? (long)(((uint64_t)av[i].y << 32) | av[i].x) : 0l;
+            a[2 * i + 1] = arow_ok ? (long)(((uint64_t)av[i].w << 32) | av[i].z) : 0l;
         }
-        out[0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
-        out[1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
-        out[2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
-        out[3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float d = f16_to_f32(hdr[t].x & 0xffffu), dmin = f16_to_f32(hdr[t].x >> 16);
+            v4i accs = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                int sc, mn;
+                if (j < 4) {
+                    sc = byte_of(hdr[t].y, j) & 63;
+                    mn = byte_of(hdr[t].z, j) & 63;
+                } else {
+                    sc = (byte_of(hdr[t].w, j - 4) & 0xF) | ((byte_of(hdr[t].y, j - 4) >> 6) << 4);
+                    mn = (byte_of(hdr[t].w, j - 4) >> 4) | ((byte_of(hdr[t].z, j - 4) >> 6) << 4);
+                }
+                const int c = j >> 1, sh = (j & 1) * 4;
+                const uint32_t lo = (q[t][c].x >> sh) & 0x0F0F0F0Fu, hi = (q[t][c].y >> sh) & 0x0F0F0F0Fu;
+                const long bw = (long)(((uint64_t)hi << 32) | lo);
+                const v4i zero = {0, 0, 0, 0};
+                const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
+                const uint32_t mrep = (uint32_t)mn * 0x01010101u;
+                const long bm = (long)(((uint64_t)mrep << 32) | mrep);
+                accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bm, accm, 0, 0, 0);
+                accs[0] += sc * dj[0];
+                accs[1] += sc * dj[1];
+                accs[2] += sc * dj[2];
+                accs[3] += sc * dj[3];
+            }
+            out[t][0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
+            out[t][1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
+            out[t][2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
+            out[t][3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
+        }
     }
     if (KS > 1) {
-        part[wave][lane] = make_float4(out[0], out[1], out[2], out[3]);
+        if (wave != 0) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) part[wave - 1][t][lane] = make_float4(out[t][0], out[t][1], out[t][2], out[t][3]);
+        }
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
-        for (int w = 1; w < KS; w++) {
-            float4 p = part[w][lane];
-            out[0] += p.x;
-            out[1] += p.y;
-            out[2] += p.z;
-            out[3] += p.w;
-        }
-    }
-    if (nrow < n) {
+        for (int w = 0; w < KS - 1; w++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int mi = 4 * g + t;
-            if (mi < m) Y[(int64_t)mi * n + nrow] = out[t];
+            for (int t = 0; t < NT; t++) {
+                const float4 p = part[w][t][lane];
+                out[t][0] += p.x;
+                out[t][1] += p.y;
+                out[t][2] += p.z;
+                out[t][3] += p.w;
+            }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int nrow = blockIdx.x * 16 * NT + 16 * t + c16;
+        if (nrow < n) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int mi = 4 * g + u;
+                if (mi < m) Y[(int64_t)mi * n + nrow] = out[t][u];
+            }
         }
     }
 }
 
-// Chunk of K staged in LDS at a time: all of K when it fits the budget.
+// Chunk of K staged in LDS at a time: the prologue quantizes at most
+// XQ blocks per wave, m * KC <= XQ * MV_WAVES * 256 elements.
 static int pick_kc(int type, int64_t K, int m) {
     const int be = type == T_Q8_0 ? 32 : 256;
-    const int64_t budget = 32768;  // bytes of int8 activations per chunk
-    int64_t kc = budget / m;
-    kc -= kc % 256;
+    int64_t kc = (int64_t)XQ * MV_WAVES * 256 / m;
+    kc -= kc % be;
     if (kc < be) kc = be;
     if (kc >= K) return (int)K;
     while (K % kc) kc -= be;  // chunks tile K exactly
@@ -404,14 +472,25 @@ static size_t lds_bytes(int type, int KC, int m) {
     return b;
 }
 
+template <int TYPE, int MB, int XN>
+static void launch_xn(const void* w, const float* x, float* y, int n, int K, int m, int KC, hipStream_t s) {
+    constexpr int R = 2;
+    const size_t shm = lds_bytes(TYPE, KC, m);
+    const dim3 grid((n + MV_WAVES * R - 1) / (MV_WAVES * R));
+    hipLaunchKernelGGL((k_matvec<TYPE, MB, R, XN>), grid, dim3(MV_THREADS), shm, s, (const uint8_t*)w, x, y, n, K,
+                       m, KC);
+}
+
 template <int TYPE, int MB>
 static hipError_t launch_mb(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
-    constexpr int R = 2;
-    int KC = pick_kc(TYPE, K, m);
-    size_t shm = lds_bytes(TYPE, KC, m);
-    dim3 grid((n + MV_WAVES * R - 1) / (MV_WAVES * R));
-    hipLaunchKernelGGL((k_matvec<TYPE, MB, R>), grid, dim3(MV_THREADS), shm, s, (const uint8_t*)w, x, y, n, K, m,
-                       KC);
+    const int KC = pick_kc(TYPE, K, m);
+    // blocks a wave quantizes per chunk: 256 elements (Q8_K) or 8 lanes x 32 (Q8_0) per step
+    const int per_step = TYPE == T_Q8_0 ? 32 * 8 * MV_WAVES : 256 * MV_WAVES;
+    const int steps = (m * KC + per_step - 1) / per_step;
+    if (steps <= 1) launch_xn<TYPE, MB, 1>(w, x, y, n, K, m, KC, s);
+    else if (steps <= 2) launch_xn<TYPE, MB, 2>(w, x, y, n, K, m, KC, s);
+    else if (steps <= 4) launch_xn<TYPE, MB, 4>(w, x, y, n, K, m, KC, s);
+    else launch_xn<TYPE, MB, 8>(w, x, y, n, K, m, KC, s);
     return hipGetLastError();
 }
 
@@ -437,9 +516,9 @@ hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int6
         split_q8k_ptrs(ws, k, m, &xq, &xd);
         hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
         if (e != hipSuccess) return e;
-        constexpr int KS = 4;
-        hipLaunchKernelGGL(k_mv_mfma_q4k<KS>, dim3((unsigned)((n + 15) / 16)), dim3(64 * KS), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
+        constexpr int KS = 8, NT = 2;
+        hipLaunchKernelGGL((k_mv_mfma_q4k<KS, NT>), dim3((unsigned)((n + 16 * NT - 1) / (16 * NT))), dim3(64 * KS),
+                           0, s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
         return hipGetLastError();
     }
     switch (type) {

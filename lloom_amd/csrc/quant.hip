@@ -33,8 +33,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
     if (lane == 0) *(float*)b = d;
 }
 
-// Q8_K into the split layout (qs [m][k], d [k/256][16]) read by the MFMA
-// kernels.  One block per wave; the values are those of k_quantize_q8k.
+// Q8_K into the split layout read by the MFMA kernels: d [k/256][16] (m
+// padded to 16) and qs [m][k] with each 256-byte superblock permuted so
+// that element 32j + 8g + b (sub-block j, lane group g, byte b) sits at
+// 64g + 8j + b: an MFMA lane group's 8 bytes of every sub-block are then
+// one contiguous 64-byte run.  One block per wave; the values are those of
+// k_quantize_q8k.
 __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restrict__ x, int8_t* __restrict__ qs,
                                                             float* __restrict__ dt, int m, int k) {
     const int lane = threadIdx.x & 63;
@@ -46,7 +50,9 @@ __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restr
     float d;
     int bs;
     const uint32_t q = q8k_block_wave(v, &d, &bs);
-    *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + 4 * lane) = q;
+    // lane owns elements 4*lane..: sub-block lane/8, group (lane%8)/2, byte 4*(lane%2)
+    const int off = 64 * ((lane & 7) >> 1) + 8 * (lane >> 3) + 4 * (lane & 1);
+    *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + off) = q;
     if (lane == 0) dt[sb * 16 + mi] = d;
 }
 
