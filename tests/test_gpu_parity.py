@@ -138,6 +138,18 @@ def test_qmatmul_matches_oracle(L, dt, m):
         assert_rows_close(y, O.matmul(dt, x, q, n), what=f"dt={dt} m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(17, 1, 256), (64, 128, 2048), (100, 7, 768), (128, 300, 512),
+                                   (200, 129, 1024), (257, 64, 256), (512, 256, 2048)])
+def test_prefill_gemm_q4k_shapes(L, m, n, k):
+    """The int8-MFMA prefill GEMM on ragged tiles (m, n not multiples of 128)."""
+    rng = np.random.default_rng(m * 7 + n)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1, :256] = 0.0  # an all-zero activation block (d = 0, S = 0)
+    y, q = _qmm(L, O.Q4K, w, x)
+    assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"gemm m={m} n={n} k={k}")
+
+
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
 def test_qmatmul_closed_form_inputs(L, dt):
     """The reference's closed-form GEMM inputs (quantized_tests.rs:1769-1903)."""
