@@ -202,16 +202,21 @@ def run_details(L, cu, np, torch, dev, args):
     # C3 Q4_K prefill
     n, k = 8192, 2048
     qt = L.QTensor.quantize(cu(L.synth_normal(2, n * k, 0.0, 0.02)).view(n, k), L.GgmlDType.Q4K)
-    c3 = {}
-    for m in (64, 512, 2048):
-        x = cu(L.synth_normal(2000 + m, m * k)).view(m, k)
-        y = torch.empty((m, n), device=dev)
-        reps = 10 if m < 2048 else 4
-        t = time_graph([lambda: L.QMatMul(qt).forward_into(x, y)], reps, 1)
-        ops = 2.0 * m * n * k
-        c3[str(m)] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 2),
-                      "mfma_frac": round(ops / t / 1e12 / I8_PEAK_TOPS, 4)}
-    out["c3_q4k_prefill"] = c3
+    from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
+
+    for mode_name, mode in (("f16", MMA_F16), ("int8", MMA_INT8)):
+        set_prefill_mma(mode)
+        c3 = {}
+        for m in (64, 512, 2048):
+            x = cu(L.synth_normal(2000 + m, m * k)).view(m, k)
+            y = torch.empty((m, n), device=dev)
+            reps = 10 if m < 2048 else 4
+            t = time_graph([lambda: L.QMatMul(qt).forward_into(x, y)], reps, 1)
+            ops = 2.0 * m * n * k
+            c3[str(m)] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 2),
+                          "i8_peak_frac": round(ops / t / 1e12 / I8_PEAK_TOPS, 4)}
+        out["c3_q4k_prefill_" + mode_name] = c3
+    set_prefill_mma(MMA_INT8)
     # C4 decoder layer decode (q,k,v,o,gate,up in Q4_K; down in Q6_K)
     shapes = [("q", 2048, 2048, 12), ("k", 512, 2048, 12), ("v", 512, 2048, 12), ("o", 2048, 2048, 12),
               ("gate", 8192, 2048, 12), ("up", 8192, 2048, 12), ("down", 2048, 8192, 14)]

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -28,6 +29,7 @@ struct lloom_hip_ctx {
     size_t ws_bytes = 0;
     int* flags = nullptr;  // [0] sticky expert-id error
     int mv_rows_max = 16;
+    int prefill_mma = GEMM_INT8;
     std::mutex mu;
 };
 
@@ -109,6 +111,7 @@ int lloom_hip_ctx_create(int device, lloom_hip_ctx** out) {
     HIP_OK(hipSetDevice(device));
     lloom_hip_ctx* c = new lloom_hip_ctx();
     c->device = device;
+    if (const char* e = getenv("LLOOM_HIP_PREFILL_MMA")) c->prefill_mma = strcmp(e, "f16") == 0 ? GEMM_F16 : GEMM_INT8;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return fail(LLOOM_HIP_EHIP, "ctx_create: stream creation failed");
@@ -141,6 +144,14 @@ int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows) {
     if (!ctx) return fail(LLOOM_HIP_EINVAL, "set_mv_rows_max: null context");
     if (rows < 1 || rows > 16) return fail(LLOOM_HIP_EINVAL, "set_mv_rows_max: %d is outside 1..16", rows);
     ctx->mv_rows_max = rows;
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_ctx_set_prefill_mma(lloom_hip_ctx* ctx, int mode) {
+    if (!ctx) return fail(LLOOM_HIP_EINVAL, "set_prefill_mma: null context");
+    if (mode != LLOOM_HIP_MMA_F16 && mode != LLOOM_HIP_MMA_INT8)
+        return fail(LLOOM_HIP_EINVAL, "set_prefill_mma: mode %d is neither F16 (0) nor INT8 (1)", mode);
+    ctx->prefill_mma = mode == LLOOM_HIP_MMA_INT8 ? GEMM_INT8 : GEMM_F16;
     return LLOOM_HIP_OK;
 }
 
@@ -263,7 +274,8 @@ int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int6
     std::lock_guard<std::mutex> lock(ctx->mu);
     const bool decode = m <= ctx->mv_rows_max;
     void* ws = nullptr;
-    size_t need = decode ? matvec_workspace_bytes(ggml_type, k, m) : gemm_workspace_bytes(ggml_type, k, m);
+    size_t need = decode ? matvec_workspace_bytes(ggml_type, k, m)
+                         : gemm_workspace_bytes(ggml_type, k, m, ctx->prefill_mma);
     if (need) {
         int rc = ensure_ws(ctx, need, &ws);
         if (rc) return rc;
@@ -271,7 +283,7 @@ int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int6
     if (decode)
         HIP_OK(launch_matvec(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, s));
     else
-        HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, s));
+        HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, ctx->prefill_mma, s));
     return LLOOM_HIP_OK;
 }
 

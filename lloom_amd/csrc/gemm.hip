@@ -34,6 +34,24 @@ namespace lloom {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// Tile order.  Workgroups are dealt round-robin to the 8 XCDs; renumber them
+// XCD-major so each XCD gets a contiguous range, then walk that range in
+// groups of GM m-blocks (column-major inside a group): the ~32 workgroups an
+// XCD runs at once cover a 4 x 8 block of tiles whose activation and weight
+// tiles fit its 4 MB L2, instead of re-reading them for every tile.
+__device__ __forceinline__ void tile_of(int nbm, int nbn, int& bm, int& bn) {
+    constexpr int GM = 4;
+    int pid = blockIdx.x;
+    if ((gridDim.x & 7) == 0) pid = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+    const int per_group = GM * nbn;
+    const int group = pid / per_group;
+    const int first = group * GM;
+    const int gsz = min(nbm - first, GM);
+    const int in = pid - group * per_group;
+    bm = first + in % gsz;
+    bn = in / gsz;
+}
+
 // --------------------------------------------------- activation prep --
 // Q8_K of every (row, superblock) block, bit-exact, into:
 //   xq  int8 [m][k]           natural order
@@ -172,13 +190,8 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / G_WN, wn = wave % G_WN;
     const int h = lane >> 5, c32 = lane & 31;
-    // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs, so
-    // renumber them XCD-major and let consecutive ids on one XCD walk the m
-    // blocks of one weight column block: that block then stays in one L2.
-    const int nbm = (m + G_BM - 1) / G_BM;
-    int lin = blockIdx.x;
-    if ((gridDim.x & 7) == 0) lin = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
-    const int bm = lin % nbm, bn = lin / nbm;
+    int bm, bn;
+    tile_of((m + G_BM - 1) / G_BM, (n + G_BN - 1) / G_BN, bm, bn);
     const int m0 = bm * G_BM, n0 = bn * G_BN;
     const int nsb = k >> 8;
 
@@ -195,27 +208,43 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
 
     for (int sb = 0; sb < nsb; sb++) {
         const uint8_t* cur = smem + (sb & 1) * G_STAGE;
-        if (sb + 1 < nsb) stage_issue(smem + ((sb + 1) & 1) * G_STAGE, xq, sp, dyt, W, m0, n0, m, n, k, sb + 1);
         const uint8_t* A = cur;
         const uint8_t* B = cur + G_A_BYTES;
         const int8_t* S = (const int8_t*)(B + G_B_BYTES);
         const float* D = (const float*)((const uint8_t*)S + G_S_BYTES);
-
-        // this lane's weight rows (one per n-tile): d, dmin, 6-bit scales and mins
-        uint4 hdr[G_NT];
+        // 1. everything this superblock needs, from LDS into registers, before
+        //    the next stage's loads are queued: the compiler cannot tell the
+        //    async LDS writes from these reads and would otherwise wait for
+        //    the next stage before the first read of this one.
+        uint4 hdr[G_NT], raw[G_NT][4];
 #pragma unroll
-        for (int b = 0; b < G_NT; b++) hdr[b] = *(const uint4*)(B + (wn * G_NT * 32 + b * 32 + c32) * 144);
+        for (int b = 0; b < G_NT; b++) {
+            const uint8_t* rb = B + (wn * G_NT * 32 + b * 32 + c32) * 144;
+            hdr[b] = *(const uint4*)rb;
+#pragma unroll
+            for (int c = 0; c < 4; c++) raw[b][c] = *(const uint4*)(rb + 16 + 32 * c + 16 * h);
+        }
+        v4i av[G_MT][8];
+        long smin[G_MT];
+        float4 dy[G_MT][4];
+#pragma unroll
+        for (int a = 0; a < G_MT; a++) {
+            const int row = wm * G_MT * 32 + a * 32 + c32;
+#pragma unroll
+            for (int j = 0; j < 8; j++) av[a][j] = *(const v4i*)(A + row * 256 + 16 * ((2 * j + h) ^ (row & 7)));
+            smin[a] = *(const long*)(S + row * 16 + 8 * h);
+            const float* dyp = D + wm * G_MT * 32 + a * 32 + 4 * h;
+#pragma unroll
+            for (int g = 0; g < 4; g++) dy[a][g] = *(const float4*)(dyp + 8 * g);
+        }
+        // 2. queue the next superblock into the other stage
+        if (sb + 1 < nsb) stage_issue(smem + ((sb + 1) & 1) * G_STAGE, xq, sp, dyt, W, m0, n0, m, n, k, sb + 1);
 
+        // 3. the MFMA work, from registers
         v16i dh[G_MT][G_NT], dl[G_MT][G_NT];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int c = j >> 1;
-            v4i av[G_MT];
-#pragma unroll
-            for (int a = 0; a < G_MT; a++) {
-                const int row = wm * G_MT * 32 + a * 32 + c32;
-                av[a] = *(const v4i*)(A + row * 256 + 16 * ((2 * j + h) ^ (row & 7)));
-            }
+            const int c = j >> 1, sh = (j & 1) * 4;
 #pragma unroll
             for (int b = 0; b < G_NT; b++) {
                 int sc;
@@ -223,10 +252,8 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
                     sc = byte_of(hdr[b].y, j) & 63;
                 else
                     sc = (byte_of(hdr[b].w, j - 4) & 0xF) | ((byte_of(hdr[b].y, j - 4) >> 6) << 4);
-                const uint4 raw = *(const uint4*)(B + (wn * G_NT * 32 + b * 32 + c32) * 144 + 16 + 32 * c + 16 * h);
-                const int sh = (j & 1) * 4;
-                const uint32_t q0 = (raw.x >> sh) & 0x0F0F0F0Fu, q1 = (raw.y >> sh) & 0x0F0F0F0Fu,
-                               q2 = (raw.z >> sh) & 0x0F0F0F0Fu, q3 = (raw.w >> sh) & 0x0F0F0F0Fu;
+                const uint32_t q0 = (raw[b][c].x >> sh) & 0x0F0F0F0Fu, q1 = (raw[b][c].y >> sh) & 0x0F0F0F0Fu,
+                               q2 = (raw[b][c].z >> sh) & 0x0F0F0F0Fu, q3 = (raw[b][c].w >> sh) & 0x0F0F0F0Fu;
                 const uint32_t shi = (uint32_t)sc >> 3, slo = (uint32_t)sc & 7u;
                 const v4i bhi = {(int)(q0 * shi), (int)(q1 * shi), (int)(q2 * shi), (int)(q3 * shi)};
                 const v4i blo = {(int)(q0 * slo), (int)(q1 * slo), (int)(q2 * slo), (int)(q3 * slo)};
@@ -234,19 +261,16 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
                 for (int a = 0; a < G_MT; a++) {
                     if (j == 0) {
                         const v16i zero = {};
-                        dh[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bhi, zero, 0, 0, 0);
-                        dl[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], blo, zero, 0, 0, 0);
+                        dh[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a][j], bhi, zero, 0, 0, 0);
+                        dl[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a][j], blo, zero, 0, 0, 0);
                     } else {
-                        dh[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bhi, dh[a][b], 0, 0, 0);
-                        dl[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], blo, dl[a][b], 0, 0, 0);
+                        dh[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a][j], bhi, dh[a][b], 0, 0, 0);
+                        dl[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a][j], blo, dl[a][b], 0, 0, 0);
                     }
                 }
             }
         }
         // superblock epilogue: min term on MFMA, then the f32 combination
-        long smin[G_MT];
-#pragma unroll
-        for (int a = 0; a < G_MT; a++) smin[a] = *(const long*)(S + (wm * G_MT * 32 + a * 32 + c32) * 16 + 8 * h);
 #pragma unroll
         for (int b = 0; b < G_NT; b++) {
             const float d = f16_to_f32(hdr[b].x & 0xffffu), dmin = f16_to_f32(hdr[b].x >> 16);
@@ -266,11 +290,9 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
                 const v16i zero = {};
                 const v16i mh = __builtin_amdgcn_mfma_i32_32x32x16_i8(smin[a], b1, zero, 0, 0, 0);
                 const v16i ml = __builtin_amdgcn_mfma_i32_32x32x16_i8(smin[a], b2, zero, 0, 0, 0);
-                const float* dyp = D + wm * G_MT * 32 + a * 32 + 4 * h;
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
-                    const float4 dy = *(const float4*)(dyp + 8 * g);
-                    const float dys[4] = {dy.x, dy.y, dy.z, dy.w};
+                    const float dys[4] = {dy[a][g].x, dy[a][g].y, dy[a][g].z, dy[a][g].w};
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
                         const int r = 4 * g + u;
@@ -281,6 +303,7 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
                 }
             }
         }
+        // 4. the next stage has landed (this wave's share) and is visible to all
         stage_wait();
     }
 
@@ -298,15 +321,202 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
         }
 }
 
+// ------------------------------------------------ Q4_K GEMM on fp16 MFMA --
+// The same product with both operands dequantized to fp16 (activations as
+// f16(dy * q8) of the bit-exact Q8_K quantization, weights as f16 of
+// d*sc*q - dmin*m) and v_mfma_f32_32x32x16_f16 accumulating all of K in f32:
+// no per-superblock epilogue at all, at half the int8 MFMA rate.  The
+// operand rounding (11 significant bits) costs about 1e-4 of a typical
+// output, which keeps a wide row inside the 1e-3 * max|y row| tolerance but
+// not a row of a handful of outputs near zero: opt-in, not the default.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// x f32 [m][k] -> Q8_K (bit-exact) -> f16(d * q) [m][k]
+__global__ __launch_bounds__(256) void k_gemm_prep_f16(const float* __restrict__ x, _Float16* __restrict__ xh, int m,
+                                                       int k) {
+    const int lane = threadIdx.x & 63;
+    const int nsb = k >> 8;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= (int64_t)m * nsb) return;
+    const int mi = (int)(blk / nsb), sb = (int)(blk - (int64_t)mi * nsb);
+    const float4 v = *(const float4*)(x + (int64_t)mi * k + sb * 256 + 4 * lane);
+    float d;
+    int bs;
+    const uint32_t q = q8k_block_wave(v, &d, &bs);
+    uint2 out;
+    out.x = (uint32_t)f32_to_f16(d * (float)(int8_t)(q & 0xff)) |
+            ((uint32_t)f32_to_f16(d * (float)(int8_t)((q >> 8) & 0xff)) << 16);
+    out.y = (uint32_t)f32_to_f16(d * (float)(int8_t)((q >> 16) & 0xff)) |
+            ((uint32_t)f32_to_f16(d * (float)(int8_t)(q >> 24)) << 16);
+    *(uint2*)(xh + (int64_t)mi * k + sb * 256 + 4 * lane) = out;
+}
+
+constexpr int H_BM = 128, H_BN = 128, H_BK = 64;
+constexpr int H_THREADS = 256;
+constexpr int H_TILE = H_BM * H_BK * 2;  // bytes of one A (or B) stage: 16 KB
+// LDS stage = A tile then B tile, each [128 rows][8 pieces of 8 halves],
+// piece p of row r at position p ^ (r & 7).
+__device__ __forceinline__ int h_pos(int row, int piece) { return row * 128 + 16 * (piece ^ (row & 7)); }
+
+__global__ __launch_bounds__(H_THREADS) void k_gemm_q4k_f16(const uint8_t* __restrict__ W,
+                                                            const _Float16* __restrict__ xh, float* __restrict__ Y,
+                                                            int m, int n, int k) {
+    __shared__ __align__(16) uint8_t smem[2][2 * H_TILE];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int h = lane >> 5, c32 = lane & 31;
+    int bm, bn;
+    tile_of((m + H_BM - 1) / H_BM, (n + H_BN - 1) / H_BN, bm, bn);
+    const int m0 = bm * H_BM, n0 = bn * H_BN;
+    const int nsteps = k / H_BK;
+    const int64_t rowbytes = (int64_t)(k >> 8) * Q4K_BYTES;
+
+    // weight dequant role: thread -> (row, half of the 32 qs bytes of a chunk)
+    const int brow = t >> 1, bhalf = t & 1;
+    const uint8_t* wrow = W + (int64_t)min(n0 + brow, n - 1) * rowbytes;
+    // activation DMA role: wave w moves chunks 4w..4w+3 (8 rows x 8 pieces each)
+    auto issue_a = [&](uint8_t* stage, int step) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = wave * 4 + i;
+            const int row = 8 * q + (lane >> 3);
+            const int piece = (lane & 7) ^ (row & 7);
+            const int grow = min(m0 + row, m - 1);
+            __builtin_amdgcn_global_load_lds(xh + (int64_t)grow * k + step * H_BK + 8 * piece,
+                                             (__attribute__((address_space(3))) void*)(stage + 1024 * q), 16, 0, 0);
+        }
+    };
+    auto dequant_b = [&](uint8_t* stage, const uint4& hdr, const uint4& raw, int step) {
+        const int c = step & 3;
+        const float d = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
+        int sc0, m0s, sc1, m1s;
+        if (c < 2) {
+            sc0 = byte_of(hdr.y, 2 * c) & 63;
+            m0s = byte_of(hdr.z, 2 * c) & 63;
+            sc1 = byte_of(hdr.y, 2 * c + 1) & 63;
+            m1s = byte_of(hdr.z, 2 * c + 1) & 63;
+        } else {
+            const uint32_t i0 = 2 * c - 4, i1 = 2 * c - 3;
+            sc0 = (byte_of(hdr.w, i0) & 0xF) | ((byte_of(hdr.y, i0) >> 6) << 4);
+            m0s = (byte_of(hdr.w, i0) >> 4) | ((byte_of(hdr.z, i0) >> 6) << 4);
+            sc1 = (byte_of(hdr.w, i1) & 0xF) | ((byte_of(hdr.y, i1) >> 6) << 4);
+            m1s = (byte_of(hdr.w, i1) >> 4) | ((byte_of(hdr.z, i1) >> 6) << 4);
+        }
+        const float d1 = d * (float)sc0, mm1 = dmin * (float)m0s;
+        const float d2 = d * (float)sc1, mm2 = dmin * (float)m1s;
+        const uint32_t R[4] = {raw.x, raw.y, raw.z, raw.w};
+        uint32_t lo[8], hi[8];  // 16 halves each, packed in pairs
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t wl = R[i] & 0x0F0F0F0Fu, wh = (R[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const _Float16 l0 = (_Float16)(d1 * (float)byte_of(wl, e) - mm1);
+                const _Float16 l1 = (_Float16)(d1 * (float)byte_of(wl, e + 1) - mm1);
+                const _Float16 h0 = (_Float16)(d2 * (float)byte_of(wh, e) - mm2);
+                const _Float16 h1 = (_Float16)(d2 * (float)byte_of(wh, e + 1) - mm2);
+                lo[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+                hi[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            }
+        }
+        uint8_t* B = stage + H_TILE;
+        // sub-block 2c -> k 0..31 (pieces 0..3), sub-block 2c+1 -> k 32..63 (pieces 4..7)
+        *(uint4*)(B + h_pos(brow, 2 * bhalf)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *(uint4*)(B + h_pos(brow, 2 * bhalf + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+        *(uint4*)(B + h_pos(brow, 4 + 2 * bhalf)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *(uint4*)(B + h_pos(brow, 4 + 2 * bhalf + 1)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
+
+    uint4 hdr = *(const uint4*)wrow;
+    uint4 raw = *(const uint4*)(wrow + 16 + 16 * bhalf);
+    issue_a(smem[0], 0);
+    dequant_b(smem[0], hdr, raw, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    for (int s = 0; s < nsteps; s++) {
+        const uint8_t* A = smem[s & 1];
+        const uint8_t* B = smem[s & 1] + H_TILE;
+        // operands of this step, LDS -> registers, before the next stage is queued
+        v8h av[2][4], bv[2][4];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+            const int row = wm * 64 + a * 32 + c32;
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) av[a][kk] = *(const v8h*)(A + h_pos(row, 2 * kk + h));
+        }
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int row = wn * 64 + b * 32 + c32;
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) bv[b][kk] = *(const v8h*)(B + h_pos(row, 2 * kk + h));
+        }
+        const bool more = s + 1 < nsteps;
+        if (more) {
+            issue_a(smem[(s + 1) & 1], s + 1);
+            const int sb = (s + 1) >> 2, c = (s + 1) & 3;
+            if (c == 0) hdr = *(const uint4*)(wrow + sb * Q4K_BYTES);
+            raw = *(const uint4*)(wrow + sb * Q4K_BYTES + 16 + 32 * c + 16 * bhalf);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[b][kk], acc[a][b], 0, 0, 0);
+        if (more) dequant_b(smem[(s + 1) & 1], hdr, raw, s + 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int col = n0 + wn * 64 + b * 32 + c32;
+            if (col >= n) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < m) Y[(int64_t)row * n + col] = acc[a][b][r];
+            }
+        }
+}
+
 // ------------------------------------------------------------ dispatch --
 
-size_t gemm_workspace_bytes(int type, int64_t k, int64_t m) {
-    if (type == T_Q4K) return prep_bytes(m, k);
+size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
+    if (type == T_Q4K) {
+        const size_t f16 = ((size_t)m * k * 2 + 255) & ~(size_t)255;
+        return mode == GEMM_INT8 ? prep_bytes(m, k) : f16;
+    }
     return matvec_workspace_bytes(type, k, 16);
 }
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                       void* qbuf, hipStream_t s) {
+                       void* qbuf, int mode, hipStream_t s) {
+    if (type == T_Q4K && mode != GEMM_INT8) {
+        _Float16* xh = (_Float16*)qbuf;
+        const int64_t nb = m * (k / 256);
+        hipLaunchKernelGGL(k_gemm_prep_f16, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, xh, (int)m, (int)k);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const unsigned grid = (unsigned)(((m + H_BM - 1) / H_BM) * ((n + H_BN - 1) / H_BN));
+        hipLaunchKernelGGL(k_gemm_q4k_f16, dim3(grid), dim3(H_THREADS), 0, s, (const uint8_t*)w, xh, y, (int)m,
+                           (int)n, (int)k);
+        return hipGetLastError();
+    }
     if (type == T_Q4K) {
         static bool attr_set = false;
         if (!attr_set) {

@@ -26,10 +26,12 @@ size_t matvec_workspace_bytes(int type, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, hipStream_t s);
 
-// gemm.hip: any m, int8 MFMA; qbuf is workspace for the quantized x
+// gemm.hip: m > 16 rows.  Q4_K on MFMA (mode: GEMM_F16 or GEMM_INT8), the
+// other types through decode tiles; qbuf is workspace for the prepared x.
+constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                       void* qbuf, hipStream_t s);
-size_t gemm_workspace_bytes(int type, int64_t k, int64_t m);
+                       void* qbuf, int mode, hipStream_t s);
+size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode);
 
 // moe.hip
 size_t moe_workspace_ints(int64_t n_experts, int64_t planes);

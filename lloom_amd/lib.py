@@ -47,6 +47,7 @@ def lib():
                 "lloom_hip_ctx_stream": ([vp], vp),
                 "lloom_hip_ctx_set_mv_rows_max": ([vp, i32], i32),
                 "lloom_hip_ctx_sync": ([vp], i32),
+                "lloom_hip_ctx_set_prefill_mma": ([vp, i32], i32),
                 "lloom_hip_alloc": ([vp, sz, ctypes.POINTER(vp)], i32),
                 "lloom_hip_free": ([vp, vp], i32),
                 "lloom_hip_memcpy_h2d": ([vp, vp, vp, sz, vp], i32),

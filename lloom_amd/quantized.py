@@ -87,6 +87,15 @@ def set_mv_rows_max(rows, device=0):
     check(lib().lloom_hip_ctx_set_mv_rows_max(_ctx(device), rows))
 
 
+MMA_F16, MMA_INT8 = 0, 1
+
+
+def set_prefill_mma(mode, device=0):
+    """Matrix-core family of the Q4_K prefill GEMM: MMA_INT8 (default, the
+    CPU arm's exact integer sums) or MMA_F16 (fp16 operands, opt-in)."""
+    check(lib().lloom_hip_ctx_set_prefill_mma(_ctx(device), mode))
+
+
 # ------------------------------------------------------------ QTensor ---
 
 def _padded_bytes(dtype, n_rows, k):

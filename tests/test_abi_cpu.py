@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol():
 
     L = lloom_amd.lib()
     names = declared_functions()
-    assert len(names) >= 18
+    assert len(names) >= 19
     for name in names:
         assert hasattr(L, name), name
     assert L.lloom_hip_version().startswith(b"lloom-hip")

@@ -138,16 +138,29 @@ def test_qmatmul_matches_oracle(L, dt, m):
         assert_rows_close(y, O.matmul(dt, x, q, n), what=f"dt={dt} m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(17, 1, 256), (64, 128, 2048), (100, 7, 768), (128, 300, 512),
-                                   (200, 129, 1024), (257, 64, 256), (512, 256, 2048)])
-def test_prefill_gemm_q4k_shapes(L, m, n, k):
-    """The int8-MFMA prefill GEMM on ragged tiles (m, n not multiples of 128)."""
+GEMM_SHAPES = [(17, 1, 256), (64, 128, 2048), (100, 7, 768), (128, 300, 512), (200, 129, 1024),
+               (257, 64, 256), (512, 256, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k,mma", [s + ("int8",) for s in GEMM_SHAPES] +
+                         [s + ("f16",) for s in GEMM_SHAPES if s[1] >= 128])
+def test_prefill_gemm_q4k_shapes(L, m, n, k, mma):
+    """Both prefill GEMMs on ragged tiles (m, n not multiples of 128).  The
+    fp16 one (opt-in) only on rows of >= 128 outputs: its operand rounding
+    is ~1e-4 of a typical output, inside the row-max bound for a wide row but
+    not for a row of a few outputs near zero."""
+    from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
+
     rng = np.random.default_rng(m * 7 + n)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[1, :256] = 0.0  # an all-zero activation block (d = 0, S = 0)
-    y, q = _qmm(L, O.Q4K, w, x)
-    assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"gemm m={m} n={n} k={k}")
+    set_prefill_mma(MMA_INT8 if mma == "int8" else MMA_F16)
+    try:
+        y, q = _qmm(L, O.Q4K, w, x)
+    finally:
+        set_prefill_mma(MMA_INT8)
+    assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"gemm {mma} m={m} n={n} k={k}")
 
 
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
