@@ -26,34 +26,34 @@ __device__ __forceinline__ uint32_t q8k_block_wave(float4 x, float* d, int* bsum
 #pragma unroll
     for (int j = 0; j < 4; j++) la = __builtin_fmaxf(la, __builtin_fabsf(xs[j]));
     const float amax = wave_max(la);
+    // The first element (lowest lane, then lowest j) with |x| == amax.  No
+    // branch anywhere: the two blocks a wave may quantize back to back then
+    // interleave, and the x loads stay ahead of the weight loads.
+    float mine = 0.0f;
+    bool hit = false;
+#pragma unroll
+    for (int j = 3; j >= 0; j--) {
+        const bool h = __builtin_fabsf(xs[j]) == amax;
+        mine = h ? xs[j] : mine;
+        hit = hit || h;
+    }
+    const unsigned long long ballot = __ballot(hit);
+    const int first = ballot ? __builtin_ctzll(ballot) : 0;
+    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
+    // amax == 0 (all zeros, or all NaN): iscale is +-inf or NaN, every
+    // product is NaN and converts to 0, and d is forced to +0 as the CPU's
+    // early return leaves it.
+    const float iscale = -127.0f / mx;
     uint32_t packed = 0;
     int s = 0;
-    if (amax == 0.0f) {
-        *d = 0.0f;
-    } else {
-        // the first element (lowest lane, then lowest j) with |x| == amax
-        float mine = 0.0f;
-        bool hit = false;
 #pragma unroll
-        for (int j = 3; j >= 0; j--)
-            if (__builtin_fabsf(xs[j]) == amax) {
-                mine = xs[j];
-                hit = true;
-            }
-        const unsigned long long ballot = __ballot(hit);
-        const int first = __builtin_ctzll(ballot);
-        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
-        const float iscale = -127.0f / mx;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float v = round_away(iscale * xs[j]);
-            v = v < -128.0f ? -128.0f : (v > 127.0f ? 127.0f : v);
-            const int q = sat_i8(v);
-            s += q;
-            packed |= ((uint32_t)q & 0xffu) << (8 * j);
-        }
-        *d = 1.0f / iscale;
+    for (int j = 0; j < 4; j++) {
+        const int q = clampi(nearest_int(iscale * xs[j]), -128, 127);
+        s += q;
+        packed |= ((uint32_t)q & 0xffu) << (8 * j);
     }
+    const float dd = 1.0f / iscale;
+    *d = amax == 0.0f ? 0.0f : dd;
     s += dppi<DPP_XOR1>(s);
     s += dppi<DPP_XOR2>(s);
     *bsum = s;
@@ -77,7 +77,7 @@ __device__ __forceinline__ uint32_t q8_0_block_8lanes(float4 x, uint16_t* d16) {
     uint32_t packed = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int q = sat_i8(round_away(xs[j] * id));
+        const int q = clampi(nearest_int(xs[j] * id), -128, 127);
         packed |= ((uint32_t)q & 0xffu) << (8 * j);
     }
     return packed;

@@ -25,9 +25,6 @@
 
 namespace lloom {
 
-constexpr int MV_WAVES = 4;
-constexpr int MV_THREADS = 64 * MV_WAVES;
-
 template <int TYPE>
 struct MvTraits;
 template <>
@@ -79,149 +76,206 @@ __device__ __forceinline__ uint32_t dw_sel(const uint4& v, uint32_t i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-template <int TYPE, int MB>
-__device__ __forceinline__ void compute_task(const TaskData& t, int p, int blk_local, int m, int KC,
-                                             const int8_t* __restrict__ lqs, const float* __restrict__ ld,
-                                             const int* __restrict__ lbs, int nbc, float* acc) {
+// A task's weights unpacked to int8 lanes and integer scales, once per row,
+// shared by every activation row.
+template <int TYPE>
+struct WPrep;
+template <>
+struct WPrep<T_Q4K> {
+    uint32_t lo[4], hi[4];
+    int sc0, sc1, m0, m1;
+    float d, dmin;
+};
+template <>
+struct WPrep<T_Q6K> {
+    uint32_t q[4][4];
+    int sc[4];
+    float d;
+};
+template <>
+struct WPrep<T_Q8_0> {
+    uint32_t w[8];
+    float d;
+};
+
+// The quantized activations of one task for one activation row.
+template <int TYPE>
+struct XTask;
+template <>
+struct XTask<T_Q4K> {
+    uint4 xl, xh;
+    int bs0, bs2;
+    float dy;
+};
+template <>
+struct XTask<T_Q6K> {
+    uint4 xv[4];
+    int bs[4];
+    float dy;
+};
+template <>
+struct XTask<T_Q8_0> {
+    uint4 x0, x1;
+    float dy;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void prep_task(const TaskData& t, int p, WPrep<TYPE>& w) {
     if constexpr (TYPE == T_Q4K) {
-        const float d = f16_to_f32(t.s.x & 0xffffu);
-        const float dmin = f16_to_f32(t.s.x >> 16);
-        const int j = p >> 1, half = p & 1;
-        // get_scale_min_k4 (utils.rs:50-60) for sub-blocks 2j and 2j+1
-        int sc0, m0, sc1, m1;
-        if (j < 2) {
-            sc0 = byte_of(t.s.y, 2 * j) & 63;
-            m0 = byte_of(t.s.z, 2 * j) & 63;
-            sc1 = byte_of(t.s.y, 2 * j + 1) & 63;
-            m1 = byte_of(t.s.z, 2 * j + 1) & 63;
-        } else {
-            uint32_t i0 = 2 * j - 4, i1 = 2 * j - 3;
-            sc0 = (byte_of(t.s.w, i0) & 0xF) | ((byte_of(t.s.y, i0) >> 6) << 4);
-            m0 = (byte_of(t.s.w, i0) >> 4) | ((byte_of(t.s.z, i0) >> 6) << 4);
-            sc1 = (byte_of(t.s.w, i1) & 0xF) | ((byte_of(t.s.y, i1) >> 6) << 4);
-            m1 = (byte_of(t.s.w, i1) >> 4) | ((byte_of(t.s.z, i1) >> 6) << 4);
-        }
-        const uint32_t lo0 = t.a.x & 0x0F0F0F0Fu, lo1 = t.a.y & 0x0F0F0F0Fu, lo2 = t.a.z & 0x0F0F0F0Fu,
-                       lo3 = t.a.w & 0x0F0F0F0Fu;
-        const uint32_t hi0 = (t.a.x >> 4) & 0x0F0F0F0Fu, hi1 = (t.a.y >> 4) & 0x0F0F0F0Fu,
-                       hi2 = (t.a.z >> 4) & 0x0F0F0F0Fu, hi3 = (t.a.w >> 4) & 0x0F0F0F0Fu;
-        const int eoff = blk_local * 256 + 64 * j + 16 * half;
+        w.d = f16_to_f32(t.s.x & 0xffffu);
+        w.dmin = f16_to_f32(t.s.x >> 16);
+        const int j = p >> 1;
+        // get_scale_min_k4 (utils.rs:50-60) for sub-blocks 2j and 2j+1: the
+        // eight 6-bit scales (and mins) assembled one byte each into a
+        // 64-bit word, then one shift by 16j picks the pair.  j varies
+        // across the wave, and a select on it is compiled into a branch.
+        const uint64_t sc8 = (uint64_t)(t.s.y & 0x3F3F3F3Fu) |
+                             ((uint64_t)((t.s.w & 0x0F0F0F0Fu) | ((t.s.y >> 2) & 0x30303030u)) << 32);
+        const uint64_t m8 = (uint64_t)(t.s.z & 0x3F3F3F3Fu) |
+                            ((uint64_t)(((t.s.w >> 4) & 0x0F0F0F0Fu) | ((t.s.z >> 2) & 0x30303030u)) << 32);
+        const uint32_t scp = (uint32_t)(sc8 >> (16 * j)), mp = (uint32_t)(m8 >> (16 * j));
+        w.sc0 = (int)(scp & 0xffu);
+        w.sc1 = (int)((scp >> 8) & 0xffu);
+        w.m0 = (int)(mp & 0xffu);
+        w.m1 = (int)((mp >> 8) & 0xffu);
+        const uint32_t A[4] = {t.a.x, t.a.y, t.a.z, t.a.w};
 #pragma unroll
-        for (int mi = 0; mi < MB; mi++) {
-            if (mi < m) {
-                const int8_t* xq = lqs + mi * KC + eoff;
-                uint4 xl = *(const uint4*)xq;
-                uint4 xh = *(const uint4*)(xq + 32);
-                int sl = dot4(lo0, xl.x, 0);
-                sl = dot4(lo1, xl.y, sl);
-                sl = dot4(lo2, xl.z, sl);
-                sl = dot4(lo3, xl.w, sl);
-                int sh = dot4(hi0, xh.x, 0);
-                sh = dot4(hi1, xh.y, sh);
-                sh = dot4(hi2, xh.z, sh);
-                sh = dot4(hi3, xh.w, sh);
-                const int* bs = lbs + (mi * nbc + blk_local) * 16 + 4 * j + half;
-                int S = sc0 * sl + sc1 * sh;
-                int Mn = m0 * bs[0] + m1 * bs[2];
-                float dy = ld[mi * nbc + blk_local];
-                acc[mi] += dy * ((float)S * d - (float)Mn * dmin);
-            }
+        for (int i = 0; i < 4; i++) {
+            w.lo[i] = A[i] & 0x0F0F0F0Fu;
+            w.hi[i] = (A[i] >> 4) & 0x0F0F0F0Fu;
         }
     } else if constexpr (TYPE == T_Q6K) {
-        const float d = f16_to_f32(t.e);
+        w.d = f16_to_f32(t.e);
         const int h = p >> 1, odd = p & 1;
         // q6 bytes of the 4 groups g (elements 128h + 32g + 16*odd + 0..15)
-        uint32_t q[4][4];
         const uint32_t A[4] = {t.a.x, t.a.y, t.a.z, t.a.w};
         const uint32_t B[4] = {t.b.x, t.b.y, t.b.z, t.b.w};
         const uint32_t C[4] = {t.c.x, t.c.y, t.c.z, t.c.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            q[0][i] = (A[i] & 0x0F0F0F0Fu) | ((C[i] & 0x03030303u) << 4);
-            q[1][i] = (B[i] & 0x0F0F0F0Fu) | (((C[i] >> 2) & 0x03030303u) << 4);
-            q[2][i] = ((A[i] >> 4) & 0x0F0F0F0Fu) | (((C[i] >> 4) & 0x03030303u) << 4);
-            q[3][i] = ((B[i] >> 4) & 0x0F0F0F0Fu) | (((C[i] >> 6) & 0x03030303u) << 4);
+            w.q[0][i] = (A[i] & 0x0F0F0F0Fu) | ((C[i] & 0x03030303u) << 4);
+            w.q[1][i] = (B[i] & 0x0F0F0F0Fu) | (((C[i] >> 2) & 0x03030303u) << 4);
+            w.q[2][i] = ((A[i] >> 4) & 0x0F0F0F0Fu) | (((C[i] >> 4) & 0x03030303u) << 4);
+            w.q[3][i] = ((B[i] >> 4) & 0x0F0F0F0Fu) | (((C[i] >> 6) & 0x03030303u) << 4);
         }
         // scales[8h + 2g + odd]: dword 2h (g < 2) or 2h + 1, byte (2g + odd) & 3
-        int sc[4];
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            uint32_t w = dw_sel(t.s, 2 * h + (g >> 1));
-            sc[g] = (int)(int8_t)byte_of(w, (2 * g + odd) & 3);
-        }
-#pragma unroll
-        for (int mi = 0; mi < MB; mi++) {
-            if (mi < m) {
-                int tot = 0;
-                const int8_t* xb = lqs + mi * KC + blk_local * 256 + 128 * h + 16 * odd;
-                const int* bs = lbs + (mi * nbc + blk_local) * 16 + 8 * h + odd;
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    uint4 xv = *(const uint4*)(xb + 32 * g);
-                    int s = dot4(q[g][0], xv.x, 0);
-                    s = dot4(q[g][1], xv.y, s);
-                    s = dot4(q[g][2], xv.z, s);
-                    s = dot4(q[g][3], xv.w, s);
-                    tot += sc[g] * (s - 32 * bs[2 * g]);
-                }
-                float dy = ld[mi * nbc + blk_local];
-                acc[mi] += (d * dy) * (float)tot;
-            }
+            uint32_t wd = dw_sel(t.s, 2 * h + (g >> 1));
+            w.sc[g] = (int)(int8_t)byte_of(wd, (2 * g + odd) & 3);
         }
     } else {
         const uint32_t s = t.c.x;
-        const float dx = f16_to_f32(s == 0 ? (t.a.x & 0xffffu) : (t.a.x >> 16));
+        w.d = f16_to_f32(s == 0 ? (t.a.x & 0xffffu) : (t.a.x >> 16));
         const uint32_t W[9] = {t.a.x, t.a.y, t.a.z, t.a.w, t.b.x, t.b.y, t.b.z, t.b.w, t.e};
-        uint32_t w[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = s == 0 ? __builtin_amdgcn_alignbyte(W[i + 1], W[i], 2) : W[i + 1];
+        for (int i = 0; i < 8; i++) w.w[i] = s == 0 ? __builtin_amdgcn_alignbyte(W[i + 1], W[i], 2) : W[i + 1];
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void load_x(int p, int blk_local, int mi, int KC, int nbc, const int8_t* __restrict__ lqs,
+                                       const float* __restrict__ ld, const int* __restrict__ lbs, XTask<TYPE>& x) {
+    if constexpr (TYPE == T_Q4K) {
+        const int j = p >> 1, half = p & 1;
+        const int8_t* xq = lqs + mi * KC + blk_local * 256 + 64 * j + 16 * half;
+        x.xl = *(const uint4*)xq;
+        x.xh = *(const uint4*)(xq + 32);
+        const int* bs = lbs + (mi * nbc + blk_local) * 16 + 4 * j + half;
+        x.bs0 = bs[0];
+        x.bs2 = bs[2];
+        x.dy = ld[mi * nbc + blk_local];
+    } else if constexpr (TYPE == T_Q6K) {
+        const int h = p >> 1, odd = p & 1;
+        const int8_t* xb = lqs + mi * KC + blk_local * 256 + 128 * h + 16 * odd;
+        const int* bs = lbs + (mi * nbc + blk_local) * 16 + 8 * h + odd;
 #pragma unroll
-        for (int mi = 0; mi < MB; mi++) {
-            if (mi < m) {
-                const int8_t* xb = lqs + mi * KC + blk_local * 32;
-                uint4 x0 = *(const uint4*)xb;
-                uint4 x1 = *(const uint4*)(xb + 16);
-                int sum = dot4(w[0], x0.x, 0);
-                sum = dot4(w[1], x0.y, sum);
-                sum = dot4(w[2], x0.z, sum);
-                sum = dot4(w[3], x0.w, sum);
-                sum = dot4(w[4], x1.x, sum);
-                sum = dot4(w[5], x1.y, sum);
-                sum = dot4(w[6], x1.z, sum);
-                sum = dot4(w[7], x1.w, sum);
-                acc[mi] += (float)sum * (dx * ld[mi * nbc + blk_local]);
-            }
+        for (int g = 0; g < 4; g++) {
+            x.xv[g] = *(const uint4*)(xb + 32 * g);
+            x.bs[g] = bs[2 * g];
         }
+        x.dy = ld[mi * nbc + blk_local];
+    } else {
+        const int8_t* xb = lqs + mi * KC + blk_local * 32;
+        x.x0 = *(const uint4*)xb;
+        x.x1 = *(const uint4*)(xb + 16);
+        x.dy = ld[mi * nbc + blk_local];
+    }
+}
+
+// One task's contribution: the exact integer block sums, then the f32
+// scales in the CPU's order (k_quants.rs vec_dot).
+template <int TYPE>
+__device__ __forceinline__ float task_dot(const WPrep<TYPE>& w, const XTask<TYPE>& x) {
+    if constexpr (TYPE == T_Q4K) {
+        int sl = dot4(w.lo[0], x.xl.x, 0);
+        sl = dot4(w.lo[1], x.xl.y, sl);
+        sl = dot4(w.lo[2], x.xl.z, sl);
+        sl = dot4(w.lo[3], x.xl.w, sl);
+        int sh = dot4(w.hi[0], x.xh.x, 0);
+        sh = dot4(w.hi[1], x.xh.y, sh);
+        sh = dot4(w.hi[2], x.xh.z, sh);
+        sh = dot4(w.hi[3], x.xh.w, sh);
+        const int S = w.sc0 * sl + w.sc1 * sh;
+        const int Mn = w.m0 * x.bs0 + w.m1 * x.bs2;
+        return x.dy * ((float)S * w.d - (float)Mn * w.dmin);
+    } else if constexpr (TYPE == T_Q6K) {
+        int tot = 0;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int s = dot4(w.q[g][0], x.xv[g].x, 0);
+            s = dot4(w.q[g][1], x.xv[g].y, s);
+            s = dot4(w.q[g][2], x.xv[g].z, s);
+            s = dot4(w.q[g][3], x.xv[g].w, s);
+            tot += w.sc[g] * (s - 32 * x.bs[g]);
+        }
+        return (w.d * x.dy) * (float)tot;
+    } else {
+        int sum = dot4(w.w[0], x.x0.x, 0);
+        sum = dot4(w.w[1], x.x0.y, sum);
+        sum = dot4(w.w[2], x.x0.z, sum);
+        sum = dot4(w.w[3], x.x0.w, sum);
+        sum = dot4(w.w[4], x.x1.x, sum);
+        sum = dot4(w.w[5], x.x1.y, sum);
+        sum = dot4(w.w[6], x.x1.z, sum);
+        sum = dot4(w.w[7], x.x1.w, sum);
+        return (float)sum * (w.d * x.dy);
     }
 }
 
 // Activation prologue, split in two so the x loads are issued before the
 // weight loads (vmcnt retires loads in order: waiting for x must not mean
-// waiting for the weights).  A wave quantizes up to XN blocks per chunk
-// (XN <= XQ); the loads are unconditional (a block past the end reloads
+// waiting for the weights).  Each of the WV waves quantizes up to XN blocks
+// per chunk; the loads are unconditional (a block past the end reloads
 // block 0) so no load sits under a branch.
 constexpr int XQ = 8;
 
-template <int VT, int XN>
+// v / nbc for the block index v < 2^16 by a multiply-high: mg = ceil(2^32 /
+// nbc) (exact while v * nbc < 2^32), or 0 for nbc = 1.  A runtime integer
+// divide would sit in front of the first x load.
+static uint32_t nbc_magic(int nbc) { return nbc <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + nbc - 1) / nbc); }
+__device__ __forceinline__ int div_nbc(int v, uint32_t mg) { return mg ? (int)__umulhi((uint32_t)v, mg) : v; }
+
+template <int VT, int WV, int XN>
 __device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int64_t K, int kc0, int KC, int m,
-                                           float4 (&xv)[XN]) {
+                                           uint32_t mg, float4 (&xv)[XN]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if constexpr (VT == T_Q8K) {
         const int nbc = KC / 256, total = m * nbc;
 #pragma unroll
         for (int i = 0; i < XN; i++) {
-            const int b = wave + MV_WAVES * i;
+            const int b = wave + WV * i;
             const int bb = b < total ? b : 0;
-            const int mi = bb / nbc, sb = bb - mi * nbc;
+            const int mi = div_nbc(bb, mg), sb = bb - mi * nbc;
             xv[i] = *(const float4*)(x + mi * K + kc0 + sb * 256 + 4 * lane);
         }
     } else {
         const int nbc = KC / 32, total = m * nbc;
 #pragma unroll
         for (int i = 0; i < XN; i++) {
-            const int b = wave * 8 + 8 * MV_WAVES * i + (lane >> 3);
+            const int b = wave * 8 + 8 * WV * i + (lane >> 3);
             const int bb = b < total ? b : 0;
-            const int mi = bb / nbc, bl = bb - mi * nbc;
+            const int mi = div_nbc(bb, mg), bl = bb - mi * nbc;
             xv[i] = *(const float4*)(x + mi * K + kc0 + bl * 32 + 4 * (lane & 7));
         }
     }
@@ -229,20 +283,23 @@ __device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int64_t 
 
 // Quantize the prefetched blocks (every block exactly as from_float) into
 // LDS: qs [m][KC], d [m][KC / block], Q8_K bsums [m][KC / 16].
-template <int VT, int XN>
-__device__ __forceinline__ void quantize_lds(const float4 (&xv)[XN], int KC, int m, int8_t* lqs, float* ld,
-                                             int* lbs) {
+template <int VT, int WV, int XN>
+__device__ __forceinline__ void quantize_lds(const float4 (&xv)[XN], int KC, int m, uint32_t mg, int8_t* lqs,
+                                             float* ld, int* lbs) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if constexpr (VT == T_Q8K) {
         const int nbc = KC / 256, total = m * nbc;
 #pragma unroll
         for (int i = 0; i < XN; i++) {
-            const int b = wave + MV_WAVES * i;
+            const int b = wave + WV * i;
+            // computed unconditionally (a block past the end is a copy of
+            // block 0), stored only if real: the x loads are then used on
+            // every path and cannot sink below the weight loads
+            float d;
+            int bs;
+            const uint32_t q = q8k_block_wave(xv[i], &d, &bs);
             if (b < total) {  // wave-uniform
-                const int mi = b / nbc, sb = b - mi * nbc;
-                float d;
-                int bs;
-                const uint32_t q = q8k_block_wave(xv[i], &d, &bs);
+                const int mi = div_nbc(b, mg), sb = b - mi * nbc;
                 *(uint32_t*)(lqs + mi * KC + sb * 256 + 4 * lane) = q;
                 if ((lane & 3) == 0) lbs[b * 16 + (lane >> 2)] = bs;
                 if (lane == 0) ld[b] = d;
@@ -252,33 +309,37 @@ __device__ __forceinline__ void quantize_lds(const float4 (&xv)[XN], int KC, int
         const int nbc = KC / 32, total = m * nbc;
 #pragma unroll
         for (int i = 0; i < XN; i++) {
-            const int b0 = wave * 8 + 8 * MV_WAVES * i;
-            if (b0 < total) {  // wave-uniform; the 8-lane groups stay whole
-                const int b = b0 + (lane >> 3), sub = lane & 7;
-                uint16_t d16;
-                const uint32_t q = q8_0_block_8lanes(xv[i], &d16);
-                if (b < total) {
-                    const int mi = b / nbc, bl = b - mi * nbc;
-                    *(uint32_t*)(lqs + mi * KC + bl * 32 + 4 * sub) = q;
-                    if (sub == 0) ld[b] = f16_to_f32(d16);
-                }
+            const int b = wave * 8 + 8 * WV * i + (lane >> 3), sub = lane & 7;
+            uint16_t d16;
+            const uint32_t q = q8_0_block_8lanes(xv[i], &d16);  // unconditional, as above
+            if (b < total) {
+                const int mi = div_nbc(b, mg), bl = b - mi * nbc;
+                *(uint32_t*)(lqs + mi * KC + bl * 32 + 4 * sub) = q;
+                if (sub == 0) ld[b] = f16_to_f32(d16);
             }
         }
     }
 }
 
-template <int TYPE, int MB, int R, int XN>
-__global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                        float* __restrict__ Y, int n, int K, int m, int KC) {
+// WV waves of R weight rows each; MB >= m activation rows; XN x blocks
+// quantized per wave per chunk of KC elements of K.
+template <int TYPE, int MB, int R, int WV, int XN>
+__global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                     float* __restrict__ Y, int n, int K, int m, int KC,
+                                                     uint32_t mg) {
     using Tr = MvTraits<TYPE>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * MV_WAVES + wave) * R;
+    const int row0 = (blockIdx.x * WV + wave) * R;
     const int64_t rowbytes = (int64_t)(K / Tr::BE) * Tr::BB;
     const int nbc = KC / Tr::BE;
     int8_t* lqs = (int8_t*)smem;
     float* ld = (float*)(smem + m * KC);
     int* lbs = (int*)(ld + m * nbc);
+    // rows past n load row n-1 and are never stored
+    const uint8_t* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) wrow[r] = W + min(row0 + r, n - 1) * rowbytes;
 
     float acc[R][MB];
 #pragma unroll
@@ -286,36 +347,51 @@ __global__ __launch_bounds__(MV_THREADS) void k_matvec(const uint8_t* __restrict
 #pragma unroll
         for (int mi = 0; mi < MB; mi++) acc[r][mi] = 0.0f;
 
+    // activation rows whose task registers are loaded ahead of the weights
+    constexpr int XPRE = MB <= 4 ? MB : 1;
     const int T = nbc * Tr::P;  // tasks per row per chunk
     for (int kc0 = 0; kc0 < K; kc0 += KC) {
         const int blk0 = kc0 / Tr::BE;
         if (kc0) __syncthreads();  // the previous chunk's readers are done with LDS
         float4 xv[XN];
-        prefetch_x<Tr::VT, XN>(X, K, kc0, KC, m, xv);
-        // first round of weight loads; rows past n and tasks past T load a
-        // valid block (row n-1, task 0) and are never accumulated
+        prefetch_x<Tr::VT, WV, XN>(X, K, kc0, KC, m, mg, xv);
+        // first round of weight loads (tasks past T load task 0, unused)
         TaskData td[R];
         int ti = lane;
-        const int t0 = ti < T ? ti : 0;
+        {
+            const int t0 = ti < T ? ti : 0;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = min(row0 + r, n - 1);
-            load_task<TYPE>(W + row * rowbytes, blk0 + t0 / Tr::P, t0 % Tr::P, td[r]);
+            for (int r = 0; r < R; r++) load_task<TYPE>(wrow[r], blk0 + t0 / Tr::P, t0 % Tr::P, td[r]);
         }
-        quantize_lds<Tr::VT, XN>(xv, KC, m, lqs, ld, lbs);
+        // every load above is issued before the quantization starts: the
+        // scheduler would otherwise interleave them with the x math and
+        // issue the last weight loads only after x has arrived
+        __builtin_amdgcn_sched_barrier(0);
+        quantize_lds<Tr::VT, WV, XN>(xv, KC, m, mg, lqs, ld, lbs);
         __syncthreads();
         for (; ti < T; ti += 64) {
             if (ti != lane) {
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    const int row = min(row0 + r, n - 1);
-                    load_task<TYPE>(W + row * rowbytes, blk0 + ti / Tr::P, ti % Tr::P, td[r]);
+                for (int r = 0; r < R; r++) load_task<TYPE>(wrow[r], blk0 + ti / Tr::P, ti % Tr::P, td[r]);
+            }
+            const int p = ti % Tr::P, bl = ti / Tr::P;
+            // LDS reads first: their latency hides under the weight loads
+            XTask<TYPE> xp[XPRE];
+#pragma unroll
+            for (int mi = 0; mi < XPRE; mi++) load_x<TYPE>(p, bl, mi < m ? mi : 0, KC, nbc, lqs, ld, lbs, xp[mi]);
+            WPrep<TYPE> wp[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) prep_task<TYPE>(td[r], p, wp[r]);
+#pragma unroll
+            for (int mi = 0; mi < MB; mi++) {
+                if (mi < m) {
+                    XTask<TYPE> xt;
+                    if (mi < XPRE) xt = xp[mi];
+                    else load_x<TYPE>(p, bl, mi, KC, nbc, lqs, ld, lbs, xt);
+#pragma unroll
+                    for (int r = 0; r < R; r++) acc[r][mi] += task_dot<TYPE>(wp[r], xt);
                 }
             }
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (row0 + r < n)
-                    compute_task<TYPE, MB>(td[r], ti % Tr::P, ti / Tr::P, m, KC, lqs, ld, lbs, nbc, acc[r]);
         }
     }
 #pragma unroll
@@ -454,10 +530,10 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma_q4k(const uint8_t* __restri
 }
 
 // Chunk of K staged in LDS at a time: the prologue quantizes at most
-// XQ blocks per wave, m * KC <= XQ * MV_WAVES * 256 elements.
-static int pick_kc(int type, int64_t K, int m) {
+// XQ blocks per wave, m * KC <= XQ * WV * 256 elements.
+static int pick_kc(int type, int64_t K, int m, int wv) {
     const int be = type == T_Q8_0 ? 32 : 256;
-    int64_t kc = (int64_t)XQ * MV_WAVES * 256 / m;
+    int64_t kc = (int64_t)XQ * wv * 256 / m;
     kc -= kc % be;
     if (kc < be) kc = be;
     if (kc >= K) return (int)K;
@@ -472,35 +548,42 @@ static size_t lds_bytes(int type, int KC, int m) {
     return b;
 }
 
-template <int TYPE, int MB, int XN>
-static void launch_xn(const void* w, const float* x, float* y, int n, int K, int m, int KC, hipStream_t s) {
-    constexpr int R = 2;
+template <int TYPE, int MB, int WV, int R>
+static hipError_t launch_cfg(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
+    const int KC = pick_kc(TYPE, K, m, WV);
+    // blocks a wave quantizes per chunk: 256 elements (Q8_K) or 8 lanes x 32 (Q8_0) per step
+    const int per_step = TYPE == T_Q8_0 ? 32 * 8 * WV : 256 * WV;
+    const int steps = (m * KC + per_step - 1) / per_step;
     const size_t shm = lds_bytes(TYPE, KC, m);
-    const dim3 grid((n + MV_WAVES * R - 1) / (MV_WAVES * R));
-    hipLaunchKernelGGL((k_matvec<TYPE, MB, R, XN>), grid, dim3(MV_THREADS), shm, s, (const uint8_t*)w, x, y, n, K,
-                       m, KC);
+    const dim3 grid((n + WV * R - 1) / (WV * R)), block(64 * WV);
+    const uint8_t* wb = (const uint8_t*)w;
+    const uint32_t mg = nbc_magic(KC / (TYPE == T_Q8_0 ? 32 : 256));
+    if (steps <= 1) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 1>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
+    else if (steps <= 2) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 2>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
+    else if (steps <= 4) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 4>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
+    else hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 8>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
+    return hipGetLastError();
 }
 
+// One or two activation rows: 8 waves per workgroup, each wave R rows, R
+// chosen so the grid is about one workgroup per CU (each workgroup
+// quantizes x once; fewer, fuller workgroups quantize it fewer times).
 template <int TYPE, int MB>
-static hipError_t launch_mb(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
-    const int KC = pick_kc(TYPE, K, m);
-    // blocks a wave quantizes per chunk: 256 elements (Q8_K) or 8 lanes x 32 (Q8_0) per step
-    const int per_step = TYPE == T_Q8_0 ? 32 * 8 * MV_WAVES : 256 * MV_WAVES;
-    const int steps = (m * KC + per_step - 1) / per_step;
-    if (steps <= 1) launch_xn<TYPE, MB, 1>(w, x, y, n, K, m, KC, s);
-    else if (steps <= 2) launch_xn<TYPE, MB, 2>(w, x, y, n, K, m, KC, s);
-    else if (steps <= 4) launch_xn<TYPE, MB, 4>(w, x, y, n, K, m, KC, s);
-    else launch_xn<TYPE, MB, 8>(w, x, y, n, K, m, KC, s);
-    return hipGetLastError();
+static hipError_t launch_small(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
+    const int r = (n + 8 * 256 - 1) / (8 * 256);
+    if (r <= 1) return launch_cfg<TYPE, MB, 8, 1>(w, x, y, n, K, m, s);
+    if (r <= 2) return launch_cfg<TYPE, MB, 8, 2>(w, x, y, n, K, m, s);
+    if (r <= 3) return launch_cfg<TYPE, MB, 8, 3>(w, x, y, n, K, m, s);
+    return launch_cfg<TYPE, MB, 8, 4>(w, x, y, n, K, m, s);
 }
 
 template <int TYPE>
 static hipError_t launch_type(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
-    if (m <= 1) return launch_mb<TYPE, 1>(w, x, y, n, K, m, s);
-    if (m <= 2) return launch_mb<TYPE, 2>(w, x, y, n, K, m, s);
-    if (m <= 4) return launch_mb<TYPE, 4>(w, x, y, n, K, m, s);
-    if (m <= 8) return launch_mb<TYPE, 8>(w, x, y, n, K, m, s);
-    return launch_mb<TYPE, 16>(w, x, y, n, K, m, s);
+    if (m <= 1) return launch_small<TYPE, 1>(w, x, y, n, K, m, s);
+    if (m <= 2) return launch_small<TYPE, 2>(w, x, y, n, K, m, s);
+    if (m <= 4) return launch_cfg<TYPE, 4, 4, 2>(w, x, y, n, K, m, s);
+    if (m <= 8) return launch_cfg<TYPE, 8, 4, 2>(w, x, y, n, K, m, s);
+    return launch_cfg<TYPE, 16, 4, 2>(w, x, y, n, K, m, s);
 }
 
 size_t matvec_workspace_bytes(int type, int64_t k, int64_t m) {
