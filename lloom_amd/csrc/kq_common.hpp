@@ -156,6 +156,42 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += dpp<DPP_ROW_MIRROR>(v);
     return v;
 }
+// V <= 8 independent full-wave sums in one butterfly: the xor-32, xor-16
+// and xor-8 exchanges each merge two values into one (a lane sends the
+// value its partner keeps and adds what it receives), then one value per
+// lane goes through the 8-lane sum.  Item i ends up in the 8 lanes l with
+// 4 * ((l >> 3) & 1) + 2 * ((l >> 4) & 1) + (l >> 5) == i; items past V
+// read as 0.  (The exchanges a value takes do not depend on V, so an item's
+// sum is the same whatever V is.)
+constexpr int DPP_ROW_ROR8 = 0x128;  // lane i <- lane i ^ 8 within 16
+template <int V>
+__device__ __forceinline__ float wave_sum_items(const float (&v)[V]) {
+    static_assert(V >= 1 && V <= 8, "wave_sum_items merges at most eight sums");
+    const bool up32 = __lane_id() >= 32, up16 = (__lane_id() >> 4) & 1, up8 = (__lane_id() >> 3) & 1;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        if (2 * p < V) {
+            const float x = v[2 * p], y = 2 * p + 1 < V ? v[2 * p + 1] : 0.0f;
+            a[p] = (up32 ? y : x) + partner32(up32 ? x : y);
+        }
+    }
+    float b[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        if (4 * q < V) b[q] = (up16 ? a[2 * q + 1] : a[2 * q]) + partner16(up16 ? a[2 * q] : a[2 * q + 1]);
+    }
+    float c = b[0];
+    if constexpr (V > 4) c = (up8 ? b[1] : b[0]) + dpp<DPP_ROW_ROR8>(up8 ? b[0] : b[1]);
+    else c += dpp<DPP_ROW_ROR8>(c);
+    c += dpp<DPP_XOR1>(c);
+    c += dpp<DPP_XOR2>(c);
+    return c + dpp<DPP_HALF_MIRROR>(c);
+}
+__device__ __forceinline__ int wave_sum_item_of_lane() {
+    const int l = __lane_id();
+    return 4 * ((l >> 3) & 1) + 2 * ((l >> 4) & 1) + (l >> 5);
+}
 // Full-wave (wave64) sum, the result in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
     v = row16_sum(v);

@@ -216,8 +216,9 @@ __device__ __forceinline__ float task_dot(const WPrep<TYPE>& w, const XTask<TYPE
         sh = dot4(w.hi[1], x.xh.y, sh);
         sh = dot4(w.hi[2], x.xh.z, sh);
         sh = dot4(w.hi[3], x.xh.w, sh);
-        const int S = w.sc0 * sl + w.sc1 * sh;
-        const int Mn = w.m0 * x.bs0 + w.m1 * x.bs2;
+        // |sl|, |sh| <= 16*15*128 and |bsum| <= 16*128: 24-bit multiplies
+        const int S = __mul24(w.sc0, sl) + __mul24(w.sc1, sh);
+        const int Mn = __mul24(w.m0, x.bs0) + __mul24(w.m1, x.bs2);
         return x.dy * ((float)S * w.d - (float)Mn * w.dmin);
     } else if constexpr (TYPE == T_Q6K) {
         int tot = 0;
@@ -227,7 +228,7 @@ __device__ __forceinline__ float task_dot(const WPrep<TYPE>& w, const XTask<TYPE
             s = dot4(w.q[g][1], x.xv[g].y, s);
             s = dot4(w.q[g][2], x.xv[g].z, s);
             s = dot4(w.q[g][3], x.xv[g].w, s);
-            tot += w.sc[g] * (s - 32 * x.bs[g]);
+            tot += __mul24(w.sc[g], s - 32 * x.bs[g]);  // |s - 32 bs| < 2^18
         }
         return (w.d * x.dy) * (float)tot;
     } else {
@@ -347,8 +348,6 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
 #pragma unroll
         for (int mi = 0; mi < MB; mi++) acc[r][mi] = 0.0f;
 
-    // activation rows whose task registers are loaded ahead of the weights
-    constexpr int XPRE = MB <= 4 ? MB : 1;
     const int T = nbc * Tr::P;  // tasks per row per chunk
     for (int kc0 = 0; kc0 < K; kc0 += KC) {
         const int blk0 = kc0 / Tr::BE;
@@ -368,40 +367,53 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         // issue the last weight loads only after x has arrived
         __builtin_amdgcn_sched_barrier(0);
         quantize_lds<Tr::VT, WV, XN>(xv, KC, m, mg, lqs, ld, lbs);
+        // unpack the first round of weights while the other waves finish
+        // their share of the quantization
+        WPrep<TYPE> wp[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) prep_task<TYPE>(td[r], ti % Tr::P, wp[r]);
         __syncthreads();
         for (; ti < T; ti += 64) {
+            const int p = ti % Tr::P, bl = ti / Tr::P;
             if (ti != lane) {
 #pragma unroll
-                for (int r = 0; r < R; r++) load_task<TYPE>(wrow[r], blk0 + ti / Tr::P, ti % Tr::P, td[r]);
+                for (int r = 0; r < R; r++) {
+                    load_task<TYPE>(wrow[r], blk0 + bl, p, td[r]);
+                    prep_task<TYPE>(td[r], p, wp[r]);
+                }
             }
-            const int p = ti % Tr::P, bl = ti / Tr::P;
-            // LDS reads first: their latency hides under the weight loads
-            XTask<TYPE> xp[XPRE];
-#pragma unroll
-            for (int mi = 0; mi < XPRE; mi++) load_x<TYPE>(p, bl, mi < m ? mi : 0, KC, nbc, lqs, ld, lbs, xp[mi]);
-            WPrep<TYPE> wp[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) prep_task<TYPE>(td[r], p, wp[r]);
 #pragma unroll
             for (int mi = 0; mi < MB; mi++) {
                 if (mi < m) {
                     XTask<TYPE> xt;
-                    if (mi < XPRE) xt = xp[mi];
-                    else load_x<TYPE>(p, bl, mi, KC, nbc, lqs, ld, lbs, xt);
+                    load_x<TYPE>(p, bl, mi, KC, nbc, lqs, ld, lbs, xt);
 #pragma unroll
                     for (int r = 0; r < R; r++) acc[r][mi] += task_dot<TYPE>(wp[r], xt);
                 }
             }
         }
     }
+    if constexpr (R * MB <= 8) {
+        // all R * MB sums in one butterfly (item = r * MB + mi)
+        float v[R * MB];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int row = row0 + r;
+        for (int r = 0; r < R; r++)
 #pragma unroll
-        for (int mi = 0; mi < MB; mi++) {
-            if (mi < m) {
-                const float v = wave_sum(acc[r][mi]);
-                if (lane == 0 && row < n) Y[(int64_t)mi * n + row] = v;
+            for (int mi = 0; mi < MB; mi++) v[r * MB + mi] = acc[r][mi];
+        const float tot = wave_sum_items<R * MB>(v);
+        const int item = wave_sum_item_of_lane();
+        const int r = item / MB, mi = item % MB;
+        if ((lane & 7) == 0 && item < R * MB && mi < m && row0 + r < n) Y[(int64_t)mi * n + row0 + r] = tot;
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = row0 + r;
+#pragma unroll
+            for (int mi = 0; mi < MB; mi++) {
+                if (mi < m) {
+                    const float v = wave_sum(acc[r][mi]);
+                    if (lane == 0 && row < n) Y[(int64_t)mi * n + row] = v;
+                }
             }
         }
     }

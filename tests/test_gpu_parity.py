@@ -182,15 +182,17 @@ def test_decode_rows_batch_invariant(L, dt):
     quantized_tests.rs:239-275, exact on the CPU arm).  Q4_K with 3..16 rows
     runs the MFMA kernel, 1..2 the dot4 kernel: each group is checked
     against its own full batch (across the two kernels only the tolerance
-    holds, as on the reference's CUDA and Metal arms).  Q8_0 / Q6_K keep one
-    K-chunk (so one task set per lane) up to 4 rows at k = 1024."""
+    holds, as on the reference's CUDA and Metal arms).  Q8_0 / Q6_K run the
+    8-wave dot4 kernel for 1..2 rows and the 4-wave one above that (their
+    lane partials meet in different reduction trees), and keep one K-chunk
+    (so one task set per lane) up to 4 rows at k = 1024."""
     rng = np.random.default_rng(3)
     n, k = 96, 1024
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     x = rng.standard_normal((16, k)).astype(np.float32)
     qt = L.QTensor.quantize(_cuda(w), dt)
     mm = L.QMatMul.from_qtensor(qt)
-    groups = [(2, (1,)), (16, (3, 5, 8, 13))] if dt == O.Q4K else [(4, (1, 2, 3))]
+    groups = [(2, (1,)), (16, (3, 5, 8, 13))] if dt == O.Q4K else [(2, (1,)), (4, (3,))]
     for full_m, ms in groups:
         full = mm.forward(_cuda(x[:full_m])).cpu().numpy()
         for m in ms:
