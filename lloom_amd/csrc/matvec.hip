@@ -419,34 +419,149 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
     }
 }
 
-// --------------------------------------------- Q4_K decode on int8 MFMA --
+// ------------------------------------- Q4_K / Q6_K decode on int8 MFMA --
 // For more activation rows the dot4 kernel turns ALU-bound; this one puts
-// the per-sub-block dot on v_mfma_i32_16x16x32_i8.  A workgroup owns 16*NT
+// the sub-block dots on v_mfma_i32_16x16x32_i8.  A workgroup owns 16*NT
 // weight rows (NT tiles of 16); its KS waves split the superblocks of K and
-// add their partials through LDS.  Operands (k within one 32-element
-// sub-block j, g = lane / 16):
+// add their partials through LDS.  Operands (k within one 32-element chunk
+// j of a superblock, g = lane / 16):
 //   A (activations): lane l holds x_q8[m = l%16][32j + 8g + 0..7]
-//   B (weights):     lane l holds q4[n = l%16][32j + 8g + 0..7]
+//   B (weights):     lane l holds q[n = l%16][32j + 8g + 0..7]
 //   D:               lane l holds D[m = 4g + t][n = l%16], t = 0..3
 // so the lane's four outputs all belong to its own weight row and the row's
-// sub-block scale is a lane-local integer: acc += sc[j] * D_j.  The Q4_K min
-// term sum_j m[j] * sum_{k in j} x_k is a second MFMA chain against the 6-bit
-// mins broadcast to all 8 bytes, accumulated over the superblock in the
-// MFMA's own C operand.  Activations come pre-quantized (Q8_K, bit-exact)
-// from k_quantize_split_q8k, laid out so a lane's 64 bytes of a superblock
-// (its 8 bytes of each sub-block) are contiguous: one A tile serves NT weight
-// tiles.
+// sub-block scales are lane-local integers.
+//  * Q4_K: a chunk is one sub-block: acc += sc[j] * D_j; the min term
+//    sum_j m[j] * sum_{k in j} x_k is a second MFMA chain against the 6-bit
+//    mins broadcast to all 8 bytes, accumulated in the MFMA's C operand.
+//  * Q6_K: a chunk holds sub-blocks 2j (g < 2) and 2j+1 (g >= 2); the q - 32
+//    values are int8 already, and two MFMAs with the other half of B zeroed
+//    give each sub-block its own sum for its signed 8-bit scale.
+// Activations come pre-quantized (Q8_K, bit-exact) from
+// k_quantize_split_q8k, laid out so a lane's 64 bytes of a superblock (its
+// 8 bytes of each chunk) are contiguous: one A tile serves NT weight tiles.
+// The loads of a wave's next superblock are issued before the current one
+// is computed.
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-template <int KS, int NT>
-__global__ __launch_bounds__(64 * KS) void k_mv_mfma_q4k(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
-                                                         const float* __restrict__ xd, float* __restrict__ Y, int n,
-                                                         int K, int m) {
+// 8 bytes at a 2-byte-aligned address (Q6_K blocks are 210 bytes).
+__device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
+    uintptr_t a = (uintptr_t)p;
+    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+    const uint32_t s = (uint32_t)(a & 3u);
+    const uint32_t v0 = q[0], v1 = q[1], v2 = q[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(v1, v0, s), __builtin_amdgcn_alignbyte(v2, v1, s));
+}
+
+template <int TYPE>
+struct MfW;
+template <>
+struct MfW<T_Q4K> {
+    uint4 hdr;
+    uint2 q[4];
+};
+template <>
+struct MfW<T_Q6K> {
+    uint2 ql[4], qh[2];
+    uint4 sc;
+    uint32_t d;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void mf_load(const uint8_t* __restrict__ b, int g, MfW<TYPE>& w) {
+    if constexpr (TYPE == T_Q4K) {
+        w.hdr = *(const uint4*)b;
+#pragma unroll
+        for (int c = 0; c < 4; c++) w.q[c] = *(const uint2*)(b + 16 + 32 * c + 8 * g);
+    } else {
+        // ql byte 64h + 32(gq & 1) + 8g + t holds chunk j = 4h + gq (low
+        // nibble for gq < 2), qh byte 32h + 8g + t its two high bits
+#pragma unroll
+        for (int c = 0; c < 4; c++) w.ql[c] = load8_a2(b + 32 * c + 8 * g);
+#pragma unroll
+        for (int h = 0; h < 2; h++) w.qh[h] = load8_a2(b + Q6K_QH + 32 * h + 8 * g);
+        w.sc = load16_a2(b + Q6K_SC);
+        w.d = *(const uint16_t*)(b + Q6K_D);
+    }
+}
+
+// q6 (0..63) per byte -> q6 - 32 as int8: t = q6 ^ 32 is q6 - 32 in 6-bit
+// two's complement; copying bit 5 into bits 6 and 7 (0x20 * 6 = 0xC0, no
+// carry between bytes) sign-extends it to 8 bits.
+__device__ __forceinline__ uint32_t q6_to_i8(uint32_t q6) {
+    const uint32_t t = q6 ^ 0x20202020u;
+    return t | ((t & 0x20202020u) * 6u);
+}
+
+// One superblock of one 16-row tile: returns the f32 contributions of the
+// lane's four outputs.
+template <int TYPE>
+__device__ __forceinline__ void mf_compute(const MfW<TYPE>& w, const long (&a)[8], const float4& dy, int g,
+                                           float (&out)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    if constexpr (TYPE == T_Q4K) {
+        const float d = f16_to_f32(w.hdr.x & 0xffffu), dmin = f16_to_f32(w.hdr.x >> 16);
+        v4i accs = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int sc, mn;
+            if (j < 4) {
+                sc = byte_of(w.hdr.y, j) & 63;
+                mn = byte_of(w.hdr.z, j) & 63;
+            } else {
+                sc = (byte_of(w.hdr.w, j - 4) & 0xF) | ((byte_of(w.hdr.y, j - 4) >> 6) << 4);
+                mn = (byte_of(w.hdr.w, j - 4) >> 4) | ((byte_of(w.hdr.z, j - 4) >> 6) << 4);
+            }
+            const int c = j >> 1, sh = (j & 1) * 4;
+            const uint32_t lo = (w.q[c].x >> sh) & 0x0F0F0F0Fu, hi = (w.q[c].y >> sh) & 0x0F0F0F0Fu;
+            const long bw = (long)(((uint64_t)hi << 32) | lo);
+            const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
+            const uint32_t mrep = (uint32_t)mn * 0x01010101u;
+            const long bm = (long)(((uint64_t)mrep << 32) | mrep);
+            accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bm, accm, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; t++) accs[t] += __mul24(sc, dj[t]);
+        }
+        out[0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
+        out[1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
+        out[2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
+        out[3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
+    } else {
+        const float d = f16_to_f32(w.d);
+        const bool lo_half = g < 2;  // this lane's k range is sub-block 2j, else 2j + 1
+        v4i accs = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int h = j >> 2, gq = j & 3, c = 2 * h + (gq & 1);
+            const uint32_t nx = gq < 2 ? (w.ql[c].x & 0x0F0F0F0Fu) : ((w.ql[c].x >> 4) & 0x0F0F0F0Fu);
+            const uint32_t ny = gq < 2 ? (w.ql[c].y & 0x0F0F0F0Fu) : ((w.ql[c].y >> 4) & 0x0F0F0F0Fu);
+            const uint32_t hx = (w.qh[h].x >> (2 * gq)) & 0x03030303u, hy = (w.qh[h].y >> (2 * gq)) & 0x03030303u;
+            const uint32_t vx = q6_to_i8(nx | (hx << 4)), vy = q6_to_i8(ny | (hy << 4));
+            const long bw = (long)(((uint64_t)vy << 32) | vx);
+            const v4i da = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], lo_half ? bw : 0l, zero, 0, 0, 0);
+            const v4i db = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], lo_half ? 0l : bw, zero, 0, 0, 0);
+            // scales[2j], scales[2j + 1]: dword j / 2, bytes 2(j & 1) and 2(j & 1) + 1
+            const uint32_t sw = j < 2 ? w.sc.x : j < 4 ? w.sc.y : j < 6 ? w.sc.z : w.sc.w;
+            const int sa = (int)(int8_t)byte_of(sw, 2 * (j & 1)), sb = (int)(int8_t)byte_of(sw, 2 * (j & 1) + 1);
+#pragma unroll
+            for (int t = 0; t < 4; t++) accs[t] += __mul24(sa, da[t]) + __mul24(sb, db[t]);
+        }
+        out[0] += (d * dy.x) * (float)accs[0];
+        out[1] += (d * dy.y) * (float)accs[1];
+        out[2] += (d * dy.z) * (float)accs[2];
+        out[3] += (d * dy.w) * (float)accs[3];
+    }
+}
+
+template <int TYPE, int KS, int NT>
+__global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                     const float* __restrict__ xd, float* __restrict__ Y, int n,
+                                                     int K, int m) {
+    constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float4 part[KS > 1 ? KS - 1 : 1][NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int nsb = K >> 8;
-    const int64_t rowbytes = (int64_t)nsb * Q4K_BYTES;
+    const int64_t rowbytes = (int64_t)nsb * BB;
     const uint8_t* wrow[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) wrow[t] = W + (int64_t)min(blockIdx.x * 16 * NT + 16 * t + c16, n - 1) * rowbytes;
@@ -455,60 +570,42 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma_q4k(const uint8_t* __restri
     float out[NT][4];
 #pragma unroll
     for (int t = 0; t < NT; t++) out[t][0] = out[t][1] = out[t][2] = out[t][3] = 0.0f;
+
+    // registers of the superblock in flight; loads are unconditional (a
+    // wave past the end reloads its last superblock) so none sits under a
+    // branch and the waits stay counted
+    MfW<TYPE> wc[NT];
+    uint4 avc[4];
+    float4 dyc;
+    auto issue = [&](int sb, MfW<TYPE>(&w)[NT], uint4(&av)[4], float4& dy) {
+        const int sbc = min(sb, nsb - 1);
+#pragma unroll
+        for (int t = 0; t < NT; t++) mf_load<TYPE>(wrow[t] + (int64_t)sbc * BB, g, w[t]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) av[i] = *(const uint4*)(xrow + sbc * 256 + 16 * i);
+        dy = *(const float4*)(xd + sbc * 16 + 4 * g);
+    };
+    issue(wave, wc, avc, dyc);
     for (int sb = wave; sb < nsb; sb += KS) {
-        uint4 hdr[NT];
-        uint2 q[NT][4];
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const uint8_t* b = wrow[t] + sb * Q4K_BYTES;
-            hdr[t] = *(const uint4*)b;
-#pragma unroll
-            for (int c = 0; c < 4; c++) q[t][c] = *(const uint2*)(b + 16 + 32 * c + 8 * g);
-        }
-        // unconditional loads (row clamped above), zeroed by select: a load
-        // under a divergent branch makes the compiler serialize them
-        uint4 av[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) av[i] = *(const uint4*)(xrow + sb * 256 + 16 * i);
-        const float4 dy = *(const float4*)(xd + sb * 16 + 4 * g);
+        MfW<TYPE> wn[NT];
+        uint4 avn[4];
+        float4 dyn;
+        issue(sb + KS, wn, avn, dyn);
+        // activation rows past m are zeroed by select (a load under a
+        // divergent branch would serialize the waits)
         long a[8];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            a[2 * i] = arow_ok ? (long)(((uint64_t)av[i].y << 32) | av[i].x) : 0l;
-            a[2 * i + 1] = arow_ok ? (long)(((uint64_t)av[i].w << 32) | av[i].z) : 0l;
+            a[2 * i] = arow_ok ? (long)(((uint64_t)avc[i].y << 32) | avc[i].x) : 0l;
+            a[2 * i + 1] = arow_ok ? (long)(((uint64_t)avc[i].w << 32) | avc[i].z) : 0l;
         }
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const float d = f16_to_f32(hdr[t].x & 0xffffu), dmin = f16_to_f32(hdr[t].x >> 16);
-            v4i accs = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
+        for (int t = 0; t < NT; t++) mf_compute<TYPE>(wc[t], a, dyc, g, out[t]);
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                int sc, mn;
-                if (j < 4) {
-                    sc = byte_of(hdr[t].y, j) & 63;
-                    mn = byte_of(hdr[t].z, j) & 63;
-                } else {
-                    sc = (byte_of(hdr[t].w, j - 4) & 0xF) | ((byte_of(hdr[t].y, j - 4) >> 6) << 4);
-                    mn = (byte_of(hdr[t].w, j - 4) >> 4) | ((byte_of(hdr[t].z, j - 4) >> 6) << 4);
-                }
-                const int c = j >> 1, sh = (j & 1) * 4;
-                const uint32_t lo = (q[t][c].x >> sh) & 0x0F0F0F0Fu, hi = (q[t][c].y >> sh) & 0x0F0F0F0Fu;
-                const long bw = (long)(((uint64_t)hi << 32) | lo);
-                const v4i zero = {0, 0, 0, 0};
-                const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
-                const uint32_t mrep = (uint32_t)mn * 0x01010101u;
-                const long bm = (long)(((uint64_t)mrep << 32) | mrep);
-                accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bm, accm, 0, 0, 0);
-                accs[0] += sc * dj[0];
-                accs[1] += sc * dj[1];
-                accs[2] += sc * dj[2];
-                accs[3] += sc * dj[3];
-            }
-            out[t][0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
-            out[t][1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
-            out[t][2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
-            out[t][3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
-        }
+        for (int t = 0; t < NT; t++) wc[t] = wn[t];
+#pragma unroll
+        for (int i = 0; i < 4; i++) avc[i] = avn[i];
+        dyc = dyn;
     }
     if (KS > 1) {
         if (wave != 0) {
@@ -599,22 +696,36 @@ static hipError_t launch_type(const void* w, const float* x, float* y, int n, in
 }
 
 size_t matvec_workspace_bytes(int type, int64_t k, int64_t m) {
-    if (type != T_Q4K || m <= MV_DOT_MAX_ROWS) return 0;
+    if (type == T_Q8_0 || m <= MV_DOT_MAX_ROWS) return 0;
     return split_q8k_bytes(k, m);
+}
+
+template <int TYPE>
+static hipError_t launch_mv_mfma(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xq,
+                                 const float* xd, hipStream_t s) {
+    // 8 waves split K; 2 row tiles per workgroup unless that leaves fewer
+    // than ~256 workgroups
+    constexpr int KS = 8;
+    if (n >= 2 * 16 * 256) {
+        hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 2>), dim3((unsigned)((n + 31) / 32)), dim3(64 * KS), 0, s,
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
+    } else {
+        hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 1>), dim3((unsigned)((n + 15) / 16)), dim3(64 * KS), 0, s,
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, hipStream_t s) {
-    if (type == T_Q4K && m > MV_DOT_MAX_ROWS) {
+    if (type != T_Q8_0 && m > MV_DOT_MAX_ROWS) {
         int8_t* xq;
         float* xd;
         split_q8k_ptrs(ws, k, m, &xq, &xd);
         hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
         if (e != hipSuccess) return e;
-        constexpr int KS = 8, NT = 2;
-        hipLaunchKernelGGL((k_mv_mfma_q4k<KS, NT>), dim3((unsigned)((n + 16 * NT - 1) / (16 * NT))), dim3(64 * KS),
-                           0, s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
-        return hipGetLastError();
+        return type == T_Q4K ? launch_mv_mfma<T_Q4K>(w, y, n, k, m, xq, xd, s)
+                             : launch_mv_mfma<T_Q6K>(w, y, n, k, m, xq, xd, s);
     }
     switch (type) {
         case T_Q4K: return launch_type<T_Q4K>(w, x, y, (int)n, (int)k, (int)m, s);

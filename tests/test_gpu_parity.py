@@ -179,12 +179,12 @@ def test_qmatmul_closed_form_inputs(L, dt):
 def test_decode_rows_batch_invariant(L, dt):
     """Within one decode kernel every activation row is computed alone, so a
     row's output does not depend on its batch (qmm_batch,
-    quantized_tests.rs:239-275, exact on the CPU arm).  Q4_K with 3..16 rows
-    runs the MFMA kernel, 1..2 the dot4 kernel: each group is checked
-    against its own full batch (across the two kernels only the tolerance
-    holds, as on the reference's CUDA and Metal arms).  Q8_0 / Q6_K run the
-    8-wave dot4 kernel for 1..2 rows and the 4-wave one above that (their
-    lane partials meet in different reduction trees), and keep one K-chunk
+    quantized_tests.rs:239-275, exact on the CPU arm).  Q4_K and Q6_K with
+    3..16 rows run the MFMA kernel, 1..2 the dot4 kernel: each group is
+    checked against its own full batch (across the two kernels only the
+    tolerance holds, as on the reference's CUDA and Metal arms).  Q8_0 runs
+    the 8-wave dot4 kernel for 1..2 rows and the 4-wave one above that (their
+    lane partials meet in different reduction trees), and keeps one K-chunk
     (so one task set per lane) up to 4 rows at k = 1024."""
     rng = np.random.default_rng(3)
     n, k = 96, 1024
@@ -192,7 +192,7 @@ def test_decode_rows_batch_invariant(L, dt):
     x = rng.standard_normal((16, k)).astype(np.float32)
     qt = L.QTensor.quantize(_cuda(w), dt)
     mm = L.QMatMul.from_qtensor(qt)
-    groups = [(2, (1,)), (16, (3, 5, 8, 13))] if dt == O.Q4K else [(2, (1,)), (4, (3,))]
+    groups = [(2, (1,)), (16, (3, 5, 8, 13))] if dt != O.Q8_0 else [(2, (1,)), (4, (3,))]
     for full_m, ms in groups:
         full = mm.forward(_cuda(x[:full_m])).cpu().numpy()
         for m in ms:
@@ -241,11 +241,12 @@ def test_baseline_c3_q4k_prefill_subset(L, m):
     assert_rows_close(y[np.ix_(rows, cols)], want, what=f"C3 m={m}")
 
 
-def test_baseline_c4_q6k_down_proj(L):
+@pytest.mark.parametrize("b", [1, 4, 16])
+def test_baseline_c4_q6k_down_proj(L, b):
     w = L.synth_normal(3, 2048 * 8192, 0.0, 0.02).reshape(2048, 8192)
-    x = L.synth_normal(3003, 4 * 8192).reshape(4, 8192)
+    x = L.synth_normal(3003, b * 8192).reshape(b, 8192)
     y, q = _qmm(L, O.Q6K, w, x)
-    assert_rows_close(y, O.matmul(O.Q6K, x, q, 2048), what="C4 down")
+    assert_rows_close(y, O.matmul(O.Q6K, x, q, 2048), what=f"C4 down b={b}")
 
 
 # -------------------------------------------------------- routed experts ---
