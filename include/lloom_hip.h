@@ -144,8 +144,11 @@ int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int6
  * matmul_t_indexed (mod.rs:766-810): W [n_experts, n, k] packed, x f32
  * [batch, in_dim1, k] with in_dim1 in {1, topk}, ids u32 [batch, topk],
  * y f32 [batch, topk, n]; plane (b, t) = x[b, t or 0] . W[ids[b, t]]^T.
- * The dots are f32 over dequantized weight rows, as the CPU arm computes
- * them (no activation quantization).  An id >= n_experts yields a zero plane
+ * The dots take the f32 activations as they are (no activation
+ * quantization, as on the CPU arm) against the exactly dequantized weights,
+ * factored per 16-element run: scale * sum(q * x) - min * sum(x), the CPU
+ * arm's dot of a dequantized row in another rounding order.  n_experts is at
+ * most 4096 (LLOOM_HIP_ESHAPE beyond).  An id >= n_experts yields a zero plane
  * and LLOOM_HIP_EEXPERT from this call (it synchronizes the stream to read
  * the device flag) unless strict is 0, in which case the next
  * lloom_hip_ctx_sync reports it. */

@@ -299,8 +299,11 @@ int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, i
     if (k % be) return fail(LLOOM_HIP_ESHAPE, "routed matmul k %lld is not divisible by block size %d", (long long)k, be);
     if (in_dim1 != 1 && in_dim1 != topk)
         return fail(LLOOM_HIP_ESHAPE, "indexed_moe_forward: x dim 1 (%lld) must be 1 or topk (%lld)", (long long)in_dim1, (long long)topk);
-    if (batch * topk > (1 << 24) || n_experts > (1 << 20) || n > INT32_MAX || k > INT32_MAX)
+    if (batch * topk > (1 << 24) || n > INT32_MAX || k > INT32_MAX)
         return fail(LLOOM_HIP_ESHAPE, "moe_matmul: shape too large");
+    if (n_experts > MOE_MAX_EXPERTS)
+        return fail(LLOOM_HIP_ESHAPE, "moe_matmul: %lld experts, at most %d are routed on the device",
+                    (long long)n_experts, MOE_MAX_EXPERTS);
     if ((uintptr_t)w_dev % (ggml_type == T_Q4K ? 16 : 4) || (uintptr_t)x_dev % 16)
         return fail(LLOOM_HIP_EINVAL, "moe_matmul: misaligned weight or x pointer");
     HIP_OK(hipSetDevice(ctx->device));

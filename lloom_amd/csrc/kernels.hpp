@@ -34,6 +34,8 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
 size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode);
 
 // moe.hip
+// The router keeps two ints per expert in LDS.
+constexpr int MOE_MAX_EXPERTS = 4096;
 size_t moe_workspace_ints(int64_t n_experts, int64_t planes);
 hipError_t launch_moe(int type, const void* w, int64_t n_experts, int64_t n, int64_t k, const float* x,
                       int64_t batch, int64_t in_dim1, const uint32_t* ids, int64_t topk, float* y, int* ws,

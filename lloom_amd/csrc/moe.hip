@@ -7,11 +7,15 @@
 // reorganizes the work for HBM:
 //  1. k_moe_route groups the (b, t) planes by expert on the device (a
 //     counting sort; ids never leave the GPU) and flags ids >= n_experts;
-//  2. k_moe_rows runs one workgroup per (active expert, row block): each
-//     weight row of a touched expert is read from HBM once and dotted with
-//     every plane routed to that expert (in groups of PG planes), instead of
-//     once per plane.
+//  2. k_moe_lds runs one workgroup per (active expert, block of rows): the
+//     activation planes routed to the expert are staged in LDS (up to eight
+//     at a time), each lane dequantizes its piece of R weight rows once and
+//     dots it with every staged plane, so each weight byte is read from HBM
+//     once per call and each activation element from L2 once per workgroup.
+//     k_moe_rows (activations read from L2 per row) is kept for rows too long
+//     to stage.
 #include "kq_common.hpp"
+#include "kq_tasks.hpp"
 #include "kernels.hpp"
 
 namespace lloom {
@@ -23,43 +27,82 @@ namespace lloom {
 // [2+3E .. 2+3E+P) planes sorted by expert, [.. +E) fill cursor.
 size_t moe_workspace_ints(int64_t n_experts, int64_t planes) { return 2 + 4 * (size_t)n_experts + (size_t)planes; }
 
+// One workgroup: count planes per expert, scan, scatter -- in LDS, one
+// global write per output.  The order of the planes inside an expert's list
+// follows the LDS atomics, but every plane's dot is computed on its own, so
+// no result depends on it.
 __global__ __launch_bounds__(1024) void k_moe_route(const uint32_t* __restrict__ ids, int planes, int E, int* ws,
                                                     int* sticky, float* __restrict__ y, int n) {
+    extern __shared__ int s_mem[];  // [E] counts, then [E] cursors
+    __shared__ int s_part[1024];
+    __shared__ int s_bad, s_active;
+    int* s_count = s_mem;
+    int* s_cur = s_mem + E;
     int* count = ws + 2;
-    if (threadIdx.x == 0) ws[0] = 0;
     int* start = count + E;
     int* active = start + E;
     int* sorted = active + E;
-    int* cursor = sorted + planes;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        count[e] = 0;
-        cursor[e] = 0;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int e = tid; e < E; e += nt) s_count[e] = 0;
+    if (tid == 0) {
+        s_bad = 0;
+        s_active = 0;
     }
     __syncthreads();
-    for (int p = threadIdx.x; p < planes; p += blockDim.x) {
-        uint32_t e = ids[p];
+    for (int p = tid; p < planes; p += nt) {
+        const uint32_t e = ids[p];
         if (e < (uint32_t)E) {
-            atomicAdd(&count[e], 1);
+            atomicAdd(&s_count[e], 1);
         } else {
-            ws[0] = 1;      // this call: read back by a strict call
-            sticky[0] = 1;  // until the next lloom_hip_ctx_sync
+            s_bad = 1;
             for (int r = 0; r < n; r++) y[(int64_t)p * n + r] = 0.0f;
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int s = 0, a = 0;
-        for (int e = 0; e < E; e++) {
-            start[e] = s;
-            s += count[e];
-            if (count[e]) active[a++] = e;
-        }
-        ws[1] = a;
+    // exclusive scan: thread t owns experts [t*per, (t+1)*per)
+    const int per = (E + nt - 1) / nt;
+    const int e0 = min(tid * per, E), e1 = min(e0 + per, E);
+    int local = 0, nact = 0;
+    for (int e = e0; e < e1; e++) {
+        local += s_count[e];
+        nact += s_count[e] > 0;
     }
+    // scan of (local, nact) packed: nact < 2^15, local < 2^16 per thread is
+    // not guaranteed, so two passes
+    int incl = local;
+    for (int o = 1; o < nt; o <<= 1) {
+        s_part[tid] = incl;
+        __syncthreads();
+        if (tid >= o) incl += s_part[tid - o];
+        __syncthreads();
+    }
+    int run = incl - local;
+    int ainc = nact;
+    for (int o = 1; o < nt; o <<= 1) {
+        s_part[tid] = ainc;
+        __syncthreads();
+        if (tid >= o) ainc += s_part[tid - o];
+        __syncthreads();
+    }
+    int arun = ainc - nact;
+    for (int e = e0; e < e1; e++) {
+        const int c = s_count[e];
+        count[e] = c;
+        start[e] = run;
+        s_cur[e] = run;
+        if (c) active[arun++] = e;
+        run += c;
+    }
+    if (tid == nt - 1) s_active = ainc;
     __syncthreads();
-    for (int p = threadIdx.x; p < planes; p += blockDim.x) {
-        uint32_t e = ids[p];
-        if (e < (uint32_t)E) sorted[start[e] + atomicAdd(&cursor[e], 1)] = p;
+    for (int p = tid; p < planes; p += nt) {
+        const uint32_t e = ids[p];
+        if (e < (uint32_t)E) sorted[atomicAdd(&s_cur[e], 1)] = p;
+    }
+    if (tid == 0) {
+        ws[0] = s_bad;             // this call: read back by a strict call
+        if (s_bad) sticky[0] = 1;  // until the next lloom_hip_ctx_sync
+        ws[1] = s_active;
     }
 }
 
@@ -222,6 +265,251 @@ __global__ __launch_bounds__(256) void k_moe_rows(const uint8_t* __restrict__ W,
     }
 }
 
+// ---------------------------------------------------- LDS-staged planes --
+// A task's weights as runs of 16 consecutive elements sharing one affine
+// dequantization value = a * q - b (k_quants.rs to_float):
+//   Q4_K  q = nibble,    a = d * sc,  b = dmin * m   (two runs)
+//   Q6_K  q = q6,        a = d * sc,  b = 32 * a     (four runs)
+//   Q8_0  q = int8,      a = d,       b = 0          (two runs)
+// The dot with f32 activations is taken as a * sum(q * x) - b * sum(x): the
+// q are small integers (exact in f32), and sum(x) over each 16-element run
+// is computed once per staged plane.
+template <int TYPE>
+struct MoeRuns;
+template <>
+struct MoeRuns<T_Q4K> {
+    static constexpr int N = 2;
+};
+template <>
+struct MoeRuns<T_Q6K> {
+    static constexpr int N = 4;
+};
+template <>
+struct MoeRuns<T_Q8_0> {
+    static constexpr int N = 2;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void task_runs(const WPrep<TYPE>& w, float (&q)[MoeRuns<TYPE>::N][16],
+                                          float (&a)[MoeRuns<TYPE>::N], float (&b)[MoeRuns<TYPE>::N]) {
+    if constexpr (TYPE == T_Q4K) {
+        a[0] = w.d * (float)w.sc0;
+        b[0] = w.dmin * (float)w.m0;
+        a[1] = w.d * (float)w.sc1;
+        b[1] = w.dmin * (float)w.m1;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            q[0][i] = (float)byte_of(w.lo[i >> 2], i & 3);
+            q[1][i] = (float)byte_of(w.hi[i >> 2], i & 3);
+        }
+    } else if constexpr (TYPE == T_Q6K) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            a[g] = w.d * (float)w.sc[g];
+            b[g] = 32.0f * a[g];
+#pragma unroll
+            for (int i = 0; i < 16; i++) q[g][i] = (float)byte_of(w.q[g][i >> 2], i & 3);
+        }
+    } else {
+        a[0] = a[1] = w.d;
+        b[0] = b[1] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) q[i >> 4][i & 15] = (float)(int8_t)byte_of(w.w[i >> 2], i & 3);
+    }
+}
+
+// Element offset (within the row) of run r of task ti.
+template <int TYPE>
+__device__ __forceinline__ int run_offset(int ti, int r) {
+    using Tr = MvTraits<TYPE>;
+    const int blk = ti / Tr::P, p = ti % Tr::P;
+    if constexpr (TYPE == T_Q4K) return blk * 256 + 64 * (p >> 1) + 16 * (p & 1) + 32 * r;
+    else if constexpr (TYPE == T_Q6K) return blk * 256 + 128 * (p >> 1) + 32 * r + 16 * (p & 1);
+    else return blk * 32 + 16 * r;
+}
+
+// Sum over the LPR lanes of a group (LPR a power of two, at most 16).
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (LPR >= 2) v += dpp<DPP_XOR1>(v);
+    if constexpr (LPR >= 4) v += dpp<DPP_XOR2>(v);
+    if constexpr (LPR >= 8) v += dpp<DPP_HALF_MIRROR>(v);
+    if constexpr (LPR >= 16) v += dpp<DPP_ROW_MIRROR>(v);
+    return v;
+}
+
+constexpr int MOE_PG = 8;          // planes staged per pass
+constexpr int MOE_LDS = 72 * 1024;  // bytes of staged planes and run sums
+
+// One workgroup (4 waves) per (block of rows, active-expert slot).  In a
+// wave, 64 / LPR groups of LPR lanes each own R consecutive rows and walk
+// the row's tasks LPR apart (TPL of them loaded at once); a lane's R rows
+// share its activation reads.
+template <int TYPE, int LPR, int R, int TPL>
+__global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                 float* __restrict__ Y, const int* __restrict__ ws, int E, int n,
+                                                 int K, int in_dim1, int topk, int pgmax) {
+    using Tr = MvTraits<TYPE>;
+    constexpr int NR = MoeRuns<TYPE>::N;
+    // [pgmax][KP] planes, then [pgmax][K / 16] run sums.  A plane stores
+    // element e at e + 4 (e / 64): the eight tasks of a superblock read
+    // 16-byte pieces 16 or 48 elements apart, which this spreads over
+    // distinct banks.
+    extern __shared__ __align__(16) float xs[];
+    const int KP = K + K / 16;
+    float* sx = xs + pgmax * KP;
+    const int* count = ws + 2;
+    const int* start = count + E;
+    const int* active = start + E;
+    const int* sorted = active + E;
+    const int slot = blockIdx.y;
+    if (slot >= ws[1]) return;  // uniform: fewer active experts than slots
+    const int e = active[slot];
+    const int np = count[e], p0 = start[e];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane / LPR, tl = lane % LPR;
+    const int row0 = ((blockIdx.x * 4 + wave) * (64 / LPR) + grp) * R;
+    const int64_t rowbytes = (int64_t)(K / Tr::BE) * Tr::BB;
+    const uint8_t* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) wrow[r] = W + ((int64_t)e * n + min(row0 + r, n - 1)) * rowbytes;
+    const int T = (K / Tr::BE) * Tr::P;
+    const int k16 = K >> 4;
+
+    for (int g0 = 0; g0 < np; g0 += pgmax) {
+        const int pg = min(pgmax, np - g0);
+        float acc[R][MOE_PG];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int q = 0; q < MOE_PG; q++) acc[r][q] = 0.0f;
+        // tasks in chunks of TPL per lane, every load of a chunk in flight
+        // at once (rows of up to TPL * LPR tasks are a single chunk)
+        for (int c0 = 0; c0 < T; c0 += TPL * LPR) {
+            TaskData td[TPL][R];
+#pragma unroll
+            for (int c = 0; c < TPL; c++) {
+                const int ti = c0 + c * LPR + tl;
+                const int tc = ti < T ? ti : 0;
+#pragma unroll
+                for (int r = 0; r < R; r++) load_task<TYPE>(wrow[r], tc / Tr::P, tc % Tr::P, td[c][r]);
+            }
+            if (c0 == 0) {
+                // stage planes g0 .. g0 + pg of this expert (the first
+                // chunk's weights are in flight meanwhile) and the sum of
+                // each 16-element run
+                if (g0) __syncthreads();  // the previous group's readers are done
+                for (int i = threadIdx.x; i < pg * k16; i += 256) {
+                    const int q = i / k16, c = i - q * k16;
+                    const int pl = sorted[p0 + g0 + q];
+                    const int b = pl / topk, t = pl - b * topk;
+                    const float4* xr =
+                        (const float4*)(X + (int64_t)(b * in_dim1 + (in_dim1 == 1 ? 0 : t)) * K + 16 * c);
+                    float4 v[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) v[u] = xr[u];
+                    float4* dst = (float4*)(xs + q * KP + 16 * c + 4 * (c >> 2));
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        dst[u] = v[u];
+                        sum += v[u].x + v[u].y + v[u].z + v[u].w;
+                    }
+                    sx[q * k16 + c] = sum;
+                }
+                __syncthreads();
+            }
+#pragma unroll
+            for (int c = 0; c < TPL; c++) {
+                const int ti = c0 + c * LPR + tl;
+                if (ti < T) {
+                    float qv[R][NR][16], ra[R][NR], rb[R][NR];
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        WPrep<TYPE> wp;
+                        prep_task<TYPE>(td[c][r], ti % Tr::P, wp);
+                        task_runs<TYPE>(wp, qv[r], ra[r], rb[r]);
+                    }
+                    int off[NR];
+#pragma unroll
+                    for (int u = 0; u < NR; u++) off[u] = run_offset<TYPE>(ti, u);
+#pragma unroll
+                    for (int q = 0; q < MOE_PG; q++) {
+                        if (q < pg) {  // uniform
+                            const float* xq = xs + q * KP;
+#pragma unroll
+                            for (int u = 0; u < NR; u++) {
+                                float dq[R];
+#pragma unroll
+                                for (int r = 0; r < R; r++) dq[r] = 0.0f;
+#pragma unroll
+                                for (int i4 = 0; i4 < 4; i4++) {
+                                    const float4 xv = *(const float4*)(xq + off[u] + 4 * (off[u] >> 6) + 4 * i4);
+#pragma unroll
+                                    for (int r = 0; r < R; r++) {
+                                        dq[r] = __builtin_fmaf(qv[r][u][4 * i4], xv.x, dq[r]);
+                                        dq[r] = __builtin_fmaf(qv[r][u][4 * i4 + 1], xv.y, dq[r]);
+                                        dq[r] = __builtin_fmaf(qv[r][u][4 * i4 + 2], xv.z, dq[r]);
+                                        dq[r] = __builtin_fmaf(qv[r][u][4 * i4 + 3], xv.w, dq[r]);
+                                    }
+                                }
+                                const float s16 = sx[q * k16 + (off[u] >> 4)];
+#pragma unroll
+                                for (int r = 0; r < R; r++)
+                                    acc[r][q] =
+                                        __builtin_fmaf(ra[r][u], dq[r], __builtin_fmaf(-rb[r][u], s16, acc[r][q]));
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        // sum over the LPR lanes of the group; lane tl == 0 stores
+#pragma unroll
+        for (int q = 0; q < MOE_PG; q++) {
+            if (q < pg) {
+                const int pl = sorted[p0 + g0 + q];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const float v = group_sum<LPR>(acc[r][q]);
+                    if (tl == 0 && row0 + r < n) Y[(int64_t)pl * n + row0 + r] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int TYPE, int LPR, int R>
+static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
+                              int in_dim1, int topk, int max_slots, int pgmax, hipStream_t s) {
+    constexpr int TPL = 4;
+    constexpr int ROWS = 4 * (64 / LPR) * R;
+    const size_t shm = (size_t)pgmax * (K + 2 * (K / 16)) * sizeof(float);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_moe_lds<TYPE, LPR, R, TPL>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, MOE_LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    dim3 grid((n + ROWS - 1) / ROWS, max_slots);
+    hipLaunchKernelGGL((k_moe_lds<TYPE, LPR, R, TPL>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ws, E, n, K,
+                       in_dim1, topk, pgmax);
+    return hipGetLastError();
+}
+
+// LPR: a row's tasks spread over LPR lanes, up to 4 per lane.
+template <int TYPE>
+static hipError_t moe_lds_type(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
+                               int in_dim1, int topk, int max_slots, int pgmax, hipStream_t s) {
+    using Tr = MvTraits<TYPE>;
+    constexpr int R = TYPE == T_Q6K ? 1 : 2;
+    const int T = (K / Tr::BE) * Tr::P;
+    if (T > 32) return moe_lds_cfg<TYPE, 16, R>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, s);
+    if (T > 16) return moe_lds_cfg<TYPE, 8, R>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, s);
+    return moe_lds_cfg<TYPE, 4, R>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, s);
+}
+
 template <int TYPE, int LPR>
 static hipError_t moe_rows_lpr(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
                                int in_dim1, int topk, int max_slots, hipStream_t s) {
@@ -247,10 +535,21 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
                       int64_t in_dim1, const uint32_t* ids, int64_t topk, float* y, int* ws, int* sticky,
                       hipStream_t s) {
     int planes = (int)(batch * topk);
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 0, s, ids, planes, (int)E, ws, sticky, y, (int)n);
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 2 * E * sizeof(int), s, ids, planes, (int)E, ws, sticky, y,
+                       (int)n);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     int max_slots = (int)(E < planes ? E : planes);
+    const int64_t per_plane = (k + 2 * (k / 16)) * (int64_t)sizeof(float);
+    const int pgmax = MOE_LDS / per_plane < MOE_PG ? (int)(MOE_LDS / per_plane) : MOE_PG;
+    if (pgmax >= 1 && (k & 15) == 0) {
+        switch (type) {
+            case T_Q4K: return moe_lds_type<T_Q4K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, pgmax, s);
+            case T_Q6K: return moe_lds_type<T_Q6K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, pgmax, s);
+            case T_Q8_0: return moe_lds_type<T_Q8_0>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, pgmax, s);
+        }
+        return hipErrorInvalidValue;
+    }
     switch (type) {
         case T_Q4K: return moe_rows_type<T_Q4K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, s);
         case T_Q6K: return moe_rows_type<T_Q6K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, s);
