@@ -127,6 +127,14 @@ constexpr int G_B_CHUNKS = (G_B_BYTES + 1023) / 1024;    // 18 (the last one par
 static_assert(G_BM == 128 && G_BN == 128, "staging assumes 128 x 128 tiles");
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Each 16-bit half of q times f (f < 2^16), modulo 2^16 per half.
+__device__ __forceinline__ int pk_mul_u16(uint32_t q, uint32_t f) {
+    const u16x2 a = __builtin_bit_cast(u16x2, q);
+    const u16x2 b = {(unsigned short)f, (unsigned short)f};
+    return __builtin_bit_cast(int, a * b);
+}
 
 __device__ __forceinline__ void lds_load16(const void* g, uint8_t* lds_chunk) {
     __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_chunk, 16, 0, 0);
@@ -135,50 +143,78 @@ __device__ __forceinline__ void lds_load4(const void* g, uint8_t* lds_chunk) {
     __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_chunk, 4, 0, 0);
 }
 
+// Per-lane byte offsets of this wave's share of a stage, fixed for the
+// whole K loop: the superblock only moves the (uniform) base pointers, so
+// the loads take the scalar-base + 32-bit-offset form and a stage costs no
+// per-lane address arithmetic.
+constexpr int G_A_PER_WAVE = G_A_CHUNKS / G_WAVES;                 // 8
+constexpr int G_B_PER_WAVE = (G_B_CHUNKS + G_WAVES - 1) / G_WAVES;  // 5
+struct StageOffs {
+    uint32_t a[G_A_PER_WAVE];
+    uint32_t b[G_B_PER_WAVE];
+    uint32_t sd;
+};
+
+__device__ __forceinline__ StageOffs stage_offsets(int m0, int n0, int m, int n, int k) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nsb = k >> 8;
+    const uint32_t rowbytes = (uint32_t)nsb * Q4K_BYTES;
+    StageOffs o;
+#pragma unroll
+    for (int i = 0; i < G_A_PER_WAVE; i++) {
+        const int q = wave * G_A_PER_WAVE + i;
+        const int row = 4 * q + (lane >> 4);
+        const int piece = (lane & 15) ^ (row & 7);
+        const int grow = min(m0 + row, m - 1);
+        o.a[i] = (uint32_t)grow * (uint32_t)k + 16u * piece;
+    }
+#pragma unroll
+    for (int i = 0; i < G_B_PER_WAVE; i++) {
+        const int q = wave + G_WAVES * i;
+        const int pc = min(64 * q + lane, G_BN * 9 - 1);
+        const int row = pc / 9, piece = pc - row * 9;
+        const int grow = min(n0 + row, n - 1);
+        o.b[i] = (uint32_t)grow * rowbytes + 16u * piece;
+    }
+    if (wave < 2) {
+        const int grow = min(m0 + 64 * wave + lane, m - 1);
+        o.sd = (uint32_t)grow * (uint32_t)nsb * 16u;
+    } else {
+        const int grow = min(m0 + 64 * (wave - 2) + lane, m - 1);
+        o.sd = 4u * (uint32_t)grow;
+    }
+    return o;
+}
+
 // Queue the loads of superblock sb into one LDS stage (each wave its share).
 __device__ __forceinline__ void stage_issue(uint8_t* stage, const int8_t* __restrict__ xq,
                                             const int8_t* __restrict__ sp, const float* __restrict__ dyt,
-                                            const uint8_t* __restrict__ W, int m0, int n0, int m, int n, int k,
-                                            int sb) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nsb = k >> 8;
-    const int64_t rowbytes = (int64_t)nsb * Q4K_BYTES;
+                                            const uint8_t* __restrict__ W, const StageOffs& o, int m, int sb) {
+    const int wave = threadIdx.x >> 6;
     uint8_t* A = stage;
     uint8_t* B = stage + G_A_BYTES;
     uint8_t* S = B + G_B_BYTES;
     uint8_t* D = S + G_S_BYTES;
+    const int8_t* xb = xq + sb * 256;
+    const uint8_t* wb = W + sb * Q4K_BYTES;
 #pragma unroll
-    for (int i = 0; i < G_A_CHUNKS / G_WAVES; i++) {
-        const int q = wave * (G_A_CHUNKS / G_WAVES) + i;
-        const int row = 4 * q + (lane >> 4);
-        const int piece = (lane & 15) ^ (row & 7);
-        const int grow = min(m0 + row, m - 1);
-        lds_load16(xq + (int64_t)grow * k + sb * 256 + 16 * piece, A + 1024 * q);
-    }
+    for (int i = 0; i < G_A_PER_WAVE; i++) lds_load16(xb + o.a[i], A + 1024 * (wave * G_A_PER_WAVE + i));
 #pragma unroll
-    for (int i = 0; i < (G_B_CHUNKS + G_WAVES - 1) / G_WAVES; i++) {
+    for (int i = 0; i < G_B_PER_WAVE; i++) {
         const int q = wave + G_WAVES * i;
-        if (q < G_B_CHUNKS) {  // wave-uniform
-            const int pc = min(64 * q + lane, G_BN * 9 - 1);
-            const int row = pc / 9, piece = pc - row * 9;
-            const int grow = min(n0 + row, n - 1);
-            lds_load16(W + grow * rowbytes + sb * Q4K_BYTES + 16 * piece, B + 1024 * q);
-        }
+        if (q < G_B_CHUNKS) lds_load16(wb + o.b[i], B + 1024 * q);  // wave-uniform
     }
-    if (wave < 2) {
-        const int row = 64 * wave + lane;
-        const int grow = min(m0 + row, m - 1);
-        lds_load16(sp + ((int64_t)grow * nsb + sb) * 16, S + 1024 * wave);
-    } else {
-        const int row = 64 * (wave - 2) + lane;
-        const int grow = min(m0 + row, m - 1);
-        lds_load4(dyt + (int64_t)sb * m + grow, D + 256 * (wave - 2));
-    }
+    if (wave < 2) lds_load16(sp + sb * 16 + o.sd, S + 1024 * wave);
+    else lds_load4((const uint8_t*)(dyt + (int64_t)sb * m) + o.sd, D + 256 * (wave - 2));
 }
 
 // All of this wave's queued LDS loads have landed; then the barrier makes
-// every wave's share visible.
+// every wave's share visible.  The scheduling barrier keeps the compute of
+// the current stage ahead of the wait: the asm orders memory operations
+// only, and without it the MFMAs drift below the wait and the next stage's
+// load latency is no longer hidden.
 __device__ __forceinline__ void stage_wait() {
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 }
@@ -203,7 +239,8 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
 #pragma unroll
             for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
 
-    stage_issue(smem, xq, sp, dyt, W, m0, n0, m, n, k, 0);
+    const StageOffs so = stage_offsets(m0, n0, m, n, k);
+    stage_issue(smem, xq, sp, dyt, W, so, m, 0);
     stage_wait();
 
     for (int sb = 0; sb < nsb; sb++) {
@@ -238,7 +275,7 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
             for (int g = 0; g < 4; g++) dy[a][g] = *(const float4*)(dyp + 8 * g);
         }
         // 2. queue the next superblock into the other stage
-        if (sb + 1 < nsb) stage_issue(smem + ((sb + 1) & 1) * G_STAGE, xq, sp, dyt, W, m0, n0, m, n, k, sb + 1);
+        if (sb + 1 < nsb) stage_issue(smem + ((sb + 1) & 1) * G_STAGE, xq, sp, dyt, W, so, m, sb + 1);
 
         // 3. the MFMA work, from registers
         v16i dh[G_MT][G_NT], dl[G_MT][G_NT];
@@ -255,8 +292,11 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
                 const uint32_t q0 = (raw[b][c].x >> sh) & 0x0F0F0F0Fu, q1 = (raw[b][c].y >> sh) & 0x0F0F0F0Fu,
                                q2 = (raw[b][c].z >> sh) & 0x0F0F0F0Fu, q3 = (raw[b][c].w >> sh) & 0x0F0F0F0Fu;
                 const uint32_t shi = (uint32_t)sc >> 3, slo = (uint32_t)sc & 7u;
-                const v4i bhi = {(int)(q0 * shi), (int)(q1 * shi), (int)(q2 * shi), (int)(q3 * shi)};
-                const v4i blo = {(int)(q0 * slo), (int)(q1 * slo), (int)(q2 * slo), (int)(q3 * slo)};
+                // four nibble bytes times a 3-bit factor: at most 105 per byte,
+                // so one packed 16-bit multiply (v_pk_mul_lo_u16, full rate)
+                // scales two bytes per half with no carry between them
+                const v4i bhi = {pk_mul_u16(q0, shi), pk_mul_u16(q1, shi), pk_mul_u16(q2, shi), pk_mul_u16(q3, shi)};
+                const v4i blo = {pk_mul_u16(q0, slo), pk_mul_u16(q1, slo), pk_mul_u16(q2, slo), pk_mul_u16(q3, slo)};
 #pragma unroll
                 for (int a = 0; a < G_MT; a++) {
                     if (j == 0) {
@@ -321,19 +361,70 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
         }
 }
 
-// ------------------------------------------------ Q4_K GEMM on fp16 MFMA --
-// The same product with both operands dequantized to fp16 (activations as
-// f16(dy * q8) of the bit-exact Q8_K quantization, weights as f16 of
-// d*sc*q - dmin*m) and v_mfma_f32_32x32x16_f16 accumulating all of K in f32:
-// no per-superblock epilogue at all, at half the int8 MFMA rate.  The
-// operand rounding (11 significant bits) costs about 1e-4 of a typical
-// output, which keeps a wide row inside the 1e-3 * max|y row| tolerance but
-// not a row of a handful of outputs near zero: opt-in, not the default.
+// ------------------------------------- Q4_K GEMM on exact fp16 MFMA --
+// The same integer sums with the operands in fp16: the quantized
+// activations x8 (|x8| <= 127) and the scaled weights sc * q (<= 945) are
+// integers fp16 holds exactly, every product is exact, and
+// v_mfma_f32_32x32x16_f16 accumulates a superblock's 256 products per output
+// in f32 (partial sums stay below 2^25, so at worst the last bit of a sum
+// past 2^24 is rounded).  One MFMA chain instead of the int8 kernel's two
+// (hi and lo scale planes), at half the int8 rate: the same MFMA time, but
+// the superblock result is f32 already.  The min term is one more MFMA per
+// tile and superblock with operands [S_hi | S_lo] (activation side, S_j =
+// 64 S_hi + S_lo) and [64 m | m] (weight side; 64 m is exact in fp16 too),
+// so the f32 epilogue per output and superblock is three instructions:
+//     out += dy * (d * D - dmin * Dmin)
+//
+// Tiling: 512 threads = 4 x 2 waves, a 256 x 128 block of y, each wave
+// 2 x 2 tiles of 32 x 32.  K moves in steps of 64 (a quarter superblock),
+// double buffered in LDS: the activation tile arrives by global_load_lds
+// (prepared as fp16 by k_gemm_prep_x16), the weight tile is built from the
+// packed Q4_K bytes by the workgroup (sc * q to fp16, two values per packed
+// 16-bit multiply).  Inside each 64-element step the k order is the one the
+// weight builder produces naturally (element e at slot e with bits 0 and 1
+// swapped); the activation prep writes the same order, and an MFMA never
+// depends on the order of k.
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// x f32 [m][k] -> Q8_K (bit-exact) -> f16(d * q) [m][k]
-__global__ __launch_bounds__(256) void k_gemm_prep_f16(const float* __restrict__ x, _Float16* __restrict__ xh, int m,
+constexpr int X_BM = 256, X_BN = 128, X_BK = 64;
+constexpr int X_WAVES = 8, X_THREADS = 64 * X_WAVES;
+constexpr int X_A_BYTES = X_BM * X_BK * 2;   // 32 KB
+constexpr int X_B_BYTES = X_BN * X_BK * 2;   // 16 KB
+constexpr int X_STAGE = X_A_BYTES + X_B_BYTES;
+constexpr int X_SB_BYTES = X_BM * 32 + X_BM * 4;  // per superblock: min operands, dy
+constexpr int X_LDS = 2 * X_STAGE + 2 * X_SB_BYTES;
+
+// Row r of a [rows][64 halves] tile: 8 pieces of 16 bytes, piece p at
+// position p ^ (r & 7) (rows that read one piece hit eight bank groups).
+__device__ __forceinline__ int x_pos(int row, int piece) { return row * 128 + 16 * (piece ^ (row & 7)); }
+
+// Activation prep: Q8_K of every (row, superblock), bit-exact, into
+//   x16  fp16 [m][k]       x8, each 64-element step in slot order
+//   amin fp16 [m][k/256][16]  S_hi[0..8) then S_lo[0..8)
+//   dyt  f32  [k/256][m]
+struct X16Ptrs {
+    _Float16* x16;
+    _Float16* amin;
+    float* dyt;
+};
+static X16Ptrs x16_ptrs(void* base, int64_t m, int64_t k) {
+    const size_t a = ((size_t)m * k * 2 + 255) & ~(size_t)255;
+    const size_t b = ((size_t)m * (k / 256) * 32 + 255) & ~(size_t)255;
+    X16Ptrs p;
+    p.x16 = (_Float16*)base;
+    p.amin = (_Float16*)((uint8_t*)base + a);
+    p.dyt = (float*)((uint8_t*)base + a + b);
+    return p;
+}
+static size_t x16_bytes(int64_t m, int64_t k) {
+    const size_t a = ((size_t)m * k * 2 + 255) & ~(size_t)255;
+    const size_t b = ((size_t)m * (k / 256) * 32 + 255) & ~(size_t)255;
+    return a + b + (size_t)(k / 256) * m * sizeof(float) + 256;
+}
+
+__global__ __launch_bounds__(256) void k_gemm_prep_x16(const float* __restrict__ x, _Float16* __restrict__ x16,
+                                                       _Float16* __restrict__ amin, float* __restrict__ dyt, int m,
                                                        int k) {
     const int lane = threadIdx.x & 63;
     const int nsb = k >> 8;
@@ -344,140 +435,225 @@ __global__ __launch_bounds__(256) void k_gemm_prep_f16(const float* __restrict__
     float d;
     int bs;
     const uint32_t q = q8k_block_wave(v, &d, &bs);
-    uint2 out;
-    out.x = (uint32_t)f32_to_f16(d * (float)(int8_t)(q & 0xff)) |
-            ((uint32_t)f32_to_f16(d * (float)(int8_t)((q >> 8) & 0xff)) << 16);
-    out.y = (uint32_t)f32_to_f16(d * (float)(int8_t)((q >> 16) & 0xff)) |
-            ((uint32_t)f32_to_f16(d * (float)(int8_t)(q >> 24)) << 16);
-    *(uint2*)(xh + (int64_t)mi * k + sb * 256 + 4 * lane) = out;
+    // elements 4l .. 4l+3 go to slots 4l, 4l+2, 4l+1, 4l+3 (bits 0, 1 swapped)
+    const _Float16 h0 = (_Float16)(float)(int8_t)(q & 0xff), h1 = (_Float16)(float)(int8_t)((q >> 8) & 0xff);
+    const _Float16 h2 = (_Float16)(float)(int8_t)((q >> 16) & 0xff), h3 = (_Float16)(float)(int8_t)(q >> 24);
+    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+    const v4h o = {h0, h2, h1, h3};
+    *(v4h*)(x16 + (int64_t)mi * k + sb * 256 + 4 * lane) = o;
+    const int S = bs + __shfl_xor(bs, 4, 64);  // S_j on lanes 8j .. 8j+7
+    if ((lane & 7) == 0) {
+        const int j = lane >> 3;
+        _Float16* a = amin + ((int64_t)mi * nsb + sb) * 16;
+        a[j] = (_Float16)(float)(S >> 6);        // S_hi in [-64, 63]
+        a[8 + j] = (_Float16)(float)(S & 63);    // S_lo in [0, 63]
+    }
+    if (lane == 0) dyt[(int64_t)sb * m + mi] = d;
 }
 
-constexpr int H_BM = 128, H_BN = 128, H_BK = 64;
-constexpr int H_THREADS = 256;
-constexpr int H_TILE = H_BM * H_BK * 2;  // bytes of one A (or B) stage: 16 KB
-// LDS stage = A tile then B tile, each [128 rows][8 pieces of 8 halves],
-// piece p of row r at position p ^ (r & 7).
-__device__ __forceinline__ int h_pos(int row, int piece) { return row * 128 + 16 * (piece ^ (row & 7)); }
+// Each 16-bit half of a times the 16-bit f: sc * q stays below 2^16.
+__device__ __forceinline__ uint32_t pk_mul16(uint32_t a, uint32_t f2) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, f2));
+}
+// Two 16-bit integers v < 1024 to fp16: 0x6400 | v is the fp16 1024 + v
+// exactly; subtracting 1024 (packed fp16) leaves v exactly.
+__device__ __forceinline__ uint32_t u16x2_to_h2(uint32_t v) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 t = __builtin_bit_cast(h2, v | 0x64006400u);
+    const h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    return __builtin_bit_cast(uint32_t, t - off);
+}
+// Eight nibbles (one per byte of w0, w1, already masked to 0..15) times sc,
+// as one 16-byte piece of fp16 in slot order [e0 e2 e1 e3 e4 e6 e5 e7].
+__device__ __forceinline__ uint4 nib8_to_piece(uint32_t w0, uint32_t w1, uint32_t sc2) {
+    uint4 r;
+    r.x = u16x2_to_h2(pk_mul16(w0 & 0x00FF00FFu, sc2));
+    r.y = u16x2_to_h2(pk_mul16((w0 >> 8) & 0x00FF00FFu, sc2));
+    r.z = u16x2_to_h2(pk_mul16(w1 & 0x00FF00FFu, sc2));
+    r.w = u16x2_to_h2(pk_mul16((w1 >> 8) & 0x00FF00FFu, sc2));
+    return r;
+}
 
-__global__ __launch_bounds__(H_THREADS) void k_gemm_q4k_f16(const uint8_t* __restrict__ W,
-                                                            const _Float16* __restrict__ xh, float* __restrict__ Y,
+__global__ __launch_bounds__(X_THREADS) void k_gemm_q4k_x16(const uint8_t* __restrict__ W,
+                                                            const _Float16* __restrict__ x16,
+                                                            const _Float16* __restrict__ amin,
+                                                            const float* __restrict__ dyt, float* __restrict__ Y,
                                                             int m, int n, int k) {
-    __shared__ __align__(16) uint8_t smem[2][2 * H_TILE];
+    extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves, 64 x 64 each
     const int h = lane >> 5, c32 = lane & 31;
     int bm, bn;
-    tile_of((m + H_BM - 1) / H_BM, (n + H_BN - 1) / H_BN, bm, bn);
-    const int m0 = bm * H_BM, n0 = bn * H_BN;
-    const int nsteps = k / H_BK;
-    const int64_t rowbytes = (int64_t)(k >> 8) * Q4K_BYTES;
+    tile_of((m + X_BM - 1) / X_BM, (n + X_BN - 1) / X_BN, bm, bn);
+    const int m0 = bm * X_BM, n0 = bn * X_BN;
+    const int nsb = k >> 8, nsteps = nsb * 4;
+    const uint32_t rowbytes = (uint32_t)nsb * Q4K_BYTES;
+    uint8_t* sbbuf = smem + 2 * X_STAGE;  // [2][X_SB_BYTES]
 
-    // weight dequant role: thread -> (row, half of the 32 qs bytes of a chunk)
-    const int brow = t >> 1, bhalf = t & 1;
-    const uint8_t* wrow = W + (int64_t)min(n0 + brow, n - 1) * rowbytes;
-    // activation DMA role: wave w moves chunks 4w..4w+3 (8 rows x 8 pieces each)
-    auto issue_a = [&](uint8_t* stage, int step) {
+    // weight builder role: thread -> (row, part): bytes 8 part .. +8 of the
+    // step's 32 qs bytes: low nibbles = slots of piece part, high = part + 4
+    const int brow = t >> 2, bpart = t & 3;
+    const uint8_t* wrow = W + (uint32_t)min(n0 + brow, n - 1) * rowbytes;
+    // activation DMA: 32 chunks of 1 KB (8 rows x 128 B) per stage, 4 per wave
+    uint32_t aoff[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int q = wave * 4 + i;
-            const int row = 8 * q + (lane >> 3);
-            const int piece = (lane & 7) ^ (row & 7);
-            const int grow = min(m0 + row, m - 1);
-            __builtin_amdgcn_global_load_lds(xh + (int64_t)grow * k + step * H_BK + 8 * piece,
-                                             (__attribute__((address_space(3))) void*)(stage + 1024 * q), 16, 0, 0);
+    for (int i = 0; i < 4; i++) {
+        const int q = wave * 4 + i;
+        const int row = 8 * q + (lane >> 3);
+        const int piece = (lane & 7) ^ (row & 7);
+        aoff[i] = (uint32_t)min(m0 + row, m - 1) * (uint32_t)k * 2u + 16u * piece;
+    }
+    // per-superblock operands: min-term A rows (32 B each) and dy (4 B each)
+    // for the 256 rows, by DMA: 8 KB + 1 KB
+    const uint32_t srow = (uint32_t)min(m0 + t / 2, m - 1);
+
+    auto issue_a = [&](int step) {
+        uint8_t* A = smem + (step & 1) * X_STAGE;
+        const uint8_t* base = (const uint8_t*)x16 + (uint32_t)step * (X_BK * 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_global_load_lds(base + aoff[i], (lds_void*)(A + 1024 * (wave * 4 + i)), 16, 0, 0);
+    };
+    auto issue_sb = [&](int sb) {
+        uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES;
+        // 512 threads x 16 B = the 256 rows' 32-byte min operands
+        const uint8_t* ab = (const uint8_t*)amin + ((uint64_t)srow * nsb + sb) * 32 + 16 * (t & 1);
+        __builtin_amdgcn_global_load_lds(ab, (lds_void*)(SB + 1024 * wave), 16, 0, 0);
+        if (wave < 4) {
+            const int row = 64 * wave + lane;
+            const float* dp = dyt + (int64_t)sb * m + min(m0 + row, m - 1);
+            __builtin_amdgcn_global_load_lds(dp, (lds_void*)(SB + X_BM * 32 + 256 * wave), 4, 0, 0);
         }
     };
-    auto dequant_b = [&](uint8_t* stage, const uint4& hdr, const uint4& raw, int step) {
+    auto load_b = [&](int step) -> uint2 {
+        const int sb = step >> 2, c = step & 3;
+        return *(const uint2*)(wrow + sb * Q4K_BYTES + 16 + 32 * c + 8 * bpart);
+    };
+    auto build_b = [&](int step, uint2 raw, const uint4& hdr) {
+        uint8_t* B = smem + (step & 1) * X_STAGE + X_A_BYTES;
         const int c = step & 3;
-        const float d = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
-        int sc0, m0s, sc1, m1s;
-        if (c < 2) {
-            sc0 = byte_of(hdr.y, 2 * c) & 63;
-            m0s = byte_of(hdr.z, 2 * c) & 63;
-            sc1 = byte_of(hdr.y, 2 * c + 1) & 63;
-            m1s = byte_of(hdr.z, 2 * c + 1) & 63;
-        } else {
-            const uint32_t i0 = 2 * c - 4, i1 = 2 * c - 3;
-            sc0 = (byte_of(hdr.w, i0) & 0xF) | ((byte_of(hdr.y, i0) >> 6) << 4);
-            m0s = (byte_of(hdr.w, i0) >> 4) | ((byte_of(hdr.z, i0) >> 6) << 4);
-            sc1 = (byte_of(hdr.w, i1) & 0xF) | ((byte_of(hdr.y, i1) >> 6) << 4);
-            m1s = (byte_of(hdr.w, i1) >> 4) | ((byte_of(hdr.z, i1) >> 6) << 4);
-        }
-        const float d1 = d * (float)sc0, mm1 = dmin * (float)m0s;
-        const float d2 = d * (float)sc1, mm2 = dmin * (float)m1s;
-        const uint32_t R[4] = {raw.x, raw.y, raw.z, raw.w};
-        uint32_t lo[8], hi[8];  // 16 halves each, packed in pairs
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t wl = R[i] & 0x0F0F0F0Fu, wh = (R[i] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-                const _Float16 l0 = (_Float16)(d1 * (float)byte_of(wl, e) - mm1);
-                const _Float16 l1 = (_Float16)(d1 * (float)byte_of(wl, e + 1) - mm1);
-                const _Float16 h0 = (_Float16)(d2 * (float)byte_of(wh, e) - mm2);
-                const _Float16 h1 = (_Float16)(d2 * (float)byte_of(wh, e + 1) - mm2);
-                lo[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-                hi[2 * i + e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-            }
-        }
-        uint8_t* B = stage + H_TILE;
-        // sub-block 2c -> k 0..31 (pieces 0..3), sub-block 2c+1 -> k 32..63 (pieces 4..7)
-        *(uint4*)(B + h_pos(brow, 2 * bhalf)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        *(uint4*)(B + h_pos(brow, 2 * bhalf + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-        *(uint4*)(B + h_pos(brow, 4 + 2 * bhalf)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *(uint4*)(B + h_pos(brow, 4 + 2 * bhalf + 1)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+        // scales of sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles)
+        const uint64_t sc8 = (uint64_t)(hdr.y & 0x3F3F3F3Fu) |
+                             ((uint64_t)((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u)) << 32);
+        const uint32_t scp = (uint32_t)(sc8 >> (16 * c));
+        const uint32_t s0 = scp & 0xffu, s1 = (scp >> 8) & 0xffu;
+        const uint4 lo = nib8_to_piece(raw.x & 0x0F0F0F0Fu, raw.y & 0x0F0F0F0Fu, s0 * 0x10001u);
+        const uint4 hi = nib8_to_piece((raw.x >> 4) & 0x0F0F0F0Fu, (raw.y >> 4) & 0x0F0F0F0Fu, s1 * 0x10001u);
+        *(uint4*)(B + x_pos(brow, bpart)) = lo;
+        *(uint4*)(B + x_pos(brow, 4 + bpart)) = hi;
     };
 
-    v16f acc[2][2];
+    v16f acc[2][2], out[2][2];
 #pragma unroll
     for (int a = 0; a < 2; a++)
 #pragma unroll
         for (int b = 0; b < 2; b++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
+            for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
 
-    uint4 hdr = *(const uint4*)wrow;
-    uint4 raw = *(const uint4*)(wrow + 16 + 16 * bhalf);
-    issue_a(smem[0], 0);
-    dequant_b(smem[0], hdr, raw, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // prologue: step 0 into stage 0, superblock 0 operands
+    uint4 bhdr = *(const uint4*)wrow, nhdr = bhdr, ehdr[2];
+    uint2 braw = load_b(0);
+    issue_a(0);
+    issue_sb(0);
+    build_b(0, braw, bhdr);
+    braw = load_b(nsteps > 1 ? 1 : 0);
+    asm volatile("s_waitcnt vmcnt(1)" ::: "memory");  // all but the next raw load
     __syncthreads();
 
     for (int s = 0; s < nsteps; s++) {
-        const uint8_t* A = smem[s & 1];
-        const uint8_t* B = smem[s & 1] + H_TILE;
-        // operands of this step, LDS -> registers, before the next stage is queued
+        const int sb = s >> 2, c = s & 3;
+        const uint8_t* A = smem + (s & 1) * X_STAGE;
+        const uint8_t* B = A + X_A_BYTES;
+        // 1. this step's operands, LDS -> registers
         v8h av[2][4], bv[2][4];
 #pragma unroll
         for (int a = 0; a < 2; a++) {
             const int row = wm * 64 + a * 32 + c32;
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) av[a][kk] = *(const v8h*)(A + h_pos(row, 2 * kk + h));
+            for (int kk = 0; kk < 4; kk++) av[a][kk] = *(const v8h*)(A + x_pos(row, 2 * kk + h));
         }
 #pragma unroll
         for (int b = 0; b < 2; b++) {
             const int row = wn * 64 + b * 32 + c32;
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) bv[b][kk] = *(const v8h*)(B + h_pos(row, 2 * kk + h));
+            for (int kk = 0; kk < 4; kk++) bv[b][kk] = *(const v8h*)(B + x_pos(row, 2 * kk + h));
         }
+        // 2. queue the next step: activation DMA, next superblock's operands
         const bool more = s + 1 < nsteps;
         if (more) {
-            issue_a(smem[(s + 1) & 1], s + 1);
-            const int sb = (s + 1) >> 2, c = (s + 1) & 3;
-            if (c == 0) hdr = *(const uint4*)(wrow + sb * Q4K_BYTES);
-            raw = *(const uint4*)(wrow + sb * Q4K_BYTES + 16 + 32 * c + 16 * bhalf);
+            issue_a(s + 1);
+            if (c == 3) issue_sb(sb + 1);
         }
+        // at a superblock's first step: the next superblock's header for the
+        // weight builder, this superblock's column headers for the epilogue
+        if (c == 0) {
+            nhdr = *(const uint4*)(wrow + min(sb + 1, nsb - 1) * Q4K_BYTES);
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+                ehdr[b] = *(const uint4*)(W + (uint32_t)min(n0 + wn * 64 + b * 32 + c32, n - 1) * rowbytes +
+                                          sb * Q4K_BYTES);
+        }
+        const uint2 nraw = load_b(s + 2 < nsteps ? s + 2 : s + 1 < nsteps ? s + 1 : s);
+        __builtin_amdgcn_sched_barrier(0);
+        // 3. MFMA: 4 k16 slices x 2 x 2 tiles
 #pragma unroll
         for (int kk = 0; kk < 4; kk++)
 #pragma unroll
             for (int a = 0; a < 2; a++)
 #pragma unroll
-                for (int b = 0; b < 2; b++)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[b][kk], acc[a][b], 0, 0, 0);
-        if (more) dequant_b(smem[(s + 1) & 1], hdr, raw, s + 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                for (int b = 0; b < 2; b++) {
+                    if (c == 0 && kk == 0) {
+                        const v16f z = {};
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[b][kk], z, 0, 0, 0);
+                    } else {
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[b][kk], acc[a][b], 0, 0, 0);
+                    }
+                }
+        // 4. build the next step's weight tile into the other stage
+        if (more) build_b(s + 1, braw, c == 3 ? nhdr : bhdr);
+        braw = nraw;
+        // 5. superblock epilogue
+        if (c == 3) {
+            const uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                // this lane's column: d, dmin and the mins as [64 m | m]
+                const uint4 eh = ehdr[b];
+                const float d = f16_to_f32(eh.x & 0xffffu), dmin = f16_to_f32(eh.x >> 16);
+                const uint64_t m8 = (uint64_t)(eh.z & 0x3F3F3F3Fu) |
+                                    ((uint64_t)(((eh.w >> 4) & 0x0F0F0F0Fu) | ((eh.z >> 2) & 0x30303030u)) << 32);
+                v8h bm;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
+                    bm[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
+                }
+#pragma unroll
+                for (int a = 0; a < 2; a++) {
+                    const int row = wm * 64 + a * 32 + c32;
+                    const v8h am = *(const v8h*)(SB + row * 32 + 16 * h);
+                    const v16f z = {};
+                    const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, z, 0, 0, 0);
+                    const float* dyp = (const float*)(SB + X_BM * 32) + wm * 64 + a * 32 + 4 * h;
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const float4 dy4 = *(const float4*)(dyp + 8 * g);
+                        const float dys[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const int r = 4 * g + u;
+                            out[a][b][r] += dys[u] * (d * acc[a][b][r] - dmin * dm[r]);
+                        }
+                    }
+                }
+            }
+        }
+        if (c == 3) bhdr = nhdr;
+        // 6. the next stage has landed and is visible: wait for everything
+        //    but the raw weight load just queued (issued last)
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
         __syncthreads();
     }
 #pragma unroll
@@ -489,35 +665,47 @@ __global__ __launch_bounds__(H_THREADS) void k_gemm_q4k_f16(const uint8_t* __res
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < m) Y[(int64_t)row * n + col] = acc[a][b][r];
+                if (row < m) Y[(int64_t)row * n + col] = out[a][b][r];
             }
         }
 }
 
 // ------------------------------------------------------------ dispatch --
 
+// The kernels index activations and weights with 32-bit byte offsets.
+static bool fits_32bit(int64_t n, int64_t k, int64_t m) {
+    const int64_t rowbytes = (k / 256) * Q4K_BYTES;
+    return n * rowbytes < ((int64_t)1 << 31) && m * k * 2 < ((int64_t)1 << 31) &&
+           m * (k / 256) * 32 < ((int64_t)1 << 31);
+}
+
 size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
-    if (type == T_Q4K) {
-        const size_t f16 = ((size_t)m * k * 2 + 255) & ~(size_t)255;
-        return mode == GEMM_INT8 ? prep_bytes(m, k) : f16;
-    }
-    return matvec_workspace_bytes(type, k, 16);
+    if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
+    return matvec_workspace_bytes(type == T_Q4K ? T_Q6K : type, k, 16);
 }
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, int mode, hipStream_t s) {
-    if (type == T_Q4K && mode != GEMM_INT8) {
-        _Float16* xh = (_Float16*)qbuf;
+    if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
+        static bool attr_set = false;
+        if (!attr_set) {
+            hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k_x16,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, X_LDS);
+            if (e != hipSuccess) return e;
+            attr_set = true;
+        }
+        X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
-        hipLaunchKernelGGL(k_gemm_prep_f16, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, xh, (int)m, (int)k);
+        hipLaunchKernelGGL(k_gemm_prep_x16, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.x16, p.amin,
+                           p.dyt, (int)m, (int)k);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        const unsigned grid = (unsigned)(((m + H_BM - 1) / H_BM) * ((n + H_BN - 1) / H_BN));
-        hipLaunchKernelGGL(k_gemm_q4k_f16, dim3(grid), dim3(H_THREADS), 0, s, (const uint8_t*)w, xh, y, (int)m,
-                           (int)n, (int)k);
+        const unsigned grid = (unsigned)(((m + X_BM - 1) / X_BM) * ((n + X_BN - 1) / X_BN));
+        hipLaunchKernelGGL(k_gemm_q4k_x16, dim3(grid), dim3(X_THREADS), X_LDS, s, (const uint8_t*)w, p.x16, p.amin,
+                           p.dyt, y, (int)m, (int)n, (int)k);
         return hipGetLastError();
     }
-    if (type == T_Q4K) {
+    if (type == T_Q4K && fits_32bit(n, k, m)) {
         static bool attr_set = false;
         if (!attr_set) {
             hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -536,7 +724,8 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                            y, (int)m, (int)n, (int)k);
         return hipGetLastError();
     }
-    // Q8_0 / Q6_K: tiles of 16 activation rows through the decode kernels
+    // Q8_0 / Q6_K (and Q4_K past 32-bit offsets): tiles of 16 activation
+    // rows through the decode kernels
     for (int64_t r = 0; r < m; r += 16) {
         const int64_t mm = m - r < 16 ? m - r : 16;
         hipError_t e = launch_matvec(type, w, x + r * k, y + r * n, n, k, mm, qbuf, s);

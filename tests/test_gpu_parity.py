@@ -142,13 +142,10 @@ GEMM_SHAPES = [(17, 1, 256), (64, 128, 2048), (100, 7, 768), (128, 300, 512), (2
                (257, 64, 256), (512, 256, 2048)]
 
 
-@pytest.mark.parametrize("m,n,k,mma", [s + ("int8",) for s in GEMM_SHAPES] +
-                         [s + ("f16",) for s in GEMM_SHAPES if s[1] >= 128])
+@pytest.mark.parametrize("m,n,k,mma", [s + (mma,) for s in GEMM_SHAPES for mma in ("f16", "int8")])
 def test_prefill_gemm_q4k_shapes(L, m, n, k, mma):
-    """Both prefill GEMMs on ragged tiles (m, n not multiples of 128).  The
-    fp16 one (opt-in) only on rows of >= 128 outputs: its operand rounding
-    is ~1e-4 of a typical output, inside the row-max bound for a wide row but
-    not for a row of a few outputs near zero."""
+    """Both prefill GEMMs (exact fp16 operands, the default, and int8 scale
+    planes) on ragged tiles (m, n not multiples of the tile)."""
     from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
 
     rng = np.random.default_rng(m * 7 + n)
@@ -159,7 +156,7 @@ def test_prefill_gemm_q4k_shapes(L, m, n, k, mma):
     try:
         y, q = _qmm(L, O.Q4K, w, x)
     finally:
-        set_prefill_mma(MMA_INT8)
+        set_prefill_mma(MMA_F16)
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"gemm {mma} m={m} n={n} k={k}")
 
 
