@@ -375,32 +375,47 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
 // so the f32 epilogue per output and superblock is three instructions:
 //     out += dy * (d * D - dmin * Dmin)
 //
-// Tiling: 512 threads = 4 x 2 waves, a 256 x 128 block of y, each wave
+// Tiling: 256 threads = 2 x 2 waves, a 128 x 128 block of y, each wave
 // 2 x 2 tiles of 32 x 32.  K moves in steps of 64 (a quarter superblock),
-// double buffered in LDS: the activation tile arrives by global_load_lds
-// (prepared as fp16 by k_gemm_prep_x16), the weight tile is built from the
-// packed Q4_K bytes by the workgroup (sc * q to fp16, two values per packed
-// 16-bit multiply).  Inside each 64-element step the k order is the one the
-// weight builder produces naturally (element e at slot e with bits 0 and 1
-// swapped); the activation prep writes the same order, and an MFMA never
-// depends on the order of k.
+// three LDS stages deep (two steps in flight).  Everything the loop reads
+// from memory arrives by global_load_lds: the fp16 activation tile (from
+// k_gemm_prep_x16), the step's 32 packed nibble bytes of each weight row,
+// and per superblock the weight headers, the min-term operands and dy.  No
+// load in the loop has a register result, so the only memory waits are the
+// counted ones before each barrier.  A lane builds its weight operands in
+// registers from 16 of its column's bytes, two values per v_pk_fma_f16.
+// Inside each 64-element step the k order is the one the nibble layout
+// gives (element e at slot e with bits 0 and 1 swapped); the activation
+// prep writes the same order, and an MFMA never depends on the order of k.
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int X_BM = 256, X_BN = 128, X_BK = 64;
-constexpr int X_WAVES = 8, X_THREADS = 64 * X_WAVES;
-constexpr int X_A_BYTES = X_BM * X_BK * 2;   // 32 KB
-constexpr int X_B_BYTES = X_BN * X_BK * 2;   // 16 KB
-constexpr int X_STAGE = X_A_BYTES + X_B_BYTES;
-constexpr int X_SB_BYTES = X_BM * 32 + X_BM * 4;  // per superblock: min operands, dy
-constexpr int X_LDS = 2 * X_STAGE + 2 * X_SB_BYTES;
+constexpr int X_BM = 128, X_BN = 128, X_BK = 64;
+constexpr int X_WAVES = 4, X_THREADS = 64 * X_WAVES;
+constexpr int X_MT = 2, X_NT = 2;  // 32 x 32 tiles per wave
+constexpr int X_STAGES = 4;
+constexpr int X_A_BYTES = X_BM * X_BK * 2;  // 16 KB: 16 DMA chunks of 1 KB
+constexpr int X_R_BYTES = X_BN * 32;        // 4 KB: the step's qs bytes of 128 rows
+constexpr int X_STAGE = X_A_BYTES + X_R_BYTES;
+constexpr int X_A_PER_WAVE = X_A_BYTES / 1024 / X_WAVES;  // 4
+// per superblock: min operands [X_BM][32 B], dy [X_BM] f32 (256 B per wave),
+// weight headers [X_BN][16 B] (1 KB per wave: lanes 32..63 reload lanes 0..31's
+// columns into a copy nobody reads, so every wave issues the same loads)
+constexpr int X_SB_AMIN = 0, X_SB_DY = X_BM * 32, X_SB_HDR = X_SB_DY + 256 * X_WAVES;
+constexpr int X_SB_BYTES = X_SB_HDR + 1024 * X_WAVES;
+constexpr int X_LDS = X_STAGES * X_STAGE + 2 * X_SB_BYTES;
+// DMA loads per wave: per step A + raw, per superblock min operands + dy + headers
+constexpr int X_DMA_STEP = X_A_PER_WAVE + 1;
+constexpr int X_DMA_SB = X_BM * 32 / 1024 / X_WAVES + 1 + 1;
+static_assert(X_BM * 32 / 1024 / X_WAVES == 1, "one min-operand chunk per wave");
 
 // Row r of a [rows][64 halves] tile: 8 pieces of 16 bytes, piece p at
 // position p ^ (r & 7) (rows that read one piece hit eight bank groups).
 __device__ __forceinline__ int x_pos(int row, int piece) { return row * 128 + 16 * (piece ^ (row & 7)); }
 
 // Activation prep: Q8_K of every (row, superblock), bit-exact, into
-//   x16  fp16 [m][k]       x8, each 64-element step in slot order
+//   x16  fp16 [m][k]          x8, each 64-element step in slot order
 //   amin fp16 [m][k/256][16]  S_hi[0..8) then S_lo[0..8)
 //   dyt  f32  [k/256][m]
 struct X16Ptrs {
@@ -437,41 +452,76 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x16(const float* __restrict__
     const uint32_t q = q8k_block_wave(v, &d, &bs);
     // elements 4l .. 4l+3 go to slots 4l, 4l+2, 4l+1, 4l+3 (bits 0, 1 swapped)
     const _Float16 h0 = (_Float16)(float)(int8_t)(q & 0xff), h1 = (_Float16)(float)(int8_t)((q >> 8) & 0xff);
-    const _Float16 h2 = (_Float16)(float)(int8_t)((q >> 16) & 0xff), h3 = (_Float16)(float)(int8_t)(q >> 24);
+    const _Float16 h2v = (_Float16)(float)(int8_t)((q >> 16) & 0xff), h3 = (_Float16)(float)(int8_t)(q >> 24);
     typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-    const v4h o = {h0, h2, h1, h3};
+    const v4h o = {h0, h2v, h1, h3};
     *(v4h*)(x16 + (int64_t)mi * k + sb * 256 + 4 * lane) = o;
     const int S = bs + __shfl_xor(bs, 4, 64);  // S_j on lanes 8j .. 8j+7
     if ((lane & 7) == 0) {
         const int j = lane >> 3;
         _Float16* a = amin + ((int64_t)mi * nsb + sb) * 16;
-        a[j] = (_Float16)(float)(S >> 6);        // S_hi in [-64, 63]
-        a[8 + j] = (_Float16)(float)(S & 63);    // S_lo in [0, 63]
+        a[j] = (_Float16)(float)(S >> 6);      // S_hi in [-64, 63]
+        a[8 + j] = (_Float16)(float)(S & 63);  // S_lo in [0, 63]
     }
     if (lane == 0) dyt[(int64_t)sb * m + mi] = d;
 }
 
-// Each 16-bit half of a times the 16-bit f: sc * q stays below 2^16.
-__device__ __forceinline__ uint32_t pk_mul16(uint32_t a, uint32_t f2) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, f2));
+// Four nibbles (one per byte of w, each 0..15) times sc, as fp16 in slot
+// order [q0 q2 q1 q3]: v_perm_b32 puts each nibble under the exponent byte
+// 0x64, making the fp16 1024 + q exactly, and one packed fma gives
+// (1024 + q) * sc - 1024 * sc = q * sc, exact (q * sc <= 945, rounded once).
+__device__ __forceinline__ uint2 nib4_to_h(uint32_t w, h2 sc, h2 off) {
+    const uint32_t e = __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u);  // [q0, q2]
+    const uint32_t o = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);  // [q1, q3]
+    const h2 ve = __builtin_elementwise_fma(__builtin_bit_cast(h2, e), sc, off);
+    const h2 vo = __builtin_elementwise_fma(__builtin_bit_cast(h2, o), sc, off);
+    return make_uint2(__builtin_bit_cast(uint32_t, ve), __builtin_bit_cast(uint32_t, vo));
 }
-// Two 16-bit integers v < 1024 to fp16: 0x6400 | v is the fp16 1024 + v
-// exactly; subtracting 1024 (packed fp16) leaves v exactly.
-__device__ __forceinline__ uint32_t u16x2_to_h2(uint32_t v) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 t = __builtin_bit_cast(h2, v | 0x64006400u);
-    const h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
-    return __builtin_bit_cast(uint32_t, t - off);
+
+// global_load_lds written as the instruction: the compiler does not see
+// these LDS writes, so it adds no vmcnt(0) in front of later LDS reads it
+// cannot prove disjoint from them; the kernel orders them itself (counted
+// vmcnt waits, then s_barrier).  m0 holds the wave's LDS destination and is
+// set right before each load; nothing else in the kernel uses m0.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
 }
-// Eight nibbles (one per byte of w0, w1, already masked to 0..15) times sc,
-// as one 16-byte piece of fp16 in slot order [e0 e2 e1 e3 e4 e6 e5 e7].
-__device__ __forceinline__ uint4 nib8_to_piece(uint32_t w0, uint32_t w1, uint32_t sc2) {
-    uint4 r;
-    r.x = u16x2_to_h2(pk_mul16(w0 & 0x00FF00FFu, sc2));
-    r.y = u16x2_to_h2(pk_mul16((w0 >> 8) & 0x00FF00FFu, sc2));
-    r.z = u16x2_to_h2(pk_mul16(w1 & 0x00FF00FFu, sc2));
-    r.w = u16x2_to_h2(pk_mul16((w1 >> 8) & 0x00FF00FFu, sc2));
-    return r;
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+
+// MFMA slice kk of a step, lane half h: piece (kk & 1) + 4 (kk >> 1) + 2h,
+// i.e. low nibbles of parts 2h, 2h + 1 (kk 0, 1), then their high nibbles:
+// a lane's weight operands of a step are the 16 contiguous bytes 16h ..
+// 16h+15 of its column's 32.
+__device__ __forceinline__ int x_piece(int kk, int h) { return (kk & 1) + 4 * (kk >> 1) + 2 * h; }
+
+// The weight operands of one step from the lane's 16 bytes: scales of
+// sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles) from the header.
+__device__ __forceinline__ void build_b(const uint4& raw, const uint4& hdr, int c, v8h (&bv)[4]) {
+    const uint64_t sc8 = (uint64_t)(hdr.y & 0x3F3F3F3Fu) |
+                         ((uint64_t)((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u)) << 32);
+    const uint32_t scp = (uint32_t)(sc8 >> (16 * c));
+    const _Float16 s0 = (_Float16)(float)(scp & 0xffu), s1 = (_Float16)(float)((scp >> 8) & 0xffu);
+    const h2 scl = {s0, s0}, sch = {s1, s1};
+    const h2 offl = {(_Float16)(-1024.0f) * s0, (_Float16)(-1024.0f) * s0};
+    const h2 offh = {(_Float16)(-1024.0f) * s1, (_Float16)(-1024.0f) * s1};
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        const uint32_t w0 = kk & 1 ? raw.z : raw.x, w1 = kk & 1 ? raw.w : raw.y;
+        const uint32_t m0w = kk < 2 ? (w0 & 0x0F0F0F0Fu) : ((w0 >> 4) & 0x0F0F0F0Fu);
+        const uint32_t m1w = kk < 2 ? (w1 & 0x0F0F0F0Fu) : ((w1 >> 4) & 0x0F0F0F0Fu);
+        const uint2 p0 = nib4_to_h(m0w, kk < 2 ? scl : sch, kk < 2 ? offl : offh);
+        const uint2 p1 = nib4_to_h(m1w, kk < 2 ? scl : sch, kk < 2 ? offl : offh);
+        bv[kk] = __builtin_bit_cast(v8h, make_uint4(p0.x, p0.y, p1.x, p1.y));
+    }
 }
 
 __global__ __launch_bounds__(X_THREADS) void k_gemm_q4k_x16(const uint8_t* __restrict__ W,
@@ -481,185 +531,199 @@ __global__ __launch_bounds__(X_THREADS) void k_gemm_q4k_x16(const uint8_t* __res
                                                             int m, int n, int k) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves, 64 x 64 each
+    const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, 64 x 64 each
     const int h = lane >> 5, c32 = lane & 31;
     int bm, bn;
     tile_of((m + X_BM - 1) / X_BM, (n + X_BN - 1) / X_BN, bm, bn);
     const int m0 = bm * X_BM, n0 = bn * X_BN;
     const int nsb = k >> 8, nsteps = nsb * 4;
     const uint32_t rowbytes = (uint32_t)nsb * Q4K_BYTES;
-    uint8_t* sbbuf = smem + 2 * X_STAGE;  // [2][X_SB_BYTES]
+    uint8_t* sbbuf = smem + X_STAGES * X_STAGE;  // [2][X_SB_BYTES]
 
-    // weight builder role: thread -> (row, part): bytes 8 part .. +8 of the
-    // step's 32 qs bytes: low nibbles = slots of piece part, high = part + 4
-    const int brow = t >> 2, bpart = t & 3;
-    const uint8_t* wrow = W + (uint32_t)min(n0 + brow, n - 1) * rowbytes;
-    // activation DMA: 32 chunks of 1 KB (8 rows x 128 B) per stage, 4 per wave
-    uint32_t aoff[4];
+    // Per-lane byte offsets, fixed for the whole K loop.
+    // activation DMA: chunk q = 8 rows x 128 B, piece p of row r at position p ^ (r & 7)
+    uint32_t aoff[X_A_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int q = wave * 4 + i;
+    for (int i = 0; i < X_A_PER_WAVE; i++) {
+        const int q = wave * X_A_PER_WAVE + i;
         const int row = 8 * q + (lane >> 3);
         const int piece = (lane & 7) ^ (row & 7);
         aoff[i] = (uint32_t)min(m0 + row, m - 1) * (uint32_t)k * 2u + 16u * piece;
     }
-    // per-superblock operands: min-term A rows (32 B each) and dy (4 B each)
-    // for the 256 rows, by DMA: 8 KB + 1 KB
-    const uint32_t srow = (uint32_t)min(m0 + t / 2, m - 1);
+    // weight-byte DMA: wave w moves columns 32w .. 32w+31; slot (16 B) l
+    // holds half l >> 5 of column 32w + (l & 31), so the 32 lanes reading one
+    // half read 32 consecutive slots
+    const uint32_t colw = (uint32_t)min(n0 + 32 * wave + c32, n - 1) * rowbytes;
+    const uint32_t roff = colw + 16u + 16u * (uint32_t)h;
+    // header DMA: wave w, lanes 0..31 -> columns 32w + lane (lanes 32..63 repeat them)
+    const uint32_t hoff = colw;
+    // min operands: wave w moves rows 32w + lane / 2, halves lane & 1
+    const uint32_t soff = (uint32_t)min(m0 + 32 * wave + (lane >> 1), m - 1) * (uint32_t)nsb * 32u + 16u * (lane & 1);
+    const int dyrow = min(m0 + 64 * wave + lane, m - 1);  // rows past X_BM land in unread padding
 
-    auto issue_a = [&](int step) {
-        uint8_t* A = smem + (step & 1) * X_STAGE;
-        const uint8_t* base = (const uint8_t*)x16 + (uint32_t)step * (X_BK * 2);
+    auto issue_step = [&](int src, int dst) {
+        uint8_t* S = smem + (dst % X_STAGES) * X_STAGE;
+        const uint8_t* ab = (const uint8_t*)x16 + (uint32_t)src * (X_BK * 2);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            __builtin_amdgcn_global_load_lds(base + aoff[i], (lds_void*)(A + 1024 * (wave * 4 + i)), 16, 0, 0);
+        for (int i = 0; i < X_A_PER_WAVE; i++) dma16(ab + aoff[i], lds_addr(S + 1024 * (wave * X_A_PER_WAVE + i)));
+        const uint8_t* rb = W + (uint32_t)(src >> 2) * Q4K_BYTES + 32u * (src & 3);
+        dma16(rb + roff, lds_addr(S + X_A_BYTES + 1024 * wave));
     };
     auto issue_sb = [&](int sb) {
         uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES;
-        // 512 threads x 16 B = the 256 rows' 32-byte min operands
-        const uint8_t* ab = (const uint8_t*)amin + ((uint64_t)srow * nsb + sb) * 32 + 16 * (t & 1);
-        __builtin_amdgcn_global_load_lds(ab, (lds_void*)(SB + 1024 * wave), 16, 0, 0);
-        if (wave < 4) {
-            const int row = 64 * wave + lane;
-            const float* dp = dyt + (int64_t)sb * m + min(m0 + row, m - 1);
-            __builtin_amdgcn_global_load_lds(dp, (lds_void*)(SB + X_BM * 32 + 256 * wave), 4, 0, 0);
-        }
+        dma16((const uint8_t*)amin + (uint32_t)sb * 32u + soff, lds_addr(SB + X_SB_AMIN + 1024 * wave));
+        dma4(dyt + (int64_t)sb * m + dyrow, lds_addr(SB + X_SB_DY + 256 * wave));
+        dma16(W + (uint32_t)sb * Q4K_BYTES + hoff, lds_addr(SB + X_SB_HDR + 1024 * wave));
     };
-    auto load_b = [&](int step) -> uint2 {
-        const int sb = step >> 2, c = step & 3;
-        return *(const uint2*)(wrow + sb * Q4K_BYTES + 16 + 32 * c + 8 * bpart);
+    // this lane's reads of a stage / superblock buffer
+    auto read_raw = [&](int step, uint4 (&r)[X_NT]) {
+        const uint8_t* S = smem + (step % X_STAGES) * X_STAGE + X_A_BYTES;
+#pragma unroll
+        for (int b = 0; b < X_NT; b++) r[b] = *(const uint4*)(S + 1024 * (2 * wn + b) + 16 * (32 * h + c32));
     };
-    auto build_b = [&](int step, uint2 raw, const uint4& hdr) {
-        uint8_t* B = smem + (step & 1) * X_STAGE + X_A_BYTES;
-        const int c = step & 3;
-        // scales of sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles)
-        const uint64_t sc8 = (uint64_t)(hdr.y & 0x3F3F3F3Fu) |
-                             ((uint64_t)((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u)) << 32);
-        const uint32_t scp = (uint32_t)(sc8 >> (16 * c));
-        const uint32_t s0 = scp & 0xffu, s1 = (scp >> 8) & 0xffu;
-        const uint4 lo = nib8_to_piece(raw.x & 0x0F0F0F0Fu, raw.y & 0x0F0F0F0Fu, s0 * 0x10001u);
-        const uint4 hi = nib8_to_piece((raw.x >> 4) & 0x0F0F0F0Fu, (raw.y >> 4) & 0x0F0F0F0Fu, s1 * 0x10001u);
-        *(uint4*)(B + x_pos(brow, bpart)) = lo;
-        *(uint4*)(B + x_pos(brow, 4 + bpart)) = hi;
+    auto read_hdr = [&](int sb, uint4 (&hd)[X_NT]) {
+        const uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES + X_SB_HDR;
+#pragma unroll
+        for (int b = 0; b < X_NT; b++) hd[b] = *(const uint4*)(SB + 1024 * (2 * wn + b) + 16 * c32);
     };
 
-    v16f acc[2][2], out[2][2];
+    v16f acc[X_MT][X_NT], out[X_MT][X_NT];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < X_MT; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int b = 0; b < X_NT; b++)
 #pragma unroll
             for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
 
-    // prologue: step 0 into stage 0, superblock 0 operands
-    uint4 bhdr = *(const uint4*)wrow, nhdr = bhdr, ehdr[2];
-    uint2 braw = load_b(0);
-    issue_a(0);
+    // Order of this wave's DMA loads (vmcnt retires in order; the scheduling
+    // barriers keep the groups in order):
+    //   prologue: step(0), SB(0), step(1), step(2)
+    //   step s:   SB(sb + 1) at a superblock's first step, then step(s + 3)
+    // The last X_DMA_STEP loads of every step are step(s + 3), so
+    // vmcnt(X_DMA_STEP) at its end means everything before has landed:
+    // step(s + 2), whose weight bytes the next step unpacks and whose
+    // activations the step after reads, and SB(sb + 1) queued in this step.
+    // Steps and superblocks past the end reload the last one into buffers
+    // nobody reads again, so the counts never change.  The barriers are bare
+    // s_barrier: __syncthreads() would wait for every load in flight.
+    issue_step(0, 0);
     issue_sb(0);
-    build_b(0, braw, bhdr);
-    braw = load_b(nsteps > 1 ? 1 : 0);
-    asm volatile("s_waitcnt vmcnt(1)" ::: "memory");  // all but the next raw load
-    __syncthreads();
+    issue_step(min(1, nsteps - 1), 1);
+    issue_step(min(2, nsteps - 1), 2);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(X_DMA_STEP) : "memory");  // step(0), SB(0), step(1) landed
+    __builtin_amdgcn_s_barrier();
 
-    for (int s = 0; s < nsteps; s++) {
-        const int sb = s >> 2, c = s & 3;
-        const uint8_t* A = smem + (s & 1) * X_STAGE;
-        const uint8_t* B = A + X_A_BYTES;
-        // 1. this step's operands, LDS -> registers
-        v8h av[2][4], bv[2][4];
+    uint4 hdr[X_NT];
+    read_hdr(0, hdr);
+    v8h bv[2][X_NT][4];  // [step & 1]: operands of the current and the next step
+    {
+        uint4 r0[X_NT];
+        read_raw(0, r0);
 #pragma unroll
-        for (int a = 0; a < 2; a++) {
-            const int row = wm * 64 + a * 32 + c32;
+        for (int b = 0; b < X_NT; b++) build_b(r0[b], hdr[b], 0, bv[0][b]);
+    }
+
+    for (int sb = 0; sb < nsb; sb++) {
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) av[a][kk] = *(const v8h*)(A + x_pos(row, 2 * kk + h));
-        }
+        for (int c = 0; c < 4; c++) {
+            const int s = 4 * sb + c;
+            const uint8_t* S = smem + (s % X_STAGES) * X_STAGE;
+            // 1. the step's LDS reads, before its DMA is queued: activations
+            //    of step s, weight bytes of step s + 1 (and its header at a
+            //    superblock's end), the epilogue's operands
+            v8h av[X_MT][4];
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int row = wn * 64 + b * 32 + c32;
+            for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) bv[b][kk] = *(const v8h*)(B + x_pos(row, 2 * kk + h));
-        }
-        // 2. queue the next step: activation DMA, next superblock's operands
-        const bool more = s + 1 < nsteps;
-        if (more) {
-            issue_a(s + 1);
-            if (c == 3) issue_sb(sb + 1);
-        }
-        // at a superblock's first step: the next superblock's header for the
-        // weight builder, this superblock's column headers for the epilogue
-        if (c == 0) {
-            nhdr = *(const uint4*)(wrow + min(sb + 1, nsb - 1) * Q4K_BYTES);
+                for (int a = 0; a < X_MT; a++)
+                    av[a][kk] = *(const v8h*)(S + x_pos(wm * 64 + a * 32 + c32, x_piece(kk, h)));
+            uint4 rn[X_NT], hn[X_NT];
+            read_raw(s + 1, rn);
+            v8h am[X_MT];
+            float4 dy[X_MT][4];
+            if (c == 3) {
+                read_hdr(sb + 1, hn);
+                const uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES;
 #pragma unroll
-            for (int b = 0; b < 2; b++)
-                ehdr[b] = *(const uint4*)(W + (uint32_t)min(n0 + wn * 64 + b * 32 + c32, n - 1) * rowbytes +
-                                          sb * Q4K_BYTES);
-        }
-        const uint2 nraw = load_b(s + 2 < nsteps ? s + 2 : s + 1 < nsteps ? s + 1 : s);
-        __builtin_amdgcn_sched_barrier(0);
-        // 3. MFMA: 4 k16 slices x 2 x 2 tiles
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++)
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-#pragma unroll
-                for (int b = 0; b < 2; b++) {
-                    if (c == 0 && kk == 0) {
-                        const v16f z = {};
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[b][kk], z, 0, 0, 0);
-                    } else {
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[b][kk], acc[a][b], 0, 0, 0);
-                    }
-                }
-        // 4. build the next step's weight tile into the other stage
-        if (more) build_b(s + 1, braw, c == 3 ? nhdr : bhdr);
-        braw = nraw;
-        // 5. superblock epilogue
-        if (c == 3) {
-            const uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES;
-#pragma unroll
-            for (int b = 0; b < 2; b++) {
-                // this lane's column: d, dmin and the mins as [64 m | m]
-                const uint4 eh = ehdr[b];
-                const float d = f16_to_f32(eh.x & 0xffffu), dmin = f16_to_f32(eh.x >> 16);
-                const uint64_t m8 = (uint64_t)(eh.z & 0x3F3F3F3Fu) |
-                                    ((uint64_t)(((eh.w >> 4) & 0x0F0F0F0Fu) | ((eh.z >> 2) & 0x30303030u)) << 32);
-                v8h bm;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
-                    bm[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
-                }
-#pragma unroll
-                for (int a = 0; a < 2; a++) {
+                for (int a = 0; a < X_MT; a++) {
                     const int row = wm * 64 + a * 32 + c32;
-                    const v8h am = *(const v8h*)(SB + row * 32 + 16 * h);
-                    const v16f z = {};
-                    const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, z, 0, 0, 0);
-                    const float* dyp = (const float*)(SB + X_BM * 32) + wm * 64 + a * 32 + 4 * h;
+                    am[a] = *(const v8h*)(SB + X_SB_AMIN + row * 32 + 16 * h);
+                    const float* dyp = (const float*)(SB + X_SB_DY) + wm * 64 + a * 32 + 4 * h;
 #pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const float4 dy4 = *(const float4*)(dyp + 8 * g);
-                        const float dys[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+                    for (int g = 0; g < 4; g++) dy[a][g] = *(const float4*)(dyp + 8 * g);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // 2. queue: the next superblock's operands (first step), step s + 3
+            if (c == 0) issue_sb(min(sb + 1, nsb - 1));
+            issue_step(min(s + 3, nsteps - 1), s + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            // 3. MFMA on step s, unpacking step s + 1's weights in between
 #pragma unroll
-                        for (int u = 0; u < 4; u++) {
-                            const int r = 4 * g + u;
-                            out[a][b][r] += dys[u] * (d * acc[a][b][r] - dmin * dm[r]);
+            for (int b = 0; b < X_NT; b++) build_b(rn[b], c == 3 ? hn[b] : hdr[b], (c + 1) & 3, bv[(c + 1) & 1][b]);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+                for (int a = 0; a < X_MT; a++)
+#pragma unroll
+                    for (int b = 0; b < X_NT; b++) {
+                        if (kk == 0 && c == 0) {
+                            const v16f z = {};
+                            acc[a][b] =
+                                __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[c & 1][b][kk], z, 0, 0, 0);
+                        } else {
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[c & 1][b][kk],
+                                                                               acc[a][b], 0, 0, 0);
+                        }
+                    }
+            // 4. superblock epilogue: min term on MFMA, then
+            //    out += dy * (d * D - dmin * Dmin)
+            if (c == 3) {
+#pragma unroll
+                for (int b = 0; b < X_NT; b++) {
+                    // this lane's column: d, dmin and the mins as [64 m | m]
+                    const float d = f16_to_f32(hdr[b].x & 0xffffu), dmin = f16_to_f32(hdr[b].x >> 16);
+                    const uint64_t m8 =
+                        (uint64_t)(hdr[b].z & 0x3F3F3F3Fu) |
+                        ((uint64_t)(((hdr[b].w >> 4) & 0x0F0F0F0Fu) | ((hdr[b].z >> 2) & 0x30303030u)) << 32);
+                    v8h bmv;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
+                        bmv[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
+                    }
+#pragma unroll
+                    for (int a = 0; a < X_MT; a++) {
+                        const v16f z = {};
+                        const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[a], bmv, z, 0, 0, 0);
+#pragma unroll
+                        for (int g = 0; g < 4; g++) {
+                            const float dys[4] = {dy[a][g].x, dy[a][g].y, dy[a][g].z, dy[a][g].w};
+#pragma unroll
+                            for (int u = 0; u < 4; u++) {
+                                const int r = 4 * g + u;
+                                out[a][b][r] += dys[u] * (d * acc[a][b][r] - dmin * dm[r]);
+                            }
                         }
                     }
                 }
+#pragma unroll
+                for (int b = 0; b < X_NT; b++) hdr[b] = hn[b];
             }
+            // 5. step s + 2 has landed; every wave is past its reads of step
+            //    s - 1's stage (which step s + 3 overwrites: queued above,
+            //    after this wave's own reads, and the other waves passed
+            //    their reads of it before the previous barrier)
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(X_DMA_STEP) : "memory");
+            __builtin_amdgcn_s_barrier();
         }
-        if (c == 3) bhdr = nhdr;
-        // 6. the next stage has landed and is visible: wait for everything
-        //    but the raw weight load just queued (issued last)
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-        __syncthreads();
     }
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < X_MT; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
+        for (int b = 0; b < X_NT; b++) {
             const int col = n0 + wn * 64 + b * 32 + c32;
             if (col >= n) continue;
 #pragma unroll
