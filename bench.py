@@ -216,7 +216,7 @@ def run_details(L, cu, np, torch, dev, args):
             c3[str(m)] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 2),
                           "i8_peak_frac": round(ops / t / 1e12 / I8_PEAK_TOPS, 4)}
         out["c3_q4k_prefill_" + mode_name] = c3
-    set_prefill_mma(MMA_INT8)
+    set_prefill_mma(MMA_F16)
     # C4 decoder layer decode (q,k,v,o,gate,up in Q4_K; down in Q6_K)
     shapes = [("q", 2048, 2048, 12), ("k", 512, 2048, 12), ("v", 512, 2048, 12), ("o", 2048, 2048, 12),
               ("gate", 8192, 2048, 12), ("up", 8192, 2048, 12), ("down", 2048, 8192, 14)]

@@ -73,15 +73,15 @@ void* lloom_hip_ctx_stream(lloom_hip_ctx* ctx);
  * more rows the MFMA GEMM (default 16, range 1..16).  The reference's knobs
  * are MMVQ_MAX_BATCH (fast_mmvq.rs:38) and qmv.mm_from (tuning.rs:1413). */
 int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows);
-/* Matrix-core family of the Q4_K prefill GEMM (m > mv_rows_max):
- * LLOOM_HIP_MMA_INT8 (default): v_mfma_i32_32x32x32_i8 on the Q8_K
- *   activations and the weights as two int8 planes (sc = 8 sc_hi + sc_lo);
- *   every integer sum exact, f32 per superblock, the CPU arm's contract;
- * LLOOM_HIP_MMA_F16: activations and weights dequantized to fp16 in the
- *   kernel, v_mfma_f32_32x32x16_f16 accumulating all of k in f32; about
- *   1e-4 of a typical output from the fp16 rounding, so a narrow output
- *   row (a few columns near zero) can miss the 1e-3 * max|y row| bound.
- * LLOOM_HIP_PREFILL_MMA=f16 sets the default of new contexts.  No
+/* Matrix-core family of the Q4_K prefill GEMM (m > mv_rows_max).  Both
+ * compute the CPU arm's integer sums exactly (Q8_K activations, per-sub-block
+ * integer scales) and combine them in f32 once per superblock:
+ * LLOOM_HIP_MMA_F16 (default): the integer operands x8 and sc * q, both
+ *   exact in fp16, on v_mfma_f32_32x32x16_f16 (f32 accumulation of exact
+ *   products), the min term as one more MFMA;
+ * LLOOM_HIP_MMA_INT8: v_mfma_i32_32x32x32_i8 with the weights split into
+ *   two int8 planes (sc = 8 sc_hi + sc_lo).
+ * LLOOM_HIP_PREFILL_MMA=int8 sets the default of new contexts.  No
  * counterpart in the reference (its CUDA arm has one MMQ kernel). */
 enum { LLOOM_HIP_MMA_F16 = 0, LLOOM_HIP_MMA_INT8 = 1 };
 int lloom_hip_ctx_set_prefill_mma(lloom_hip_ctx* ctx, int mode);

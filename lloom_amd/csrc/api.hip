@@ -29,7 +29,7 @@ struct lloom_hip_ctx {
     size_t ws_bytes = 0;
     int* flags = nullptr;  // [0] sticky expert-id error
     int mv_rows_max = 16;
-    int prefill_mma = GEMM_INT8;
+    int prefill_mma = GEMM_F16;
     std::mutex mu;
 };
 
@@ -111,7 +111,7 @@ int lloom_hip_ctx_create(int device, lloom_hip_ctx** out) {
     HIP_OK(hipSetDevice(device));
     lloom_hip_ctx* c = new lloom_hip_ctx();
     c->device = device;
-    if (const char* e = getenv("LLOOM_HIP_PREFILL_MMA")) c->prefill_mma = strcmp(e, "f16") == 0 ? GEMM_F16 : GEMM_INT8;
+    if (const char* e = getenv("LLOOM_HIP_PREFILL_MMA")) c->prefill_mma = strcmp(e, "int8") == 0 ? GEMM_INT8 : GEMM_F16;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return fail(LLOOM_HIP_EHIP, "ctx_create: stream creation failed");

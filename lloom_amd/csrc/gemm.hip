@@ -375,40 +375,48 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
 // so the f32 epilogue per output and superblock is three instructions:
 //     out += dy * (d * D - dmin * Dmin)
 //
-// Tiling: 256 threads = 2 x 2 waves, a 128 x 128 block of y, each wave
-// 2 x 2 tiles of 32 x 32.  K moves in steps of 64 (a quarter superblock),
-// three LDS stages deep (two steps in flight).  Everything the loop reads
-// from memory arrives by global_load_lds: the fp16 activation tile (from
-// k_gemm_prep_x16), the step's 32 packed nibble bytes of each weight row,
-// and per superblock the weight headers, the min-term operands and dy.  No
-// load in the loop has a register result, so the only memory waits are the
-// counted ones before each barrier.  A lane builds its weight operands in
-// registers from 16 of its column's bytes, two values per v_pk_fma_f16.
-// Inside each 64-element step the k order is the one the nibble layout
-// gives (element e at slot e with bits 0 and 1 swapped); the activation
-// prep writes the same order, and an MFMA never depends on the order of k.
+// Tiling: 256 threads = 2 x 2 waves, a 256 x 128 block of y, each wave
+// 4 x 2 tiles of 32 x 32 (128 x 64; one wave per SIMD).  K moves in steps
+// of 64 (a quarter superblock).  Everything the loop reads from memory
+// arrives by global_load_lds: the fp16 activation tile (from
+// k_gemm_prep_x16; a ring of three stages), the step's 32 packed nibble
+// bytes of each weight row (a ring of four slots), and per superblock the
+// weight headers, the min-term operands and dy.  No load in the loop has a
+// register result, so the only memory waits are the counted ones before
+// each barrier.  A lane builds its weight operands in registers from 16 of
+// its column's bytes (two values per v_pk_fma_f16), one step ahead, while
+// the MFMAs of the current step run.  Inside each 64-element step the k
+// order is the one the nibble layout gives (element e at slot e with bits
+// 0 and 1 swapped); the activation prep writes the same order, and an MFMA
+// never depends on the order of k.
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int X_BM = 128, X_BN = 128, X_BK = 64;
-constexpr int X_WAVES = 4, X_THREADS = 64 * X_WAVES;
-constexpr int X_MT = 2, X_NT = 2;  // 32 x 32 tiles per wave
-constexpr int X_STAGES = 4;
-constexpr int X_A_BYTES = X_BM * X_BK * 2;  // 16 KB: 16 DMA chunks of 1 KB
-constexpr int X_R_BYTES = X_BN * 32;        // 4 KB: the step's qs bytes of 128 rows
-constexpr int X_STAGE = X_A_BYTES + X_R_BYTES;
-constexpr int X_A_PER_WAVE = X_A_BYTES / 1024 / X_WAVES;  // 4
-// per superblock: min operands [X_BM][32 B], dy [X_BM] f32 (256 B per wave),
-// weight headers [X_BN][16 B] (1 KB per wave: lanes 32..63 reload lanes 0..31's
-// columns into a copy nobody reads, so every wave issues the same loads)
-constexpr int X_SB_AMIN = 0, X_SB_DY = X_BM * 32, X_SB_HDR = X_SB_DY + 256 * X_WAVES;
-constexpr int X_SB_BYTES = X_SB_HDR + 1024 * X_WAVES;
-constexpr int X_LDS = X_STAGES * X_STAGE + 2 * X_SB_BYTES;
-// DMA loads per wave: per step A + raw, per superblock min operands + dy + headers
-constexpr int X_DMA_STEP = X_A_PER_WAVE + 1;
-constexpr int X_DMA_SB = X_BM * 32 / 1024 / X_WAVES + 1 + 1;
-static_assert(X_BM * 32 / 1024 / X_WAVES == 1, "one min-operand chunk per wave");
+// Tile geometry, MT = 32 x 32 tiles per wave along M (2 or 4): a
+// workgroup covers 64 MT rows x 128 columns.
+template <int MT>
+struct XCfg {
+    static constexpr int BM = 64 * MT, BN = 128, BK = 64;
+    static constexpr int WAVES = 4, THREADS = 64 * WAVES, NT = 2;
+    static constexpr int A_STAGES = 3, R_SLOTS = 4;
+    static constexpr int A_BYTES = BM * BK * 2;  // 1 KB DMA chunks
+    static constexpr int R_BYTES = BN * 32;      // the step's qs bytes of 128 rows
+    static constexpr int A_PER_WAVE = A_BYTES / 1024 / WAVES;
+    // per superblock: min operands [BM][32 B], dy [BM] f32 (256 B per
+    // wave), weight headers [BN][16 B] (1 KB per wave: lanes 32..63 reload
+    // lanes 0..31's columns into a copy nobody reads, so every wave issues
+    // the same loads)
+    static constexpr int S_PER_WAVE = BM * 32 / 1024 / WAVES;
+    static constexpr int SB_AMIN = 0, SB_DY = BM * 32, SB_HDR = SB_DY + 256 * WAVES;
+    static constexpr int SB_BYTES = SB_HDR + 1024 * WAVES;
+    static constexpr int R_OFF = A_STAGES * A_BYTES, SB_OFF = R_OFF + R_SLOTS * R_BYTES;
+    static constexpr int LDS = SB_OFF + 2 * SB_BYTES;
+    // loads per wave and step: SB (first step of a superblock), A(s + 2), raw(s + 3)
+    static constexpr int DMA_AFTER_RAW = A_PER_WAVE + 1;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(BM <= 256 && S_PER_WAVE >= 1, "row DMA shares");
+};
 
 // Row r of a [rows][64 halves] tile: 8 pieces of 16 bytes, piece p at
 // position p ^ (r & 7) (rows that read one piece hit eight bank groups).
@@ -524,28 +532,29 @@ __device__ __forceinline__ void build_b(const uint4& raw, const uint4& hdr, int 
     }
 }
 
-__global__ __launch_bounds__(X_THREADS) void k_gemm_q4k_x16(const uint8_t* __restrict__ W,
+template <int MT>
+__global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict__ W,
                                                             const _Float16* __restrict__ x16,
                                                             const _Float16* __restrict__ amin,
                                                             const float* __restrict__ dyt, float* __restrict__ Y,
                                                             int m, int n, int k) {
+    using C = XCfg<MT>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, 64 x 64 each
+    const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, 32 MT x 64 each
     const int h = lane >> 5, c32 = lane & 31;
     int bm, bn;
-    tile_of((m + X_BM - 1) / X_BM, (n + X_BN - 1) / X_BN, bm, bn);
-    const int m0 = bm * X_BM, n0 = bn * X_BN;
+    tile_of((m + C::BM - 1) / C::BM, (n + C::BN - 1) / C::BN, bm, bn);
+    const int m0 = bm * C::BM, n0 = bn * C::BN;
     const int nsb = k >> 8, nsteps = nsb * 4;
     const uint32_t rowbytes = (uint32_t)nsb * Q4K_BYTES;
-    uint8_t* sbbuf = smem + X_STAGES * X_STAGE;  // [2][X_SB_BYTES]
 
     // Per-lane byte offsets, fixed for the whole K loop.
     // activation DMA: chunk q = 8 rows x 128 B, piece p of row r at position p ^ (r & 7)
-    uint32_t aoff[X_A_PER_WAVE];
+    uint32_t aoff[C::A_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < X_A_PER_WAVE; i++) {
-        const int q = wave * X_A_PER_WAVE + i;
+    for (int i = 0; i < C::A_PER_WAVE; i++) {
+        const int q = wave * C::A_PER_WAVE + i;
         const int row = 8 * q + (lane >> 3);
         const int piece = (lane & 7) ^ (row & 7);
         aoff[i] = (uint32_t)min(m0 + row, m - 1) * (uint32_t)k * 2u + 16u * piece;
@@ -555,133 +564,126 @@ __global__ __launch_bounds__(X_THREADS) void k_gemm_q4k_x16(const uint8_t* __res
     // half read 32 consecutive slots
     const uint32_t colw = (uint32_t)min(n0 + 32 * wave + c32, n - 1) * rowbytes;
     const uint32_t roff = colw + 16u + 16u * (uint32_t)h;
-    // header DMA: wave w, lanes 0..31 -> columns 32w + lane (lanes 32..63 repeat them)
-    const uint32_t hoff = colw;
-    // min operands: wave w moves rows 32w + lane / 2, halves lane & 1
-    const uint32_t soff = (uint32_t)min(m0 + 32 * wave + (lane >> 1), m - 1) * (uint32_t)nsb * 32u + 16u * (lane & 1);
-    const int dyrow = min(m0 + 64 * wave + lane, m - 1);  // rows past X_BM land in unread padding
-
-    auto issue_step = [&](int src, int dst) {
-        uint8_t* S = smem + (dst % X_STAGES) * X_STAGE;
-        const uint8_t* ab = (const uint8_t*)x16 + (uint32_t)src * (X_BK * 2);
+    // min operands: wave w moves rows 32 (C::S_PER_WAVE w + i) + lane / 2, halves lane & 1
+    uint32_t soff[C::S_PER_WAVE];
 #pragma unroll
-        for (int i = 0; i < X_A_PER_WAVE; i++) dma16(ab + aoff[i], lds_addr(S + 1024 * (wave * X_A_PER_WAVE + i)));
+    for (int i = 0; i < C::S_PER_WAVE; i++)
+        soff[i] = (uint32_t)min(m0 + 32 * (C::S_PER_WAVE * wave + i) + (lane >> 1), m - 1) * (uint32_t)nsb * 32u +
+                  16u * (lane & 1);
+    const int dyrow = min(m0 + 64 * wave + lane, m - 1);
+
+    auto issue_a = [&](int src, int dst) {
+        uint8_t* A = smem + (dst % C::A_STAGES) * C::A_BYTES;
+        const uint8_t* ab = (const uint8_t*)x16 + (uint32_t)src * (C::BK * 2);
+#pragma unroll
+        for (int i = 0; i < C::A_PER_WAVE; i++) dma16(ab + aoff[i], lds_addr(A + 1024 * (wave * C::A_PER_WAVE + i)));
+    };
+    auto issue_raw = [&](int src, int dst) {
+        uint8_t* R = smem + C::R_OFF + (dst % C::R_SLOTS) * C::R_BYTES;
         const uint8_t* rb = W + (uint32_t)(src >> 2) * Q4K_BYTES + 32u * (src & 3);
-        dma16(rb + roff, lds_addr(S + X_A_BYTES + 1024 * wave));
+        dma16(rb + roff, lds_addr(R + 1024 * wave));
     };
     auto issue_sb = [&](int sb) {
-        uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES;
-        dma16((const uint8_t*)amin + (uint32_t)sb * 32u + soff, lds_addr(SB + X_SB_AMIN + 1024 * wave));
-        dma4(dyt + (int64_t)sb * m + dyrow, lds_addr(SB + X_SB_DY + 256 * wave));
-        dma16(W + (uint32_t)sb * Q4K_BYTES + hoff, lds_addr(SB + X_SB_HDR + 1024 * wave));
-    };
-    // this lane's reads of a stage / superblock buffer
-    auto read_raw = [&](int step, uint4 (&r)[X_NT]) {
-        const uint8_t* S = smem + (step % X_STAGES) * X_STAGE + X_A_BYTES;
+        uint8_t* SB = smem + C::SB_OFF + (sb & 1) * C::SB_BYTES;
 #pragma unroll
-        for (int b = 0; b < X_NT; b++) r[b] = *(const uint4*)(S + 1024 * (2 * wn + b) + 16 * (32 * h + c32));
+        for (int i = 0; i < C::S_PER_WAVE; i++)
+            dma16((const uint8_t*)amin + (uint32_t)sb * 32u + soff[i],
+                  lds_addr(SB + C::SB_AMIN + 1024 * (C::S_PER_WAVE * wave + i)));
+        dma4(dyt + (int64_t)sb * m + dyrow, lds_addr(SB + C::SB_DY + 256 * wave));
+        dma16(W + (uint32_t)sb * Q4K_BYTES + colw, lds_addr(SB + C::SB_HDR + 1024 * wave));
     };
-    auto read_hdr = [&](int sb, uint4 (&hd)[X_NT]) {
-        const uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES + X_SB_HDR;
+    auto read_raw = [&](int step, uint4 (&r)[C::NT]) {
+        const uint8_t* R = smem + C::R_OFF + (step % C::R_SLOTS) * C::R_BYTES;
 #pragma unroll
-        for (int b = 0; b < X_NT; b++) hd[b] = *(const uint4*)(SB + 1024 * (2 * wn + b) + 16 * c32);
+        for (int b = 0; b < C::NT; b++) r[b] = *(const uint4*)(R + 1024 * (2 * wn + b) + 16 * (32 * h + c32));
+    };
+    auto read_hdr = [&](int sb, uint4 (&hd)[C::NT]) {
+        const uint8_t* SB = smem + C::SB_OFF + (sb & 1) * C::SB_BYTES + C::SB_HDR;
+#pragma unroll
+        for (int b = 0; b < C::NT; b++) hd[b] = *(const uint4*)(SB + 1024 * (2 * wn + b) + 16 * c32);
     };
 
-    v16f acc[X_MT][X_NT], out[X_MT][X_NT];
+    v16f acc[MT][C::NT], out[MT][C::NT];
 #pragma unroll
-    for (int a = 0; a < X_MT; a++)
+    for (int a = 0; a < MT; a++)
 #pragma unroll
-        for (int b = 0; b < X_NT; b++)
+        for (int b = 0; b < C::NT; b++)
 #pragma unroll
             for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
 
     // Order of this wave's DMA loads (vmcnt retires in order; the scheduling
     // barriers keep the groups in order):
-    //   prologue: step(0), SB(0), step(1), step(2)
-    //   step s:   SB(sb + 1) at a superblock's first step, then step(s + 3)
-    // The last X_DMA_STEP loads of every step are step(s + 3), so
-    // vmcnt(X_DMA_STEP) at its end means everything before has landed:
-    // step(s + 2), whose weight bytes the next step unpacks and whose
-    // activations the step after reads, and SB(sb + 1) queued in this step.
-    // Steps and superblocks past the end reload the last one into buffers
-    // nobody reads again, so the counts never change.  The barriers are bare
-    // s_barrier: __syncthreads() would wait for every load in flight.
-    issue_step(0, 0);
+    //   prologue: SB(0), A(0), raw(0), raw(1), A(1), raw(2)
+    //   step s:   SB(sb + 1) at a superblock's first step, A(s + 2), raw(s + 3)
+    // At the end of step s, vmcnt(C::DMA_AFTER_RAW) leaves only A(s + 2) and
+    // raw(s + 3) in flight: A(s + 1) (read in step s + 1), raw(s + 2) (unpacked
+    // in step s + 1) and SB(sb + 1) have landed.  Steps and superblocks past
+    // the end reload the last one into buffers nobody reads again, so the
+    // counts never change.  The barriers are bare s_barrier:
+    // __syncthreads() would wait for every load in flight.
     issue_sb(0);
-    issue_step(min(1, nsteps - 1), 1);
-    issue_step(min(2, nsteps - 1), 2);
+    issue_a(0, 0);
+    issue_raw(0, 0);
+    issue_raw(min(1, nsteps - 1), 1);
+    issue_a(min(1, nsteps - 1), 1);
+    issue_raw(min(2, nsteps - 1), 2);
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(X_DMA_STEP) : "memory");  // step(0), SB(0), step(1) landed
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_AFTER_RAW) : "memory");
     __builtin_amdgcn_s_barrier();
 
-    uint4 hdr[X_NT];
+    uint4 hdr[C::NT];
     read_hdr(0, hdr);
-    v8h bv[2][X_NT][4];  // [step & 1]: operands of the current and the next step
+    v8h bv[2][C::NT][4];  // [step & 1]: operands of the current and the next step
     {
-        uint4 r0[X_NT];
+        uint4 r0[C::NT];
         read_raw(0, r0);
 #pragma unroll
-        for (int b = 0; b < X_NT; b++) build_b(r0[b], hdr[b], 0, bv[0][b]);
+        for (int b = 0; b < C::NT; b++) build_b(r0[b], hdr[b], 0, bv[0][b]);
     }
 
     for (int sb = 0; sb < nsb; sb++) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int s = 4 * sb + c;
-            const uint8_t* S = smem + (s % X_STAGES) * X_STAGE;
-            // 1. the step's LDS reads, before its DMA is queued: activations
-            //    of step s, weight bytes of step s + 1 (and its header at a
-            //    superblock's end), the epilogue's operands
-            v8h av[X_MT][4];
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-#pragma unroll
-                for (int a = 0; a < X_MT; a++)
-                    av[a][kk] = *(const v8h*)(S + x_pos(wm * 64 + a * 32 + c32, x_piece(kk, h)));
-            uint4 rn[X_NT], hn[X_NT];
-            read_raw(s + 1, rn);
-            v8h am[X_MT];
-            float4 dy[X_MT][4];
-            if (c == 3) {
-                read_hdr(sb + 1, hn);
-                const uint8_t* SB = sbbuf + (sb & 1) * X_SB_BYTES;
-#pragma unroll
-                for (int a = 0; a < X_MT; a++) {
-                    const int row = wm * 64 + a * 32 + c32;
-                    am[a] = *(const v8h*)(SB + X_SB_AMIN + row * 32 + 16 * h);
-                    const float* dyp = (const float*)(SB + X_SB_DY) + wm * 64 + a * 32 + 4 * h;
-#pragma unroll
-                    for (int g = 0; g < 4; g++) dy[a][g] = *(const float4*)(dyp + 8 * g);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            // 2. queue: the next superblock's operands (first step), step s + 3
+            const uint8_t* A = smem + (s % C::A_STAGES) * C::A_BYTES;
+            // 1. queue: the next superblock's operands (first step), A(s + 2)
+            //    into the stage step s - 1 used, raw(s + 3) into step s - 1's slot
             if (c == 0) issue_sb(min(sb + 1, nsb - 1));
-            issue_step(min(s + 3, nsteps - 1), s + 3);
+            issue_a(min(s + 2, nsteps - 1), s + 2);
+            issue_raw(min(s + 3, nsteps - 1), s + 3);
             __builtin_amdgcn_sched_barrier(0);
+            // 2. the next step's weight bytes (and header at a superblock's end)
+            uint4 rn[C::NT], hn[C::NT];
+            read_raw(s + 1, rn);
+            if (c == 3) read_hdr(sb + 1, hn);
             // 3. MFMA on step s, unpacking step s + 1's weights in between
 #pragma unroll
-            for (int b = 0; b < X_NT; b++) build_b(rn[b], c == 3 ? hn[b] : hdr[b], (c + 1) & 3, bv[(c + 1) & 1][b]);
+            for (int b = 0; b < C::NT; b++) build_b(rn[b], c == 3 ? hn[b] : hdr[b], (c + 1) & 3, bv[(c + 1) & 1][b]);
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)
+            for (int kk = 0; kk < 4; kk++) {
+                v8h av[MT];
 #pragma unroll
-                for (int a = 0; a < X_MT; a++)
+                for (int a = 0; a < MT; a++)
+                    av[a] = *(const v8h*)(A + x_pos(wm * (32 * MT) + a * 32 + c32, x_piece(kk, h)));
 #pragma unroll
-                    for (int b = 0; b < X_NT; b++) {
+                for (int a = 0; a < MT; a++)
+#pragma unroll
+                    for (int b = 0; b < C::NT; b++) {
                         if (kk == 0 && c == 0) {
                             const v16f z = {};
-                            acc[a][b] =
-                                __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[c & 1][b][kk], z, 0, 0, 0);
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[c & 1][b][kk], z, 0, 0, 0);
                         } else {
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], bv[c & 1][b][kk],
-                                                                               acc[a][b], 0, 0, 0);
+                            acc[a][b] =
+                                __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[c & 1][b][kk], acc[a][b], 0, 0, 0);
                         }
                     }
+            }
             // 4. superblock epilogue: min term on MFMA, then
             //    out += dy * (d * D - dmin * Dmin)
             if (c == 3) {
+                const uint8_t* SB = smem + C::SB_OFF + (sb & 1) * C::SB_BYTES;
 #pragma unroll
-                for (int b = 0; b < X_NT; b++) {
+                for (int b = 0; b < C::NT; b++) {
                     // this lane's column: d, dmin and the mins as [64 m | m]
                     const float d = f16_to_f32(hdr[b].x & 0xffffu), dmin = f16_to_f32(hdr[b].x >> 16);
                     const uint64_t m8 =
@@ -694,12 +696,16 @@ __global__ __launch_bounds__(X_THREADS) void k_gemm_q4k_x16(const uint8_t* __res
                         bmv[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
                     }
 #pragma unroll
-                    for (int a = 0; a < X_MT; a++) {
+                    for (int a = 0; a < MT; a++) {
+                        const int row = wm * (32 * MT) + a * 32 + c32;
+                        const v8h am = *(const v8h*)(SB + C::SB_AMIN + row * 32 + 16 * h);
                         const v16f z = {};
-                        const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[a], bmv, z, 0, 0, 0);
+                        const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bmv, z, 0, 0, 0);
+                        const float* dyp = (const float*)(SB + C::SB_DY) + wm * (32 * MT) + a * 32 + 4 * h;
 #pragma unroll
                         for (int g = 0; g < 4; g++) {
-                            const float dys[4] = {dy[a][g].x, dy[a][g].y, dy[a][g].z, dy[a][g].w};
+                            const float4 dy4 = *(const float4*)(dyp + 8 * g);
+                            const float dys[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
                             for (int u = 0; u < 4; u++) {
                                 const int r = 4 * g + u;
@@ -709,26 +715,25 @@ __global__ __launch_bounds__(X_THREADS) void k_gemm_q4k_x16(const uint8_t* __res
                     }
                 }
 #pragma unroll
-                for (int b = 0; b < X_NT; b++) hdr[b] = hn[b];
+                for (int b = 0; b < C::NT; b++) hdr[b] = hn[b];
             }
-            // 5. step s + 2 has landed; every wave is past its reads of step
-            //    s - 1's stage (which step s + 3 overwrites: queued above,
-            //    after this wave's own reads, and the other waves passed
-            //    their reads of it before the previous barrier)
+            // 5. A(s + 1), raw(s + 2), SB(sb + 1) have landed; every wave is
+            //    past its reads of the stage and slot the next step's DMA
+            //    overwrites (step s's)
             __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(X_DMA_STEP) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_AFTER_RAW) : "memory");
             __builtin_amdgcn_s_barrier();
         }
     }
 #pragma unroll
-    for (int a = 0; a < X_MT; a++)
+    for (int a = 0; a < MT; a++)
 #pragma unroll
-        for (int b = 0; b < X_NT; b++) {
+        for (int b = 0; b < C::NT; b++) {
             const int col = n0 + wn * 64 + b * 32 + c32;
             if (col >= n) continue;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int row = m0 + wm * (32 * MT) + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (row < m) Y[(int64_t)row * n + col] = out[a][b][r];
             }
         }
@@ -748,26 +753,34 @@ size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
     return matvec_workspace_bytes(type == T_Q4K ? T_Q6K : type, k, 16);
 }
 
+template <int MT>
+static hipError_t launch_x16(const void* w, const X16Ptrs& p, float* y, int64_t n, int64_t k, int64_t m,
+                             hipStream_t s) {
+    using C = XCfg<MT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e =
+            hipFuncSetAttribute((const void*)k_gemm_q4k_x16<MT>, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const unsigned grid = (unsigned)(((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN));
+    hipLaunchKernelGGL((k_gemm_q4k_x16<MT>), dim3(grid), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.x16,
+                       p.amin, p.dyt, y, (int)m, (int)n, (int)k);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, int mode, hipStream_t s) {
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
-        static bool attr_set = false;
-        if (!attr_set) {
-            hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k_x16,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, X_LDS);
-            if (e != hipSuccess) return e;
-            attr_set = true;
-        }
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
         hipLaunchKernelGGL(k_gemm_prep_x16, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.x16, p.amin,
                            p.dyt, (int)m, (int)k);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        const unsigned grid = (unsigned)(((m + X_BM - 1) / X_BM) * ((n + X_BN - 1) / X_BN));
-        hipLaunchKernelGGL(k_gemm_q4k_x16, dim3(grid), dim3(X_THREADS), X_LDS, s, (const uint8_t*)w, p.x16, p.amin,
-                           p.dyt, y, (int)m, (int)n, (int)k);
-        return hipGetLastError();
+        // 256-row tiles once there are enough of them to fill the chip
+        return m >= 1024 ? launch_x16<4>(w, p, y, n, k, m, s) : launch_x16<2>(w, p, y, n, k, m, s);
     }
     if (type == T_Q4K && fits_32bit(n, k, m)) {
         static bool attr_set = false;

@@ -26,7 +26,8 @@ size_t matvec_workspace_bytes(int type, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, hipStream_t s);
 
-// gemm.hip: m > 16 rows.  Q4_K on MFMA (mode: GEMM_F16 or GEMM_INT8), the
+// gemm.hip: m > 16 rows.  Q4_K on MFMA (mode: GEMM_F16, exact integer
+// operands on fp16 MFMA, or GEMM_INT8, two int8 scale planes), the
 // other types through decode tiles; qbuf is workspace for the prepared x.
 constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,

@@ -91,8 +91,9 @@ MMA_F16, MMA_INT8 = 0, 1
 
 
 def set_prefill_mma(mode, device=0):
-    """Matrix-core family of the Q4_K prefill GEMM: MMA_INT8 (default, the
-    CPU arm's exact integer sums) or MMA_F16 (fp16 operands, opt-in)."""
+    """Matrix-core family of the Q4_K prefill GEMM: MMA_F16 (default: the
+    exact integer operands on fp16 MFMA) or MMA_INT8 (two int8 scale planes).
+    Both compute the CPU arm's integer sums exactly."""
     check(lib().lloom_hip_ctx_set_prefill_mma(_ctx(device), mode))
 
 
