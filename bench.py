@@ -12,6 +12,9 @@ timed steps are replayed from one HIP graph (decode launches are a few
 microseconds each; the graph keeps host launch overhead out), bracketed by
 HIP events on the stream they run on.
 
+`roofline` is the dominant kernel's: the single-row decode matvec (C2 at
+B=1), algorithmic bytes per launch over its average launch time.
+
 `details` adds the other BASELINE configs (C1 Q8_0 decode, C3 Q4_K prefill
 TFLOP/s, C4 decoder-layer decode, C5 routed experts) measured the same way,
 and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
@@ -41,6 +44,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-details", action="store_true", help="only the headline config")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="launch only the roofline kernel (C2 at B=1, eagerly, on cold weight copies) and a "
+                         "64 MiB device copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     return ap.parse_args()
 
 
@@ -132,6 +138,18 @@ def main():
     def launch(b, qtensor):
         return lambda: L.QMatMul(qtensor).forward_into(xs[b], ys[b])
 
+    if args.pmc_probe:
+        # the calibration copy (64 MiB read, 64 MiB written), then the kernel
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        for i in range(20):
+            launch(1, rot.tensors[i % len(rot)])()
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": "c2_b1", "algorithmic_bytes": algo[1], "copy_bytes": 64 << 20}))
+        return
+
     sweep = []
     for step in range(args.steps):
         for b in Bs:
@@ -152,6 +170,20 @@ def main():
 
     details = {"c2_q4k_decode_per_batch": per_b, "rotation_copies": len(rot),
                "rotation_bytes": len(rot) * wbytes}
+    # Roofline of the path's dominant kernel: the single-row decode matvec
+    # (C2 at B=1, one kernel per call): algorithmic bytes per launch over the
+    # kernel's average launch time, from the per-B graph above (events on the
+    # replay stream).  traffic: measured HBM bytes per launch, from the
+    # committed rocprofv3 FETCH_SIZE / WRITE_SIZE calibration when present.
+    t_b1 = per_b["1"]["us"] * 1e-6
+    ach = algo[1] / t_b1 / 1e9
+    roofline = {"bound": "hbm", "kernel": "k_matvec<Q4_K, 1 row> (C2, B=1)", "achieved": round(ach, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes": algo[1], "us_per_launch": per_b["1"]["us"], "traffic": None}
+    tpath = os.path.join(ROOT, "profiles", "traffic_c2_b1.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            roofline["traffic"] = json.load(f).get("hbm_bytes_per_launch")
     del rot
     torch.cuda.empty_cache()
 
@@ -178,8 +210,7 @@ def main():
         "config": {"workload": "C2 Q4_K decode matvec sweep, W [6144,2048] Q4_K, x f32 [B,2048], "
                                "B in {1,2,4,8,16}; one step = the 5 calls",
                    "n": n, "k": k, "batches": Bs},
-        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "details": details,
     }
