@@ -302,7 +302,7 @@ def run_details(L, cu, np, torch, dev, args):
     out["c5_moe_experts"] = {"us": round(t * 1e6, 2), "distinct_experts": distinct,
                              "unique_expert_bytes": int(byts), "GB/s": round(byts / t / 1e9, 1),
                              "hbm_frac": round(byts / t / 1e9 / 8000.0, 4),
-                             "note": "gate+up+down, 3 routed calls; working set fits the 256 MB MALL"}
+                             "note": "gate+up+down, 3 routed calls on the same graph replay; the 307 MB of touched experts exceed the 256 MB MALL"}
     return out
 
 
