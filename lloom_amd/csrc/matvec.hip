@@ -445,9 +445,8 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
 #pragma unroll
     for (int t = 0; t < NT; t++) out[t][0] = out[t][1] = out[t][2] = out[t][3] = 0.0f;
 
-    // registers of the superblock in flight; loads are unconditional (a
-    // wave past the end reloads its last superblock) so none sits under a
-    // branch and the waits stay counted
+    // registers of the superblock in flight (the row and superblock
+    // indices are clamped, so no load sits under a divergent branch)
     MfW<TYPE> wc[NT];
     uint4 avc[4];
     float4 dyc;
@@ -461,10 +460,12 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
     };
     issue(wave, wc, avc, dyc);
     for (int sb = wave; sb < nsb; sb += KS) {
+        // the next superblock's loads, when this wave has one (wave-uniform)
+        const bool more = sb + KS < nsb;
         MfW<TYPE> wn[NT];
         uint4 avn[4];
         float4 dyn;
-        issue(sb + KS, wn, avn, dyn);
+        if (more) issue(sb + KS, wn, avn, dyn);
         // activation rows past m are zeroed by select (a load under a
         // divergent branch would serialize the waits)
         long a[8];
@@ -475,6 +476,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
         }
 #pragma unroll
         for (int t = 0; t < NT; t++) mf_compute<TYPE>(wc[t], a, dyc, g, out[t]);
+        if (!more) break;
 #pragma unroll
         for (int t = 0; t < NT; t++) wc[t] = wn[t];
 #pragma unroll
