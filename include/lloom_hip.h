@@ -87,7 +87,8 @@ enum { LLOOM_HIP_MMA_F16 = 0, LLOOM_HIP_MMA_INT8 = 1 };
 int lloom_hip_ctx_set_prefill_mma(lloom_hip_ctx* ctx, int mode);
 
 /* Wait for the device; report a device-side error (an out-of-range expert
- * id seen by a routed matmul) recorded since the last check, and clear it. */
+ * id seen by a routed matmul, or an out-of-range embedding id) recorded
+ * since the last check, and clear it. */
 int lloom_hip_ctx_sync(lloom_hip_ctx* ctx);
 
 /* ---------------------------------------------------------------- memory --
@@ -139,6 +140,23 @@ int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int6
                       const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype,
                       void* stream);
 
+/* Store epilogues of the matmul: QMatMul::forward_silu and forward_mul_into
+ * (mod.rs:2102-2156), the MvStore::{Silu, MulInto} blocks of the reference's
+ * Metal matvec store (mod.rs:1667-1696, kernels/metal_src/
+ * quantized_store.metal): the product is formed as in lloom_hip_qmatmul and
+ * then stored as
+ *   LLOOM_HIP_STORE_PLAIN     y = v
+ *   LLOOM_HIP_STORE_SILU      y = v / (1 + exp(-v))
+ *   LLOOM_HIP_STORE_MUL_INTO  y = y * v  (y is read: the SwiGLU gate's own
+ *                             buffer holding silu(g), which then holds
+ *                             silu(g) * u; y must have no other reader)
+ * in the same launch, on every row count (decode and prefill); the
+ * reference serves these on Metal only and returns None elsewhere. */
+enum { LLOOM_HIP_STORE_PLAIN = 0, LLOOM_HIP_STORE_SILU = 1, LLOOM_HIP_STORE_MUL_INTO = 2 };
+int lloom_hip_qmatmul_store(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                            const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, int store,
+                            void* stream);
+
 /* ------------------------------------------------------- routed experts --
  * QTensor::indexed_moe_forward{,_with,_as} (mod.rs:1560-1645), CPU arm
  * matmul_t_indexed (mod.rs:766-810): W [n_experts, n, k] packed, x f32
@@ -156,6 +174,40 @@ int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, i
                          int64_t n, int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1,
                          const uint32_t* ids_dev, int64_t topk, float* y_dev, int strict,
                          void* stream);
+
+/* Gate and up of one routed layer in one launch: QTensor::
+ * indexed_moe_forward_pair (mod.rs:1365-1455; one Metal launch,
+ * kernel_mul_mv_id2, on the reference).  Both stacks have the same type and
+ * shape [n_experts, n, k]; y_gate and y_up are each what
+ * lloom_hip_moe_matmul computes for its weight, bit for bit. */
+int lloom_hip_moe_matmul_pair(lloom_hip_ctx* ctx, int ggml_type, const void* w_gate_dev,
+                              const void* w_up_dev, int64_t n_experts, int64_t n, int64_t k,
+                              const float* x_dev, int64_t batch, int64_t in_dim1,
+                              const uint32_t* ids_dev, int64_t topk, float* y_gate_dev,
+                              float* y_up_dev, int strict, void* stream);
+
+/* silu(gate) * up of the pair in one launch, y [batch, topk, n]: QTensor::
+ * indexed_moe_forward_glu_as (mod.rs:1457-1531), silu_mul's element
+ * (silu(g) = g / (1 + exp(-g)), then the product) over the two sums the
+ * pair stores. */
+int lloom_hip_moe_matmul_glu(lloom_hip_ctx* ctx, int ggml_type, const void* w_gate_dev,
+                             const void* w_up_dev, int64_t n_experts, int64_t n, int64_t k,
+                             const float* x_dev, int64_t batch, int64_t in_dim1,
+                             const uint32_t* ids_dev, int64_t topk, float* y_dev, int strict,
+                             void* stream);
+
+/* ------------------------------------------------------------- embedding --
+ * QTensor::embedding (mod.rs:1101-1137; CPU arm QuantizedType::embedding,
+ * :812-838; CUDA quantized.cu get_rows): y[i, :] = to_float of weight row
+ * ids[i] of a packed [rows, hidden] weight, bit-exact; out_dtype F32 or F16
+ * (RNE of the f32 value).  hidden must be a multiple of the block.  An
+ * id >= rows stores a zero row and fails the call with LLOOM_HIP_EEXPERT
+ * ("embedding id ... is out of range"; the call synchronizes to read the
+ * device flag) unless strict is 0, when the next lloom_hip_ctx_sync reports
+ * it.  n_ids = 0 is a no-op. */
+int lloom_hip_embedding(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t rows,
+                        int64_t hidden, const uint32_t* ids_dev, int64_t n_ids, void* y_dev,
+                        int out_dtype, int strict, void* stream);
 
 /* ------------------------------------------------------- synthetic data --
  * The benchmark/test input generator (not part of the reference): SplitMix64

@@ -11,6 +11,7 @@ from .lib import LloomHipError, lib, lib_path  # noqa: F401
 from .quantized import (  # noqa: F401
     GgmlDType,
     MoeArm,
+    MvStore,
     QMatMul,
     QTensor,
     dequantize,

@@ -164,7 +164,7 @@ int lloom_hip_ctx_sync(lloom_hip_ctx* ctx) {
     if (flag) {
         int zero = 0;
         HIP_OK(hipMemcpy(ctx->flags, &zero, sizeof(int), hipMemcpyHostToDevice));
-        return fail(LLOOM_HIP_EEXPERT, "a routed matmul saw an expert id out of range for its experts");
+        return fail(LLOOM_HIP_EEXPERT, "a routed matmul or embedding saw an id out of range");
     }
     return LLOOM_HIP_OK;
 }
@@ -254,8 +254,8 @@ int lloom_hip_dequantize(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, i
     return LLOOM_HIP_OK;
 }
 
-int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
-                      const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, void* stream) {
+static int qmatmul_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                        const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, int epi, void* stream) {
     if (!ctx || !w_dev || !x_dev || !y_dev) return fail(LLOOM_HIP_EINVAL, "qmatmul: null argument");
     if (!is_weight_type(ggml_type))
         return fail(LLOOM_HIP_EDTYPE, "qmatmul: weight dtype %s (%d) is not supported on the HIP quantized path (Q8_0, Q4K, Q6K)", type_name(ggml_type), ggml_type);
@@ -281,16 +281,44 @@ int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int6
         if (rc) return rc;
     }
     if (decode)
-        HIP_OK(launch_matvec(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, s));
+        HIP_OK(launch_matvec(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, epi, s));
     else
-        HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, ctx->prefill_mma, s));
+        HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, ctx->prefill_mma, epi, s));
     return LLOOM_HIP_OK;
 }
 
-int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n_experts, int64_t n,
-                         int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1, const uint32_t* ids_dev,
-                         int64_t topk, float* y_dev, int strict, void* stream) {
+}  // extern "C"
+
+static int moe_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, const void* w2_dev, int64_t n_experts,
+                    int64_t n, int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1,
+                    const uint32_t* ids_dev, int64_t topk, float* y_dev, float* y2_dev, int mode, int strict,
+                    void* stream);
+
+extern "C" {
+
+int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                      const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, void* stream) {
+    return qmatmul_impl(ctx, ggml_type, w_dev, n, k, x_dev, x_dtype, m, y_dev, y_dtype, EPI_STORE, stream);
+}
+
+int lloom_hip_qmatmul_store(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                            const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, int store,
+                            void* stream) {
+    if (store != LLOOM_HIP_STORE_PLAIN && store != LLOOM_HIP_STORE_SILU && store != LLOOM_HIP_STORE_MUL_INTO)
+        return fail(LLOOM_HIP_EINVAL, "qmatmul_store: store %d is not PLAIN (0), SILU (1) or MUL_INTO (2)", store);
+    const int epi = store == LLOOM_HIP_STORE_SILU ? EPI_SILU : store == LLOOM_HIP_STORE_MUL_INTO ? EPI_MUL_INTO : EPI_STORE;
+    return qmatmul_impl(ctx, ggml_type, w_dev, n, k, x_dev, x_dtype, m, y_dev, y_dtype, epi, stream);
+}
+
+}  // extern "C"
+
+static int moe_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, const void* w2_dev, int64_t n_experts,
+                    int64_t n, int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1,
+                    const uint32_t* ids_dev, int64_t topk, float* y_dev, float* y2_dev, int mode, int strict,
+                    void* stream) {
     if (!ctx || !w_dev || !x_dev || !ids_dev || !y_dev) return fail(LLOOM_HIP_EINVAL, "moe_matmul: null argument");
+    if (mode != MOE_ONE && !w2_dev) return fail(LLOOM_HIP_EINVAL, "moe_matmul: null up weight");
+    if (mode == MOE_PAIR && !y2_dev) return fail(LLOOM_HIP_EINVAL, "moe_matmul: null up output");
     if (!is_weight_type(ggml_type))
         return fail(LLOOM_HIP_EDTYPE, "moe_matmul: weight dtype %s (%d) is not supported on the HIP quantized path", type_name(ggml_type), ggml_type);
     int be = block_elems(ggml_type);
@@ -304,16 +332,17 @@ int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, i
     if (n_experts > MOE_MAX_EXPERTS)
         return fail(LLOOM_HIP_ESHAPE, "moe_matmul: %lld experts, at most %d are routed on the device",
                     (long long)n_experts, MOE_MAX_EXPERTS);
-    if ((uintptr_t)w_dev % (ggml_type == T_Q4K ? 16 : 4) || (uintptr_t)x_dev % 16)
+    if ((uintptr_t)w_dev % (ggml_type == T_Q4K ? 16 : 4) || (uintptr_t)x_dev % 16 ||
+        (w2_dev && (uintptr_t)w2_dev % (ggml_type == T_Q4K ? 16 : 4)))
         return fail(LLOOM_HIP_EINVAL, "moe_matmul: misaligned weight or x pointer");
     HIP_OK(hipSetDevice(ctx->device));
     hipStream_t s = pick_stream(ctx, stream);
     std::lock_guard<std::mutex> lock(ctx->mu);
     void* ws = nullptr;
-    int rc = ensure_ws(ctx, moe_workspace_ints(n_experts, batch * topk) * sizeof(int), &ws);
+    int rc = ensure_ws(ctx, moe_workspace_bytes(n_experts, batch * topk, n, k, mode), &ws);
     if (rc) return rc;
     HIP_OK(launch_moe(ggml_type, w_dev, n_experts, n, k, x_dev, batch, in_dim1, ids_dev, topk, y_dev, (int*)ws,
-                      ctx->flags, s));
+                      ctx->flags, mode, w2_dev, y2_dev, s));
     if (strict) {
         int flag = 0;
         HIP_OK(hipMemcpyAsync(&flag, ws, sizeof(int), hipMemcpyDeviceToHost, s));
@@ -322,6 +351,63 @@ int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, i
             int zero = 0;
             HIP_OK(hipMemcpy(ctx->flags, &zero, sizeof(int), hipMemcpyHostToDevice));
             return fail(LLOOM_HIP_EEXPERT, "expert id is out of range for %lld experts", (long long)n_experts);
+        }
+    }
+    return LLOOM_HIP_OK;
+}
+
+extern "C" {
+
+int lloom_hip_moe_matmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n_experts, int64_t n,
+                         int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1, const uint32_t* ids_dev,
+                         int64_t topk, float* y_dev, int strict, void* stream) {
+    return moe_impl(ctx, ggml_type, w_dev, nullptr, n_experts, n, k, x_dev, batch, in_dim1, ids_dev, topk, y_dev,
+                    nullptr, MOE_ONE, strict, stream);
+}
+
+int lloom_hip_moe_matmul_pair(lloom_hip_ctx* ctx, int ggml_type, const void* w_gate_dev, const void* w_up_dev,
+                              int64_t n_experts, int64_t n, int64_t k, const float* x_dev, int64_t batch,
+                              int64_t in_dim1, const uint32_t* ids_dev, int64_t topk, float* y_gate_dev,
+                              float* y_up_dev, int strict, void* stream) {
+    return moe_impl(ctx, ggml_type, w_gate_dev, w_up_dev, n_experts, n, k, x_dev, batch, in_dim1, ids_dev, topk,
+                    y_gate_dev, y_up_dev, MOE_PAIR, strict, stream);
+}
+
+int lloom_hip_moe_matmul_glu(lloom_hip_ctx* ctx, int ggml_type, const void* w_gate_dev, const void* w_up_dev,
+                             int64_t n_experts, int64_t n, int64_t k, const float* x_dev, int64_t batch,
+                             int64_t in_dim1, const uint32_t* ids_dev, int64_t topk, float* y_dev, int strict,
+                             void* stream) {
+    return moe_impl(ctx, ggml_type, w_gate_dev, w_up_dev, n_experts, n, k, x_dev, batch, in_dim1, ids_dev, topk,
+                    y_dev, nullptr, MOE_GLU, strict, stream);
+}
+
+int lloom_hip_embedding(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t rows, int64_t hidden,
+                        const uint32_t* ids_dev, int64_t n_ids, void* y_dev, int out_dtype, int strict,
+                        void* stream) {
+    if (!ctx || !w_dev || (n_ids && (!ids_dev || !y_dev))) return fail(LLOOM_HIP_EINVAL, "embedding: null argument");
+    if (!is_weight_type(ggml_type))
+        return fail(LLOOM_HIP_EDTYPE, "embedding: %s (%d) is not supported on the HIP quantized path", type_name(ggml_type), ggml_type);
+    if (out_dtype != T_F32 && out_dtype != T_F16)
+        return fail(LLOOM_HIP_EDTYPE, "embedding: output dtype %s (%d) must be F32 or F16", type_name(out_dtype), out_dtype);
+    const int be = block_elems(ggml_type);
+    if (rows <= 0 || hidden <= 0 || n_ids < 0) return fail(LLOOM_HIP_EINVAL, "embedding: empty or negative shape");
+    if (hidden % be)
+        return fail(LLOOM_HIP_ESHAPE, "quantized embedding hidden size %lld is not divisible by block size %d", (long long)hidden, be);
+    if ((uintptr_t)w_dev % 4) return fail(LLOOM_HIP_EINVAL, "embedding: weight must be 4-byte aligned");
+    if (n_ids == 0) return LLOOM_HIP_OK;
+    HIP_OK(hipSetDevice(ctx->device));
+    hipStream_t s = pick_stream(ctx, stream);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (strict) HIP_OK(hipMemsetAsync(ctx->flags + 1, 0, sizeof(int), s));
+    HIP_OK(launch_embedding(ggml_type, w_dev, rows, hidden, ids_dev, n_ids, y_dev, out_dtype, ctx->flags, s));
+    if (strict) {
+        int flag = 0;
+        HIP_OK(hipMemcpyAsync(&flag, ctx->flags + 1, sizeof(int), hipMemcpyDeviceToHost, s));
+        HIP_OK(hipStreamSynchronize(s));
+        if (flag) {
+            int zero = 0;
+            HIP_OK(hipMemcpy(ctx->flags, &zero, sizeof(int), hipMemcpyHostToDevice));
+            return fail(LLOOM_HIP_EEXPERT, "embedding id is out of range for %lld rows", (long long)rows);
         }
     }
     return LLOOM_HIP_OK;

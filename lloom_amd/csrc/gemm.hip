@@ -221,7 +221,7 @@ __device__ __forceinline__ void stage_wait() {
 
 __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                         const int8_t* __restrict__ sp, const float* __restrict__ dyt,
-                                                        float* __restrict__ Y, int m, int n, int k) {
+                                                        float* __restrict__ Y, int m, int n, int k, int epi) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / G_WN, wn = wave % G_WN;
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm * G_MT * 32 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < m) Y[(int64_t)row * n + col] = out[a][b][r];
+                if (row < m) store_epi(&Y[(int64_t)row * n + col], out[a][b][r], epi);
             }
         }
 }
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
                                                             const _Float16* __restrict__ x16,
                                                             const _Float16* __restrict__ amin,
                                                             const float* __restrict__ dyt, float* __restrict__ Y,
-                                                            int m, int n, int k) {
+                                                            int m, int n, int k, int epi) {
     using C = XCfg<MT>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm * (32 * MT) + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < m) Y[(int64_t)row * n + col] = out[a][b][r];
+                if (row < m) store_epi(&Y[(int64_t)row * n + col], out[a][b][r], epi);
             }
         }
 }
@@ -755,7 +755,7 @@ size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
 
 template <int MT>
 static hipError_t launch_x16(const void* w, const X16Ptrs& p, float* y, int64_t n, int64_t k, int64_t m,
-                             hipStream_t s) {
+                             int epi, hipStream_t s) {
     using C = XCfg<MT>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -766,12 +766,12 @@ static hipError_t launch_x16(const void* w, const X16Ptrs& p, float* y, int64_t 
     }
     const unsigned grid = (unsigned)(((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN));
     hipLaunchKernelGGL((k_gemm_q4k_x16<MT>), dim3(grid), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.x16,
-                       p.amin, p.dyt, y, (int)m, (int)n, (int)k);
+                       p.amin, p.dyt, y, (int)m, (int)n, (int)k, epi);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                       void* qbuf, int mode, hipStream_t s) {
+                       void* qbuf, int mode, int epi, hipStream_t s) {
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
@@ -780,7 +780,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         // 256-row tiles once there are enough of them to fill the chip
-        return m >= 1024 ? launch_x16<4>(w, p, y, n, k, m, s) : launch_x16<2>(w, p, y, n, k, m, s);
+        return m >= 1024 ? launch_x16<4>(w, p, y, n, k, m, epi, s) : launch_x16<2>(w, p, y, n, k, m, epi, s);
     }
     if (type == T_Q4K && fits_32bit(n, k, m)) {
         static bool attr_set = false;
@@ -798,14 +798,14 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
         if (e != hipSuccess) return e;
         const unsigned grid = (unsigned)(((m + G_BM - 1) / G_BM) * ((n + G_BN - 1) / G_BN));
         hipLaunchKernelGGL(k_gemm_q4k, dim3(grid), dim3(G_THREADS), G_LDS, s, (const uint8_t*)w, p.xq, p.sp, p.dyt,
-                           y, (int)m, (int)n, (int)k);
+                           y, (int)m, (int)n, (int)k, epi);
         return hipGetLastError();
     }
     // Q8_0 / Q6_K (and Q4_K past 32-bit offsets): tiles of 16 activation
     // rows through the decode kernels
     for (int64_t r = 0; r < m; r += 16) {
         const int64_t mm = m - r < 16 ? m - r : 16;
-        hipError_t e = launch_matvec(type, w, x + r * k, y + r * n, n, k, mm, qbuf, s);
+        hipError_t e = launch_matvec(type, w, x + r * k, y + r * n, n, k, mm, qbuf, epi, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -11,6 +11,10 @@ namespace lloom {
 hipError_t launch_quantize_act(int vec_dot_type, const float* x, void* out, int64_t elems, hipStream_t s);
 hipError_t launch_quantize_weights(int type, const float* x, void* out, int64_t elems, hipStream_t s);
 hipError_t launch_dequantize(int type, const void* w, void* y, int out_dtype, int64_t elems, hipStream_t s);
+// Rows ids[0 .. n_ids) of an [rows, hidden] weight, dequantized; a bad id
+// gives a zero row and sets flag[0] and flag[1].
+hipError_t launch_embedding(int type, const void* w, int64_t rows, int64_t hidden, const uint32_t* ids, int64_t n_ids,
+                            void* y, int out_dtype, int* flag, hipStream_t s);
 
 // quant.hip: Q8_K activations in the split layout the MFMA kernels read:
 // qs int8 [m][k] then d f32 [k/256][16] (m padded to 16), 256-byte aligned.
@@ -24,22 +28,28 @@ hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_
 constexpr int MV_DOT_MAX_ROWS = 2;
 size_t matvec_workspace_bytes(int type, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                         void* ws, hipStream_t s);
+                         void* ws, int epi, hipStream_t s);
 
 // gemm.hip: m > 16 rows.  Q4_K on MFMA (mode: GEMM_F16, exact integer
 // operands on fp16 MFMA, or GEMM_INT8, two int8 scale planes), the
 // other types through decode tiles; qbuf is workspace for the prepared x.
 constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                       void* qbuf, int mode, hipStream_t s);
+                       void* qbuf, int mode, int epi, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode);
 
 // moe.hip
 // The router keeps two ints per expert in LDS.
 constexpr int MOE_MAX_EXPERTS = 4096;
 size_t moe_workspace_ints(int64_t n_experts, int64_t planes);
+// mode MOE_ONE: y = W . x; MOE_PAIR: y = W . x and y2 = W2 . x in one
+// launch; MOE_GLU: y = silu(W . x) * (W2 . x).  The workspace holds the
+// routing ints (and, for a GLU over rows too long to stage, the up planes).
+constexpr int MOE_ONE = 0, MOE_PAIR = 1, MOE_GLU = 2;
+size_t moe_workspace_bytes(int64_t n_experts, int64_t planes, int64_t n, int64_t k, int mode);
+bool moe_stages(int64_t k);
 hipError_t launch_moe(int type, const void* w, int64_t n_experts, int64_t n, int64_t k, const float* x,
                       int64_t batch, int64_t in_dim1, const uint32_t* ids, int64_t topk, float* y, int* ws,
-                      int* sticky, hipStream_t s);
+                      int* sticky, int mode, const void* w2, float* y2, hipStream_t s);
 
 }  // namespace lloom

@@ -199,6 +199,18 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v + partner32(v);
 }
 // Full-wave max (NaN-ignoring, as fmaxf), the result in every lane.
+// The quantized matmul's store epilogues (QMatMul::forward_silu /
+// forward_mul_into, mod.rs:2102-2156; the Metal store types of
+// kernels/metal_src/quantized_store.metal): the plain store, silu(v) =
+// v / (1 + exp(-v)), and y = y * v into the buffer's own value (the SwiGLU's
+// up projection multiplied into silu(gate)).
+constexpr int EPI_STORE = 0, EPI_SILU = 1, EPI_MUL_INTO = 2;
+__device__ __forceinline__ void store_epi(float* p, float v, int epi) {
+    if (epi == EPI_SILU) v = v / (1.0f + expf(-v));
+    else if (epi == EPI_MUL_INTO) v = *p * v;
+    *p = v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = __builtin_fmaxf(v, dpp<DPP_XOR1>(v));
     v = __builtin_fmaxf(v, dpp<DPP_XOR2>(v));

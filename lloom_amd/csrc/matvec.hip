@@ -201,7 +201,7 @@ __device__ __forceinline__ void quantize_lds(const float4 (&xv)[XN], int KC, int
 template <int TYPE, int MB, int R, int WV, int XN>
 __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                      float* __restrict__ Y, int n, int K, int m, int KC,
-                                                     uint32_t mg) {
+                                                     uint32_t mg, int epi) {
     using Tr = MvTraits<TYPE>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         const float tot = wave_sum_items<R * MB>(v);
         const int item = wave_sum_item_of_lane();
         const int r = item / MB, mi = item % MB;
-        if ((lane & 7) == 0 && item < R * MB && mi < m && row0 + r < n) Y[(int64_t)mi * n + row0 + r] = tot;
+        if ((lane & 7) == 0 && item < R * MB && mi < m && row0 + r < n) store_epi(&Y[(int64_t)mi * n + row0 + r], tot, epi);
     } else {
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
             for (int mi = 0; mi < MB; mi++) {
                 if (mi < m) {
                     const float v = wave_sum(acc[r][mi]);
-                    if (lane == 0 && row < n) Y[(int64_t)mi * n + row] = v;
+                    if (lane == 0 && row < n) store_epi(&Y[(int64_t)mi * n + row], v, epi);
                 }
             }
         }
@@ -429,7 +429,7 @@ __device__ __forceinline__ void mf_compute(const MfW<TYPE>& w, const long (&a)[8
 template <int TYPE, int KS, int NT>
 __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                      const float* __restrict__ xd, float* __restrict__ Y, int n,
-                                                     int K, int m) {
+                                                     int K, int m, int epi) {
     constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float4 part[KS > 1 ? KS - 1 : 1][NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -508,7 +508,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int mi = 4 * g + u;
-                if (mi < m) Y[(int64_t)mi * n + nrow] = out[t][u];
+                if (mi < m) store_epi(&Y[(int64_t)mi * n + nrow], out[t][u], epi);
             }
         }
     }
@@ -534,7 +534,7 @@ static size_t lds_bytes(int type, int KC, int m) {
 }
 
 template <int TYPE, int MB, int WV, int R>
-static hipError_t launch_cfg(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
+static hipError_t launch_cfg(const void* w, const float* x, float* y, int n, int K, int m, int epi, hipStream_t s) {
     const int KC = pick_kc(TYPE, K, m, WV);
     // blocks a wave quantizes per chunk: 256 elements (Q8_K) or 8 lanes x 32 (Q8_0) per step
     const int per_step = TYPE == T_Q8_0 ? 32 * 8 * WV : 256 * WV;
@@ -543,10 +543,10 @@ static hipError_t launch_cfg(const void* w, const float* x, float* y, int n, int
     const dim3 grid((n + WV * R - 1) / (WV * R)), block(64 * WV);
     const uint8_t* wb = (const uint8_t*)w;
     const uint32_t mg = nbc_magic(KC / (TYPE == T_Q8_0 ? 32 : 256));
-    if (steps <= 1) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 1>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
-    else if (steps <= 2) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 2>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
-    else if (steps <= 4) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 4>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
-    else hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 8>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg);
+    if (steps <= 1) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 1>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    else if (steps <= 2) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 2>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    else if (steps <= 4) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 4>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    else hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 8>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
     return hipGetLastError();
 }
 
@@ -554,21 +554,21 @@ static hipError_t launch_cfg(const void* w, const float* x, float* y, int n, int
 // chosen so the grid is about one workgroup per CU (each workgroup
 // quantizes x once; fewer, fuller workgroups quantize it fewer times).
 template <int TYPE, int MB>
-static hipError_t launch_small(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
+static hipError_t launch_small(const void* w, const float* x, float* y, int n, int K, int m, int epi, hipStream_t s) {
     const int r = (n + 8 * 256 - 1) / (8 * 256);
-    if (r <= 1) return launch_cfg<TYPE, MB, 8, 1>(w, x, y, n, K, m, s);
-    if (r <= 2) return launch_cfg<TYPE, MB, 8, 2>(w, x, y, n, K, m, s);
-    if (r <= 3) return launch_cfg<TYPE, MB, 8, 3>(w, x, y, n, K, m, s);
-    return launch_cfg<TYPE, MB, 8, 4>(w, x, y, n, K, m, s);
+    if (r <= 1) return launch_cfg<TYPE, MB, 8, 1>(w, x, y, n, K, m, epi, s);
+    if (r <= 2) return launch_cfg<TYPE, MB, 8, 2>(w, x, y, n, K, m, epi, s);
+    if (r <= 3) return launch_cfg<TYPE, MB, 8, 3>(w, x, y, n, K, m, epi, s);
+    return launch_cfg<TYPE, MB, 8, 4>(w, x, y, n, K, m, epi, s);
 }
 
 template <int TYPE>
-static hipError_t launch_type(const void* w, const float* x, float* y, int n, int K, int m, hipStream_t s) {
-    if (m <= 1) return launch_small<TYPE, 1>(w, x, y, n, K, m, s);
-    if (m <= 2) return launch_small<TYPE, 2>(w, x, y, n, K, m, s);
-    if (m <= 4) return launch_cfg<TYPE, 4, 4, 2>(w, x, y, n, K, m, s);
-    if (m <= 8) return launch_cfg<TYPE, 8, 4, 2>(w, x, y, n, K, m, s);
-    return launch_cfg<TYPE, 16, 4, 2>(w, x, y, n, K, m, s);
+static hipError_t launch_type(const void* w, const float* x, float* y, int n, int K, int m, int epi, hipStream_t s) {
+    if (m <= 1) return launch_small<TYPE, 1>(w, x, y, n, K, m, epi, s);
+    if (m <= 2) return launch_small<TYPE, 2>(w, x, y, n, K, m, epi, s);
+    if (m <= 4) return launch_cfg<TYPE, 4, 4, 2>(w, x, y, n, K, m, epi, s);
+    if (m <= 8) return launch_cfg<TYPE, 8, 4, 2>(w, x, y, n, K, m, epi, s);
+    return launch_cfg<TYPE, 16, 4, 2>(w, x, y, n, K, m, epi, s);
 }
 
 size_t matvec_workspace_bytes(int type, int64_t k, int64_t m) {
@@ -578,35 +578,35 @@ size_t matvec_workspace_bytes(int type, int64_t k, int64_t m) {
 
 template <int TYPE>
 static hipError_t launch_mv_mfma(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xq,
-                                 const float* xd, hipStream_t s) {
+                                 const float* xd, int epi, hipStream_t s) {
     // 8 waves split K; 2 row tiles per workgroup unless that leaves fewer
     // than ~256 workgroups
     constexpr int KS = 8;
     if (n >= 2 * 16 * 256) {
         hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 2>), dim3((unsigned)((n + 31) / 32)), dim3(64 * KS), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, epi);
     } else {
         hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 1>), dim3((unsigned)((n + 15) / 16)), dim3(64 * KS), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m);
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, epi);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                         void* ws, hipStream_t s) {
+                         void* ws, int epi, hipStream_t s) {
     if (type != T_Q8_0 && m > MV_DOT_MAX_ROWS) {
         int8_t* xq;
         float* xd;
         split_q8k_ptrs(ws, k, m, &xq, &xd);
         hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
         if (e != hipSuccess) return e;
-        return type == T_Q4K ? launch_mv_mfma<T_Q4K>(w, y, n, k, m, xq, xd, s)
-                             : launch_mv_mfma<T_Q6K>(w, y, n, k, m, xq, xd, s);
+        return type == T_Q4K ? launch_mv_mfma<T_Q4K>(w, y, n, k, m, xq, xd, epi, s)
+                             : launch_mv_mfma<T_Q6K>(w, y, n, k, m, xq, xd, epi, s);
     }
     switch (type) {
-        case T_Q4K: return launch_type<T_Q4K>(w, x, y, (int)n, (int)k, (int)m, s);
-        case T_Q6K: return launch_type<T_Q6K>(w, x, y, (int)n, (int)k, (int)m, s);
-        case T_Q8_0: return launch_type<T_Q8_0>(w, x, y, (int)n, (int)k, (int)m, s);
+        case T_Q4K: return launch_type<T_Q4K>(w, x, y, (int)n, (int)k, (int)m, epi, s);
+        case T_Q6K: return launch_type<T_Q6K>(w, x, y, (int)n, (int)k, (int)m, epi, s);
+        case T_Q8_0: return launch_type<T_Q8_0>(w, x, y, (int)n, (int)k, (int)m, epi, s);
     }
     return hipErrorInvalidValue;
 }

@@ -32,7 +32,7 @@ size_t moe_workspace_ints(int64_t n_experts, int64_t planes) { return 2 + 4 * (s
 // follows the LDS atomics, but every plane's dot is computed on its own, so
 // no result depends on it.
 __global__ __launch_bounds__(1024) void k_moe_route(const uint32_t* __restrict__ ids, int planes, int E, int* ws,
-                                                    int* sticky, float* __restrict__ y, int n) {
+                                                    int* sticky, float* __restrict__ y, float* __restrict__ y2, int n) {
     extern __shared__ int s_mem[];  // [E] counts, then [E] cursors
     __shared__ int s_part[1024];
     __shared__ int s_bad, s_active;
@@ -56,6 +56,8 @@ __global__ __launch_bounds__(1024) void k_moe_route(const uint32_t* __restrict__
         } else {
             s_bad = 1;
             for (int r = 0; r < n; r++) y[(int64_t)p * n + r] = 0.0f;
+            if (y2)
+                for (int r = 0; r < n; r++) y2[(int64_t)p * n + r] = 0.0f;
         }
     }
     __syncthreads();
@@ -201,7 +203,13 @@ __device__ __forceinline__ void dequant_task(const uint8_t* __restrict__ row, in
 template <int TYPE, int LPR, int PG>
 __global__ __launch_bounds__(256) void k_moe_rows(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                   float* __restrict__ Y, const int* __restrict__ ws, int E, int n,
-                                                  int K, int in_dim1, int topk) {
+                                                  int K, int in_dim1, int topk, const uint8_t* __restrict__ W2,
+                                                  float* __restrict__ Y2) {
+    // the second weight of a pair (gate, up) is grid layer z = 1
+    if (blockIdx.z) {
+        W = W2;
+        Y = Y2;
+    }
     using Tr = MoeTraits<TYPE>;
     constexpr int RPW = 64 / LPR;  // rows per wave
     const int* count = ws + 2;
@@ -345,12 +353,23 @@ constexpr int MOE_LDS = 72 * 1024;  // bytes of staged planes and run sums
 // wave, 64 / LPR groups of LPR lanes each own R consecutive rows and walk
 // the row's tasks LPR apart (TPL of them loaded at once); a lane's R rows
 // share its activation reads.
-template <int TYPE, int LPR, int R, int TPL>
+// A gate/up pair (indexed_moe_forward_pair, mod.rs:1365-1455) is one launch
+// of two grid layers, z = 1 reading W2 into Y2.  GLU (indexed_moe_forward
+// _glu_as, mod.rs:1457-1531): a lane holds R rows of the gate W and the same
+// R rows of the up weight W2, and stores silu(gate) * up, the SwiGLU's
+// element (silu_mul order) over the two sums the pair would store.
+template <int TYPE, int LPR, int R, int TPL, bool GLU>
 __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                  float* __restrict__ Y, const int* __restrict__ ws, int E, int n,
-                                                 int K, int in_dim1, int topk, int pgmax) {
+                                                 int K, int in_dim1, int topk, int pgmax,
+                                                 const uint8_t* __restrict__ W2, float* __restrict__ Y2) {
     using Tr = MvTraits<TYPE>;
     constexpr int NR = MoeRuns<TYPE>::N;
+    constexpr int RR = GLU ? 2 * R : R;  // weight rows a lane holds
+    if (!GLU && blockIdx.z) {
+        W = W2;
+        Y = Y2;
+    }
     // [pgmax][KP] planes, then [pgmax][K / 16] run sums.  A plane stores
     // element e at e + 4 (e / 64): the eight tasks of a superblock read
     // 16-byte pieces 16 or 48 elements apart, which this spreads over
@@ -370,29 +389,30 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
     const int grp = lane / LPR, tl = lane % LPR;
     const int row0 = ((blockIdx.x * 4 + wave) * (64 / LPR) + grp) * R;
     const int64_t rowbytes = (int64_t)(K / Tr::BE) * Tr::BB;
-    const uint8_t* wrow[R];
+    const uint8_t* wrow[RR];
 #pragma unroll
-    for (int r = 0; r < R; r++) wrow[r] = W + ((int64_t)e * n + min(row0 + r, n - 1)) * rowbytes;
+    for (int r = 0; r < RR; r++)
+        wrow[r] = (r < R ? W : W2) + ((int64_t)e * n + min(row0 + r % R, n - 1)) * rowbytes;
     const int T = (K / Tr::BE) * Tr::P;
     const int k16 = K >> 4;
 
     for (int g0 = 0; g0 < np; g0 += pgmax) {
         const int pg = min(pgmax, np - g0);
-        float acc[R][MOE_PG];
+        float acc[RR][MOE_PG];
 #pragma unroll
-        for (int r = 0; r < R; r++)
+        for (int r = 0; r < RR; r++)
 #pragma unroll
             for (int q = 0; q < MOE_PG; q++) acc[r][q] = 0.0f;
         // tasks in chunks of TPL per lane, every load of a chunk in flight
         // at once (rows of up to TPL * LPR tasks are a single chunk)
         for (int c0 = 0; c0 < T; c0 += TPL * LPR) {
-            TaskData td[TPL][R];
+            TaskData td[TPL][RR];
 #pragma unroll
             for (int c = 0; c < TPL; c++) {
                 const int ti = c0 + c * LPR + tl;
                 const int tc = ti < T ? ti : 0;
 #pragma unroll
-                for (int r = 0; r < R; r++) load_task<TYPE>(wrow[r], tc / Tr::P, tc % Tr::P, td[c][r]);
+                for (int r = 0; r < RR; r++) load_task<TYPE>(wrow[r], tc / Tr::P, tc % Tr::P, td[c][r]);
             }
             if (c0 == 0) {
                 // stage planes g0 .. g0 + pg of this expert (the first
@@ -423,9 +443,9 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
             for (int c = 0; c < TPL; c++) {
                 const int ti = c0 + c * LPR + tl;
                 if (ti < T) {
-                    float qv[R][NR][16], ra[R][NR], rb[R][NR];
+                    float qv[RR][NR][16], ra[RR][NR], rb[RR][NR];
 #pragma unroll
-                    for (int r = 0; r < R; r++) {
+                    for (int r = 0; r < RR; r++) {
                         WPrep<TYPE> wp;
                         prep_task<TYPE>(td[c][r], ti % Tr::P, wp);
                         task_runs<TYPE>(wp, qv[r], ra[r], rb[r]);
@@ -439,14 +459,14 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
                             const float* xq = xs + q * KP;
 #pragma unroll
                             for (int u = 0; u < NR; u++) {
-                                float dq[R];
+                                float dq[RR];
 #pragma unroll
-                                for (int r = 0; r < R; r++) dq[r] = 0.0f;
+                                for (int r = 0; r < RR; r++) dq[r] = 0.0f;
 #pragma unroll
                                 for (int i4 = 0; i4 < 4; i4++) {
                                     const float4 xv = *(const float4*)(xq + off[u] + 4 * (off[u] >> 6) + 4 * i4);
 #pragma unroll
-                                    for (int r = 0; r < R; r++) {
+                                    for (int r = 0; r < RR; r++) {
                                         dq[r] = __builtin_fmaf(qv[r][u][4 * i4], xv.x, dq[r]);
                                         dq[r] = __builtin_fmaf(qv[r][u][4 * i4 + 1], xv.y, dq[r]);
                                         dq[r] = __builtin_fmaf(qv[r][u][4 * i4 + 2], xv.z, dq[r]);
@@ -455,7 +475,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
                                 }
                                 const float s16 = sx[q * k16 + (off[u] >> 4)];
 #pragma unroll
-                                for (int r = 0; r < R; r++)
+                                for (int r = 0; r < RR; r++)
                                     acc[r][q] =
                                         __builtin_fmaf(ra[r][u], dq[r], __builtin_fmaf(-rb[r][u], s16, acc[r][q]));
                             }
@@ -471,7 +491,11 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
                 const int pl = sorted[p0 + g0 + q];
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    const float v = group_sum<LPR>(acc[r][q]);
+                    float v = group_sum<LPR>(acc[r][q]);
+                    if constexpr (GLU) {
+                        const float u = group_sum<LPR>(acc[R + r][q]);
+                        v = v / (1.0f + expf(-v)) * u;
+                    }
                     if (tl == 0 && row0 + r < n) Y[(int64_t)pl * n + row0 + r] = v;
                 }
             }
@@ -479,83 +503,133 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
     }
 }
 
-template <int TYPE, int LPR, int R>
+// The weights of one call: w alone (MOE_ONE), w and w2 into y and y2
+// (MOE_PAIR), or silu(w . x) * (w2 . x) into y (MOE_GLU).
+struct MoeOut {
+    int mode;
+    const void* w2;
+    float* y2;
+};
+
+template <int TYPE, int LPR, int R, bool GLU>
 static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
-                              int in_dim1, int topk, int max_slots, int pgmax, hipStream_t s) {
+                              int in_dim1, int topk, int max_slots, int pgmax, const MoeOut& o, hipStream_t s) {
     constexpr int TPL = 4;
     constexpr int ROWS = 4 * (64 / LPR) * R;
     const size_t shm = (size_t)pgmax * (K + 2 * (K / 16)) * sizeof(float);
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_moe_lds<TYPE, LPR, R, TPL>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_moe_lds<TYPE, LPR, R, TPL, GLU>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, MOE_LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    dim3 grid((n + ROWS - 1) / ROWS, max_slots);
-    hipLaunchKernelGGL((k_moe_lds<TYPE, LPR, R, TPL>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ws, E, n, K,
-                       in_dim1, topk, pgmax);
+    dim3 grid((n + ROWS - 1) / ROWS, max_slots, o.mode == MOE_PAIR ? 2 : 1);
+    hipLaunchKernelGGL((k_moe_lds<TYPE, LPR, R, TPL, GLU>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ws, E,
+                       n, K, in_dim1, topk, pgmax, (const uint8_t*)o.w2, o.y2);
     return hipGetLastError();
 }
 
 // LPR: a row's tasks spread over LPR lanes, up to 4 per lane.
-template <int TYPE>
+// GLU holds each row of both weights: half the rows per lane of the plain
+// kernel, the same registers.
+template <int TYPE, bool GLU>
 static hipError_t moe_lds_type(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
-                               int in_dim1, int topk, int max_slots, int pgmax, hipStream_t s) {
+                               int in_dim1, int topk, int max_slots, int pgmax, const MoeOut& o, hipStream_t s) {
     using Tr = MvTraits<TYPE>;
-    constexpr int R = TYPE == T_Q6K ? 1 : 2;
+    constexpr int R = (TYPE == T_Q6K || GLU) ? 1 : 2;
     const int T = (K / Tr::BE) * Tr::P;
-    if (T > 32) return moe_lds_cfg<TYPE, 16, R>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, s);
-    if (T > 16) return moe_lds_cfg<TYPE, 8, R>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, s);
-    return moe_lds_cfg<TYPE, 4, R>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, s);
+    if (T > 32) return moe_lds_cfg<TYPE, 16, R, GLU>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, o, s);
+    if (T > 16) return moe_lds_cfg<TYPE, 8, R, GLU>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, o, s);
+    return moe_lds_cfg<TYPE, 4, R, GLU>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, pgmax, o, s);
 }
 
 template <int TYPE, int LPR>
 static hipError_t moe_rows_lpr(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
-                               int in_dim1, int topk, int max_slots, hipStream_t s) {
+                               int in_dim1, int topk, int max_slots, const void* w2, float* y2, hipStream_t s) {
     constexpr int RPW = 64 / LPR;
-    dim3 grid((n + 4 * RPW - 1) / (4 * RPW), max_slots);
+    dim3 grid((n + 4 * RPW - 1) / (4 * RPW), max_slots, w2 ? 2 : 1);
     hipLaunchKernelGGL((k_moe_rows<TYPE, LPR, 4>), grid, dim3(256), 0, s, (const uint8_t*)w, x, y, ws, E, n, K,
-                       in_dim1, topk);
+                       in_dim1, topk, (const uint8_t*)w2, y2);
     return hipGetLastError();
 }
 
 template <int TYPE>
 static hipError_t moe_rows_type(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
-                                int in_dim1, int topk, int max_slots, hipStream_t s) {
+                                int in_dim1, int topk, int max_slots, const void* w2, float* y2, hipStream_t s) {
     using Tr = MoeTraits<TYPE>;
     int T = (K / Tr::BE) * Tr::P;
-    if (T > 32) return moe_rows_lpr<TYPE, 64>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, s);
-    if (T > 16) return moe_rows_lpr<TYPE, 32>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, s);
-    if (T > 8) return moe_rows_lpr<TYPE, 16>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, s);
-    return moe_rows_lpr<TYPE, 8>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, s);
+    if (T > 32) return moe_rows_lpr<TYPE, 64>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, w2, y2, s);
+    if (T > 16) return moe_rows_lpr<TYPE, 32>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, w2, y2, s);
+    if (T > 8) return moe_rows_lpr<TYPE, 16>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, w2, y2, s);
+    return moe_rows_lpr<TYPE, 8>(w, x, y, ws, E, n, K, in_dim1, topk, max_slots, w2, y2, s);
+}
+
+// silu(g) * u elementwise, the fallback GLU for rows too long to stage
+__global__ __launch_bounds__(256) void k_silu_mul(float* __restrict__ g, const float* __restrict__ u, int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < count) {
+        const float v = g[i];
+        g[i] = v / (1.0f + expf(-v)) * u[i];
+    }
+}
+
+size_t moe_workspace_bytes(int64_t n_experts, int64_t planes, int64_t n, int64_t k, int mode) {
+    size_t b = (moe_workspace_ints(n_experts, planes) * sizeof(int) + 255) & ~(size_t)255;
+    if (mode == MOE_GLU && !moe_stages(k)) b += (size_t)planes * n * sizeof(float);
+    return b;
+}
+
+bool moe_stages(int64_t k) {
+    const int64_t per_plane = (k + 2 * (k / 16)) * (int64_t)sizeof(float);
+    return MOE_LDS / per_plane >= 1 && (k & 15) == 0;
 }
 
 hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, const float* x, int64_t batch,
                       int64_t in_dim1, const uint32_t* ids, int64_t topk, float* y, int* ws, int* sticky,
-                      hipStream_t s) {
+                      int mode, const void* w2, float* y2, hipStream_t s) {
     int planes = (int)(batch * topk);
+    // planes of bad ids are zeroed in every output
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 2 * E * sizeof(int), s, ids, planes, (int)E, ws, sticky, y,
-                       (int)n);
+                       mode == MOE_PAIR ? y2 : nullptr, (int)n);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     int max_slots = (int)(E < planes ? E : planes);
     const int64_t per_plane = (k + 2 * (k / 16)) * (int64_t)sizeof(float);
     const int pgmax = MOE_LDS / per_plane < MOE_PG ? (int)(MOE_LDS / per_plane) : MOE_PG;
-    if (pgmax >= 1 && (k & 15) == 0) {
+    const MoeOut o{mode, w2, y2};
+    const int Ei = (int)E, ni = (int)n, ki = (int)k, d1 = (int)in_dim1, tk = (int)topk;
+    if (moe_stages(k)) {
+        if (mode == MOE_GLU) {
+            switch (type) {
+                case T_Q4K: return moe_lds_type<T_Q4K, true>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pgmax, o, s);
+                case T_Q6K: return moe_lds_type<T_Q6K, true>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pgmax, o, s);
+                case T_Q8_0: return moe_lds_type<T_Q8_0, true>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pgmax, o, s);
+            }
+            return hipErrorInvalidValue;
+        }
         switch (type) {
-            case T_Q4K: return moe_lds_type<T_Q4K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, pgmax, s);
-            case T_Q6K: return moe_lds_type<T_Q6K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, pgmax, s);
-            case T_Q8_0: return moe_lds_type<T_Q8_0>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, pgmax, s);
+            case T_Q4K: return moe_lds_type<T_Q4K, false>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pgmax, o, s);
+            case T_Q6K: return moe_lds_type<T_Q6K, false>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pgmax, o, s);
+            case T_Q8_0: return moe_lds_type<T_Q8_0, false>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pgmax, o, s);
         }
         return hipErrorInvalidValue;
     }
+    // rows too long to stage: a GLU is the pair (up into the workspace
+    // after the routing ints) and one elementwise launch
+    const void* pw2 = mode == MOE_ONE ? nullptr : w2;
+    float* py2 = mode == MOE_PAIR ? y2 : mode == MOE_GLU
+        ? (float*)((uint8_t*)ws + ((moe_workspace_ints(E, planes) * sizeof(int) + 255) & ~(size_t)255)) : nullptr;
     switch (type) {
-        case T_Q4K: return moe_rows_type<T_Q4K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, s);
-        case T_Q6K: return moe_rows_type<T_Q6K>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, s);
-        case T_Q8_0: return moe_rows_type<T_Q8_0>(w, x, y, ws, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, max_slots, s);
+        case T_Q4K: err = moe_rows_type<T_Q4K>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pw2, py2, s); break;
+        case T_Q6K: err = moe_rows_type<T_Q6K>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pw2, py2, s); break;
+        case T_Q8_0: err = moe_rows_type<T_Q8_0>(w, x, y, ws, Ei, ni, ki, d1, tk, max_slots, pw2, py2, s); break;
+        default: return hipErrorInvalidValue;
     }
-    return hipErrorInvalidValue;
+    if (err != hipSuccess || mode != MOE_GLU) return err;
+    const int64_t count = (int64_t)planes * n;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, y, py2, count);
+    return hipGetLastError();
 }
 
 }  // namespace lloom

@@ -422,13 +422,44 @@ __device__ __forceinline__ void store_out<uint16_t>(uint16_t* y, int64_t i, floa
     y[i] = f32_to_f16(v);
 }
 
+// Row gather of the dequantizers (QTensor::embedding, mod.rs:1101-1137; the
+// CPU arm's QuantizedType::embedding, :812-838): output block ob belongs to
+// output row ob / rb and reads block ob % rb of weight row ids[row].  With
+// ids null the map is the identity (dequantize).  An id >= rows stores a
+// zero row and raises flag[0] (sticky) and flag[1] (this call).
+struct RowMap {
+    const uint32_t* ids;
+    int64_t rb, rows;
+    int* flag;
+};
+
+// The source block of output block ob, or -1 for a bad id.
+__device__ __forceinline__ int64_t src_block(int64_t ob, const RowMap& rm) {
+    if (!rm.ids) return ob;
+    const int64_t r = ob / rm.rb;
+    const uint32_t id = rm.ids[r];
+    if ((int64_t)id >= rm.rows) {
+        if (ob % rm.rb == 0) {
+            atomicOr(&rm.flag[0], 1);
+            atomicOr(&rm.flag[1], 1);
+        }
+        return -1;
+    }
+    return (int64_t)id * rm.rb + (ob - r * rm.rb);
+}
+
 // BlockQ8_0::to_float (k_quants.rs:720-736): y = q * f32(d).
 template <typename OutT>
 __global__ __launch_bounds__(256) void k_dequant_q8_0(const uint8_t* __restrict__ w, OutT* __restrict__ y,
-                                                      int64_t elems) {
+                                                      int64_t elems, RowMap rm) {
     int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= elems) return;
-    const uint8_t* b = w + (i >> 5) * Q8_0_BYTES;
+    const int64_t sb = src_block(i >> 5, rm);
+    if (sb < 0) {
+        store_out(y, i, 0.0f);
+        return;
+    }
+    const uint8_t* b = w + sb * Q8_0_BYTES;
     float d = f16_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
     store_out(y, i, (float)(int8_t)b[2 + (i & 31)] * d);
 }
@@ -436,10 +467,15 @@ __global__ __launch_bounds__(256) void k_dequant_q8_0(const uint8_t* __restrict_
 // BlockQ8K::to_float (k_quants.rs:2440-2451): y = d * q.
 template <typename OutT>
 __global__ __launch_bounds__(256) void k_dequant_q8k(const uint8_t* __restrict__ w, OutT* __restrict__ y,
-                                                     int64_t elems) {
+                                                     int64_t elems, RowMap rm) {
     int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= elems) return;
-    const uint8_t* b = w + (i >> 8) * Q8K_BYTES;
+    const int64_t sb = src_block(i >> 8, rm);
+    if (sb < 0) {
+        store_out(y, i, 0.0f);
+        return;
+    }
+    const uint8_t* b = w + sb * Q8K_BYTES;
     float d = *(const float*)b;
     store_out(y, i, d * (float)(int8_t)b[Q8K_QS + (i & 255)]);
 }
@@ -449,11 +485,16 @@ __global__ __launch_bounds__(256) void k_dequant_q8k(const uint8_t* __restrict__
 // 64 threads per superblock, each 2 bytes -> 4 outputs.
 template <typename OutT>
 __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ w, OutT* __restrict__ y,
-                                                     int64_t nblocks) {
+                                                     int64_t nblocks, RowMap rm) {
     int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     int t = threadIdx.x & 63;
-    const uint8_t* b = w + blk * Q4K_BYTES;
+    const int64_t sb = src_block(blk, rm);
+    if (sb < 0) {
+        for (int e = 0; e < 4; e++) store_out(y, blk * 256 + 4 * t + e, 0.0f);
+        return;
+    }
+    const uint8_t* b = w + sb * Q4K_BYTES;
     float d = f16_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
     float mn = f16_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
     const uint8_t* sc = b + 4;
@@ -475,11 +516,16 @@ __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__
 // q = (4 low bits | 2 high bits) - 32.  64 threads per superblock.
 template <typename OutT>
 __global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t* __restrict__ w, OutT* __restrict__ y,
-                                                     int64_t nblocks) {
+                                                     int64_t nblocks, RowMap rm) {
     int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     int t = threadIdx.x & 63;
-    const uint8_t* b = w + blk * Q6K_BYTES;
+    const int64_t sb = src_block(blk, rm);
+    if (sb < 0) {
+        for (int e = 0; e < 4; e++) store_out(y, blk * 256 + 4 * t + e, 0.0f);
+        return;
+    }
+    const uint8_t* b = w + sb * Q6K_BYTES;
     float d = f16_to_f32((uint32_t)b[Q6K_D] | ((uint32_t)b[Q6K_D + 1] << 8));
     int h = t >> 5, l = t & 31;
     const uint8_t* ql = b + 64 * h;
@@ -532,22 +578,22 @@ hipError_t launch_quantize_weights(int type, const float* x, void* out, int64_t 
 }
 
 template <typename OutT>
-static hipError_t dequant_t(int type, const void* w, OutT* y, int64_t elems, hipStream_t s) {
+static hipError_t dequant_t(int type, const void* w, OutT* y, int64_t elems, const RowMap& rm, hipStream_t s) {
     const uint8_t* b = (const uint8_t*)w;
     switch (type) {
         case T_Q8_0:
-            hipLaunchKernelGGL(k_dequant_q8_0<OutT>, dim3(grid_of(elems, 256)), dim3(256), 0, s, b, y, elems);
+            hipLaunchKernelGGL(k_dequant_q8_0<OutT>, dim3(grid_of(elems, 256)), dim3(256), 0, s, b, y, elems, rm);
             break;
         case T_Q8K:
-            hipLaunchKernelGGL(k_dequant_q8k<OutT>, dim3(grid_of(elems, 256)), dim3(256), 0, s, b, y, elems);
+            hipLaunchKernelGGL(k_dequant_q8k<OutT>, dim3(grid_of(elems, 256)), dim3(256), 0, s, b, y, elems, rm);
             break;
         case T_Q4K:
             hipLaunchKernelGGL(k_dequant_q4k<OutT>, dim3(grid_of(elems / 256, 4)), dim3(256), 0, s, b, y,
-                               elems / 256);
+                               elems / 256, rm);
             break;
         case T_Q6K:
             hipLaunchKernelGGL(k_dequant_q6k<OutT>, dim3(grid_of(elems / 256, 4)), dim3(256), 0, s, b, y,
-                               elems / 256);
+                               elems / 256, rm);
             break;
         default: return hipErrorInvalidValue;
     }
@@ -555,8 +601,17 @@ static hipError_t dequant_t(int type, const void* w, OutT* y, int64_t elems, hip
 }
 
 hipError_t launch_dequantize(int type, const void* w, void* y, int out_dtype, int64_t elems, hipStream_t s) {
-    if (out_dtype == T_F16) return dequant_t<uint16_t>(type, w, (uint16_t*)y, elems, s);
-    return dequant_t<float>(type, w, (float*)y, elems, s);
+    const RowMap rm{nullptr, 1, 0, nullptr};
+    if (out_dtype == T_F16) return dequant_t<uint16_t>(type, w, (uint16_t*)y, elems, rm, s);
+    return dequant_t<float>(type, w, (float*)y, elems, rm, s);
+}
+
+hipError_t launch_embedding(int type, const void* w, int64_t rows, int64_t hidden, const uint32_t* ids, int64_t n_ids,
+                            void* y, int out_dtype, int* flag, hipStream_t s) {
+    const RowMap rm{ids, hidden / block_elems(type), rows, flag};
+    const int64_t elems = n_ids * hidden;
+    if (out_dtype == T_F16) return dequant_t<uint16_t>(type, w, (uint16_t*)y, elems, rm, s);
+    return dequant_t<float>(type, w, (float*)y, elems, rm, s);
 }
 
 }  // namespace lloom

@@ -57,7 +57,13 @@ def lib():
                 "lloom_hip_quantize_act": ([vp, i32, vp, i64, i64, vp, vp], i32),
                 "lloom_hip_dequantize": ([vp, i32, vp, i64, vp, i32, vp], i32),
                 "lloom_hip_qmatmul": ([vp, i32, vp, i64, i64, vp, i32, i64, vp, i32, vp], i32),
+                "lloom_hip_qmatmul_store": ([vp, i32, vp, i64, i64, vp, i32, i64, vp, i32, i32, vp], i32),
                 "lloom_hip_moe_matmul": ([vp, i32, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, i32, vp], i32),
+                "lloom_hip_moe_matmul_pair": ([vp, i32, vp, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, vp, i32,
+                                               vp], i32),
+                "lloom_hip_moe_matmul_glu": ([vp, i32, vp, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, i32, vp],
+                                             i32),
+                "lloom_hip_embedding": ([vp, i32, vp, i64, i64, vp, i64, vp, i32, i32, vp], i32),
                 "lloom_hip_synth_normal": ([ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp, i64], i32),
                 "lloom_hip_synth_uniform": ([ctypes.c_uint64, ctypes.c_float, ctypes.c_float, vp, i64], i32),
             }

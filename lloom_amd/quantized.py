@@ -6,7 +6,10 @@ Names, argument meaning and refusals follow lloom-tensor/src/quantized/mod.rs:
   QTensor.from_data    mod.rs:136-223   (QStorage::from_data: an upload)
   QTensor.dequantize   mod.rs:1065-1086 (and dequantize_f16)
   QTensor.indexed_moe_forward{,_with,_as}  mod.rs:1560-1645
+  QTensor.indexed_moe_forward_pair / _glu_as  mod.rs:1365-1531
+  QTensor.embedding    mod.rs:1101-1137
   QMatMul.from_qtensor / forward          mod.rs:1698-1729, 2022-2025
+  QMatMul.forward_silu / forward_mul_into, MvStore  mod.rs:1667-1696, 2102-2156
   MoeArm               mod.rs:2290-2310
 Tensors are torch tensors on the GPU (device memory and streams only); the
 arithmetic is the C ABI's.
@@ -95,6 +98,13 @@ def set_prefill_mma(mode, device=0):
     exact integer operands on fp16 MFMA) or MMA_INT8 (two int8 scale planes).
     Both compute the CPU arm's integer sums exactly."""
     check(lib().lloom_hip_ctx_set_prefill_mma(_ctx(device), mode))
+
+
+class MvStore(enum.IntEnum):
+    """The matmul's store block (MvStore, mod.rs:1667-1696): the value
+    stored is silu(v) or y * v instead of v (LLOOM_HIP_STORE_*)."""
+    Silu = 1
+    MulInto = 2
 
 
 # ------------------------------------------------------------ QTensor ---
@@ -199,9 +209,67 @@ class QTensor:
                                          k, _ptr(x), batch, in_dim1, _ptr(ids), topk, _ptr(y), 0, _stream(x)))
         return y
 
-    def indexed_moe_forward_pair(self, up, x, ids, arm=None):
-        """Gate and up of one routed layer: two calls (mod.rs:1472-1475 off Metal)."""
-        return self.indexed_moe_forward(x, ids, arm), up.indexed_moe_forward(x, ids, arm)
+    def _moe_check(self, up, x, ids):
+        if len(self.shape) != 3:
+            raise LloomHipError(3, f"indexed_moe_forward: weight {self.shape} is not [experts, n, k]")
+        if up.dtype != self.dtype or up.shape != self.shape:
+            raise LloomHipError(3, f"indexed_moe_forward_pair: gate {self.dtype.name}{list(self.shape)} and "
+                                   f"up {up.dtype.name}{list(up.shape)} differ")
+        n_experts, n, k = self.shape
+        if x.dim() != 3 or ids.dim() != 2:
+            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
+        batch, in_dim1, k_in = x.shape
+        batch_ids, topk = ids.shape
+        if k_in != k or batch != batch_ids or (in_dim1 != 1 and in_dim1 != topk):
+            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
+        return n_experts, n, k, batch, in_dim1, topk
+
+    def indexed_moe_forward_pair(self, up, x, ids, arm=None, strict=True):
+        """Gate and up of one routed layer in ONE launch (the reference's
+        Metal kernel_mul_mv_id2, mod.rs:1365-1455): each half is bit for bit
+        what indexed_moe_forward computes for it."""
+        n_experts, n, k, batch, in_dim1, topk = self._moe_check(up, x, ids)
+        x = x.to(torch.float32).contiguous()
+        ids = ids.to(torch.int32).contiguous()
+        yg = torch.empty((batch, topk, n), dtype=torch.float32, device=x.device)
+        yu = torch.empty_like(yg)
+        check(lib().lloom_hip_moe_matmul_pair(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage),
+                                              _ptr(up.storage), n_experts, n, k, _ptr(x), batch, in_dim1, _ptr(ids),
+                                              topk, _ptr(yg), _ptr(yu), 1 if strict else 0, _stream(x)))
+        return yg, yu
+
+    indexed_moe_forward_pair_with = indexed_moe_forward_pair
+
+    def indexed_moe_forward_glu_as(self, up, x, ids, arm=None, act=None, strict=True):
+        """silu(gate) * up of the pair in ONE launch (mod.rs:1457-1531).  The
+        reference returns None off Metal and the caller composes; here the
+        fused launch always serves."""
+        n_experts, n, k, batch, in_dim1, topk = self._moe_check(up, x, ids)
+        x = x.to(torch.float32).contiguous()
+        ids = ids.to(torch.int32).contiguous()
+        y = torch.empty((batch, topk, n), dtype=torch.float32, device=x.device)
+        check(lib().lloom_hip_moe_matmul_glu(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage),
+                                             _ptr(up.storage), n_experts, n, k, _ptr(x), batch, in_dim1, _ptr(ids),
+                                             topk, _ptr(y), 1 if strict else 0, _stream(x)))
+        return y
+
+    # QTensor::embedding (mod.rs:1101-1137)
+    def embedding(self, ids, strict=True, f16=False):
+        """Rows ids of a [rows, hidden] weight, dequantized: out shape
+        ids.shape + (hidden,), f32 (or f16, the RNE of the f32 value)."""
+        if len(self.shape) != 2:
+            raise LloomHipError(3, f"embedding: weight {self.shape} is not [rows, hidden]")
+        rows, hidden = self.shape
+        bs = self.dtype.block_size()
+        if hidden % bs:
+            raise LloomHipError(3, f"quantized embedding hidden size {hidden} is not divisible by block size {bs}")
+        out_shape = tuple(ids.shape) + (hidden,)
+        flat = ids.to(device=self.storage.device, dtype=torch.int32).reshape(-1).contiguous()
+        y = torch.empty(out_shape, dtype=torch.float16 if f16 else torch.float32, device=self.storage.device)
+        check(lib().lloom_hip_embedding(_ctx(_dev_index(self.storage)), int(self.dtype), _ptr(self.storage), rows,
+                                        hidden, _ptr(flat), flat.numel(), _ptr(y), 1 if f16 else 0,
+                                        1 if strict else 0, _stream(self.storage)))
+        return y
 
     def __repr__(self):
         return f"QTensor[{list(self.shape)}; {self.dtype.name}]"
@@ -239,6 +307,33 @@ class QMatMul:
         return y
 
     __call__ = forward
+
+    def _store(self, xs, y, store):
+        n, k = self.qtensor.shape
+        if xs.dim() < 2 or xs.shape[-1] != k:
+            raise LloomHipError(3, f"input tensor {tuple(xs.shape)} incompatible with {self.qtensor.shape}")
+        if xs.dtype != torch.float32 or not xs.is_contiguous():
+            raise LloomHipError(2, f"Expected contiguous f32 activations, got {xs.dtype}")
+        m = xs.numel() // k
+        check(lib().lloom_hip_qmatmul_store(_ctx(_dev_index(xs)), int(self.qtensor.dtype), _ptr(self.qtensor.storage),
+                                            n, k, _ptr(xs), 0, m, _ptr(y), 0, int(store), _stream(xs)))
+        return y
+
+    def forward_silu(self, xs):
+        """silu(x . W^T) with the SiLU on the matmul's store, one launch
+        (QMatMul::forward_silu, mod.rs:2102-2120; MvStore::Silu)."""
+        n, _ = self.qtensor.shape
+        y = torch.empty(tuple(xs.shape[:-1]) + (n,), dtype=torch.float32, device=xs.device)
+        return self._store(xs, y, MvStore.Silu)
+
+    def forward_mul_into(self, xs, gate):
+        """gate <- gate * (x . W^T) at the store, one launch
+        (QMatMul::forward_mul_into, mod.rs:2122-2156; MvStore::MulInto).
+        gate is an f32 contiguous [.., n] and is overwritten."""
+        n, _ = self.qtensor.shape
+        if gate.dtype != torch.float32 or not gate.is_contiguous() or gate.numel() != xs.numel() // xs.shape[-1] * n:
+            raise LloomHipError(3, f"forward_mul_into: gate {tuple(gate.shape)} {gate.dtype} does not fit the output")
+        self._store(xs, gate, MvStore.MulInto)
 
     def forward_into(self, xs, y):
         """forward into a preallocated contiguous f32 y [m, n] (xs [m, k] f32

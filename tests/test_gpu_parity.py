@@ -197,6 +197,29 @@ def test_decode_rows_batch_invariant(L, dt):
             assert np.array_equal(part.view(np.uint32), full[:m].view(np.uint32)), (full_m, m)
 
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
+def test_mfma_decode_repeatable(L, dt):
+    """3..16 rows run the workspace quantizer and the MFMA decode kernel:
+    calls of other shapes in between (other k, other row counts, the shared
+    workspace rewritten) must leave every repeat of a call bit-identical and
+    within tolerance of the oracle."""
+    rng = np.random.default_rng(21)
+    shapes = [(1000, 4096, 5), (4100, 2048, 16), (300, 8192, 9), (64, 512, 3)]
+    prepared = []
+    for n, k, m in shapes:
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        qt = L.QTensor.quantize(_cuda(w), dt)
+        prepared.append((L.QMatMul.from_qtensor(qt), _cuda(x), x, qt.data(), n))
+    first = [mm.forward(xd).cpu().numpy() for mm, xd, _, _, _ in prepared]
+    for (mm, xd, x, q, n), y in zip(prepared, first):
+        assert_rows_close(y, O.matmul(dt, x, q, n), what=f"decode dt={dt} n={n} m={x.shape[0]}")
+    for _ in range(2):
+        for (mm, xd, _, _, _), y in zip(prepared[::-1], first[::-1]):
+            again = mm.forward(xd).cpu().numpy()
+            assert np.array_equal(again.view(np.uint32), y.view(np.uint32))
+
+
 def test_qmatmul_rank3_input(L):
     rng = np.random.default_rng(4)
     w = (rng.standard_normal((40, 512)) * 0.02).astype(np.float32)
@@ -311,6 +334,140 @@ def test_moe_out_of_range_expert_is_refused(L):
     assert lib().lloom_hip_ctx_sync(_ctx(0)) == 0
     good = qt.indexed_moe_forward(x, _cuda(np.array([[0, 3], [1, 2]], dtype=np.int32)))
     assert np.isfinite(good.cpu().numpy()).all()
+
+
+# ------------------------------------------------ store epilogues (f3) ---
+
+def _silu32(v):
+    v = np.asarray(v, dtype=np.float32)
+    return (v / (np.float32(1) + np.exp(-v))).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 40])
+def test_forward_silu_and_mul_into(L, dt, m):
+    """QMatMul::forward_silu / forward_mul_into (mod.rs:2102-2156): the
+    stored value is silu(v) (resp. gate * v) of the product the plain
+    forward stores.  Against the oracle: silu is 1.1-Lipschitz, so the
+    matmul bar scaled by 1.1 bounds it; the product into the gate is bounded
+    by the bar times |gate|.  Against the plain forward on the GPU the SiLU
+    store is the same sum through v / (1 + exp(-v))."""
+    rng = np.random.default_rng(40 + m)
+    n, k = 300, 1024
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), dt)
+    mm = L.QMatMul.from_qtensor(qt)
+    xd = _cuda(x)
+    plain = mm.forward(xd).cpu().numpy()
+    want = O.matmul(dt, x, qt.data(), n)
+    rowmax = np.abs(want).max(axis=1, keepdims=True)
+    silu = mm.forward_silu(xd).cpu().numpy()
+    assert np.all(np.abs(silu - _silu32(want)) <= 1.1 * MATMUL_TOL * rowmax + 1e-30)
+    np.testing.assert_allclose(silu, _silu32(plain), rtol=2e-6, atol=1e-7)
+    gate = rng.standard_normal((m, n)).astype(np.float32)
+    g = _cuda(gate)
+    mm.forward_mul_into(xd, g)
+    got = g.cpu().numpy()
+    assert np.all(np.abs(got - gate * want) <= MATMUL_TOL * rowmax * np.abs(gate) + 1e-30)
+    assert np.array_equal(got.view(np.uint32), (gate * plain).astype(np.float32).view(np.uint32))
+
+
+def test_swiglu_silu_then_mul_into(L):
+    """The SwiGLU as two launches: gate's forward_silu, then up's
+    forward_mul_into its buffer = silu(g) * u (silu_mul order)."""
+    rng = np.random.default_rng(7)
+    n, k, m = 512, 2048, 4
+    wg = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wu = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = _cuda(rng.standard_normal((m, k)).astype(np.float32))
+    g = L.QMatMul.from_qtensor(L.QTensor.quantize(_cuda(wg), L.GgmlDType.Q4K))
+    u = L.QMatMul.from_qtensor(L.QTensor.quantize(_cuda(wu), L.GgmlDType.Q4K))
+    buf = g.forward_silu(x)
+    u.forward_mul_into(x, buf)
+    ref = (_silu32(g.forward(x).cpu().numpy()) * u.forward(x).cpu().numpy()).astype(np.float32)
+    np.testing.assert_allclose(buf.cpu().numpy(), ref, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+@pytest.mark.parametrize("k", [768, 2048])
+def test_moe_pair_and_glu(L, dt, k):
+    """indexed_moe_forward_pair: each half bit for bit the single call's;
+    _glu_as: silu(g) * u of those halves (mod.rs:1365-1531)."""
+    rng = np.random.default_rng(k + dt)
+    E, n, batch, topk = 16, 96, 6, 4
+    wg = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
+    wu = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
+    x = _cuda(rng.standard_normal((batch, 1, k)).astype(np.float32))
+    ids = _cuda(rng.integers(0, E, (batch, topk)).astype(np.int32))
+    qg, qu = L.QTensor.quantize(_cuda(wg), dt), L.QTensor.quantize(_cuda(wu), dt)
+    sg = qg.indexed_moe_forward(x, ids).cpu().numpy()
+    su = qu.indexed_moe_forward(x, ids).cpu().numpy()
+    pg, pu = qg.indexed_moe_forward_pair(qu, x, ids)
+    assert np.array_equal(pg.cpu().numpy().view(np.uint32), sg.view(np.uint32))
+    assert np.array_equal(pu.cpu().numpy().view(np.uint32), su.view(np.uint32))
+    glu = qg.indexed_moe_forward_glu_as(qu, x, ids).cpu().numpy()
+    np.testing.assert_allclose(glu, _silu32(sg) * su, rtol=2e-6, atol=1e-7)
+    want = O.matmul_indexed(dt, qg.data(), E, n, k, x.cpu().numpy(), ids.cpu().numpy().astype(np.uint32))
+    assert_rows_close(sg, want, what="moe gate vs oracle")
+
+
+def test_moe_pair_bad_id_zeroes_both(L):
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((4, 8, 256)) * 0.05).astype(np.float32)
+    qg = L.QTensor.quantize(_cuda(w), L.GgmlDType.Q4K)
+    qu = L.QTensor.quantize(_cuda(w * 2), L.GgmlDType.Q4K)
+    x = _cuda(rng.standard_normal((2, 1, 256)).astype(np.float32))
+    bad = _cuda(np.array([[0, 4], [1, 2]], dtype=np.int32))
+    with pytest.raises(L.LloomHipError) as e:
+        qg.indexed_moe_forward_pair(qu, x, bad)
+    assert e.value.name == "EEXPERT"
+    yg, yu = qg.indexed_moe_forward_pair(qu, x, bad, strict=False)
+    assert np.all(yg[0, 1].cpu().numpy() == 0) and np.all(yu[0, 1].cpu().numpy() == 0)
+    from lloom_amd.quantized import _ctx
+    from lloom_amd.lib import lib
+
+    assert lib().lloom_hip_ctx_sync(_ctx(0)) == 4
+    with pytest.raises(L.LloomHipError):
+        qg.indexed_moe_forward_pair(L.QTensor.quantize(_cuda(w[:, :4]), L.GgmlDType.Q4K), x, bad)
+
+
+# ---------------------------------------------------------- embedding (f4) ---
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
+def test_embedding_bit_exact(L, dt):
+    """QTensor::embedding (mod.rs:1101-1137): rows of to_float, bit-exact,
+    ids of any shape; f16 out is the RNE of the f32 rows."""
+    rng = np.random.default_rng(dt)
+    rows, hidden = 300, 512
+    w = rng.standard_normal((rows, hidden)).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), dt)
+    full = O.dequantize(dt, qt.data(), rows * hidden).reshape(rows, hidden)
+    ids = rng.integers(0, rows, (3, 7)).astype(np.int32)
+    ids[0, 0] = rows - 1
+    ids[0, 1] = 0
+    got = qt.embedding(_cuda(ids)).cpu().numpy()
+    assert got.shape == (3, 7, hidden)
+    assert np.array_equal(got.view(np.uint32), full[ids].view(np.uint32))
+    h = qt.embedding(_cuda(ids), f16=True).cpu().numpy()
+    assert np.array_equal(h.view(np.uint16), full[ids].astype(np.float16).view(np.uint16))
+    assert qt.embedding(_cuda(np.zeros((0,), np.int32))).shape == (0, hidden)
+
+
+def test_embedding_bad_id(L):
+    rng = np.random.default_rng(1)
+    qt = L.QTensor.quantize(_cuda(rng.standard_normal((10, 256)).astype(np.float32)), L.GgmlDType.Q4K)
+    bad = _cuda(np.array([3, 10, 2], dtype=np.int32))
+    with pytest.raises(L.LloomHipError) as e:
+        qt.embedding(bad)
+    assert e.value.name == "EEXPERT" and "out of range" in str(e.value)
+    y = qt.embedding(bad, strict=False).cpu().numpy()
+    assert np.all(y[1] == 0) and np.any(y[0] != 0)
+    from lloom_amd.quantized import _ctx
+    from lloom_amd.lib import lib
+
+    assert lib().lloom_hip_ctx_sync(_ctx(0)) == 4
+    assert lib().lloom_hip_ctx_sync(_ctx(0)) == 0
 
 
 # ------------------------------------------------------------- refusals ---
