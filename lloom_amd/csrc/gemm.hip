@@ -25,6 +25,8 @@
 //   A (activations): lane l holds x8[m = l%32][32j + 16(l/32) + 0..15]
 //   B (weights):     lane l holds q[n = l%32][32j + 16(l/32) + 0..15]
 //   D:               lane l, reg r holds D[m = 8(r/4) + 4(l/32) + r%4][n = l%32]
+#include <cstdlib>
+
 #include "kq_common.hpp"
 #include "kq_quant.hpp"
 #include "kernels.hpp"
@@ -338,7 +340,8 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
                         const int r = 4 * g + u;
                         const int tot = dh[a][b][r] * 8 + dl[a][b][r];
                         const int mn = mh[r] * 64 + ml[r];
-                        out[a][b][r] += dys[u] * ((float)tot * d - (float)mn * dmin);
+                        out[a][b][r] = __builtin_fmaf(dys[u], __builtin_fmaf((float)tot, d, -((float)mn * dmin)),
+                                                      out[a][b][r]);
                     }
                 }
             }
@@ -356,7 +359,10 @@ __global__ __launch_bounds__(G_THREADS) void k_gemm_q4k(const uint8_t* __restric
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm * G_MT * 32 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < m) store_epi(&Y[(int64_t)row * n + col], out[a][b][r], epi);
+                if (row < m) {
+                    if (epi == EPI_STORE) Y[(int64_t)row * n + col] = out[a][b][r];
+                    else store_epi_slow(&Y[(int64_t)row * n + col], out[a][b][r], epi);
+                }
             }
         }
 }
@@ -512,24 +518,30 @@ __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
 __device__ __forceinline__ int x_piece(int kk, int h) { return (kk & 1) + 4 * (kk >> 1) + 2 * h; }
 
 // The weight operands of one step from the lane's 16 bytes: scales of
-// sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles) from the header.
-__device__ __forceinline__ void build_b(const uint4& raw, const uint4& hdr, int c, v8h (&bv)[4]) {
+// sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles) from the header
+// (bscale), then MFMA slice kk (build_kk).
+struct BScale {
+    h2 scl, sch, offl, offh;
+};
+__device__ __forceinline__ BScale bscale(const uint4& hdr, int c) {
     const uint64_t sc8 = (uint64_t)(hdr.y & 0x3F3F3F3Fu) |
                          ((uint64_t)((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u)) << 32);
     const uint32_t scp = (uint32_t)(sc8 >> (16 * c));
     const _Float16 s0 = (_Float16)(float)(scp & 0xffu), s1 = (_Float16)(float)((scp >> 8) & 0xffu);
-    const h2 scl = {s0, s0}, sch = {s1, s1};
-    const h2 offl = {(_Float16)(-1024.0f) * s0, (_Float16)(-1024.0f) * s0};
-    const h2 offh = {(_Float16)(-1024.0f) * s1, (_Float16)(-1024.0f) * s1};
-#pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-        const uint32_t w0 = kk & 1 ? raw.z : raw.x, w1 = kk & 1 ? raw.w : raw.y;
-        const uint32_t m0w = kk < 2 ? (w0 & 0x0F0F0F0Fu) : ((w0 >> 4) & 0x0F0F0F0Fu);
-        const uint32_t m1w = kk < 2 ? (w1 & 0x0F0F0F0Fu) : ((w1 >> 4) & 0x0F0F0F0Fu);
-        const uint2 p0 = nib4_to_h(m0w, kk < 2 ? scl : sch, kk < 2 ? offl : offh);
-        const uint2 p1 = nib4_to_h(m1w, kk < 2 ? scl : sch, kk < 2 ? offl : offh);
-        bv[kk] = __builtin_bit_cast(v8h, make_uint4(p0.x, p0.y, p1.x, p1.y));
-    }
+    BScale b;
+    b.scl = h2{s0, s0};
+    b.sch = h2{s1, s1};
+    b.offl = h2{(_Float16)(-1024.0f) * s0, (_Float16)(-1024.0f) * s0};
+    b.offh = h2{(_Float16)(-1024.0f) * s1, (_Float16)(-1024.0f) * s1};
+    return b;
+}
+__device__ __forceinline__ v8h build_kk(const uint4& raw, const BScale& bs, int kk) {
+    const uint32_t w0 = kk & 1 ? raw.z : raw.x, w1 = kk & 1 ? raw.w : raw.y;
+    const uint32_t m0w = kk < 2 ? (w0 & 0x0F0F0F0Fu) : ((w0 >> 4) & 0x0F0F0F0Fu);
+    const uint32_t m1w = kk < 2 ? (w1 & 0x0F0F0F0Fu) : ((w1 >> 4) & 0x0F0F0F0Fu);
+    const uint2 p0 = nib4_to_h(m0w, kk < 2 ? bs.scl : bs.sch, kk < 2 ? bs.offl : bs.offh);
+    const uint2 p1 = nib4_to_h(m1w, kk < 2 ? bs.scl : bs.sch, kk < 2 ? bs.offl : bs.offh);
+    return __builtin_bit_cast(v8h, make_uint4(p0.x, p0.y, p1.x, p1.y));
 }
 
 template <int MT>
@@ -631,14 +643,22 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_AFTER_RAW) : "memory");
     __builtin_amdgcn_s_barrier();
 
-    uint4 hdr[C::NT];
+    // Registers across the loop: the current step's weight bytes (raw) and
+    // scales (bs), the operands of the MFMA slice in flight (bcur) and the
+    // activation fragments of two slices (abuf: slice kk + 1 is read from
+    // LDS while slice kk's MFMAs run).  The next step's bytes are read in
+    // slice 1 and its first operands built in slice 3, so only a step's
+    // first activation read waits on LDS.
+    uint4 hdr[C::NT], raw[C::NT];
+    BScale bs[C::NT];
+    v8h bcur[C::NT];
+    v8h abuf[2][MT];
     read_hdr(0, hdr);
-    v8h bv[2][C::NT][4];  // [step & 1]: operands of the current and the next step
-    {
-        uint4 r0[C::NT];
-        read_raw(0, r0);
+    read_raw(0, raw);
 #pragma unroll
-        for (int b = 0; b < C::NT; b++) build_b(r0[b], hdr[b], 0, bv[0][b]);
+    for (int b = 0; b < C::NT; b++) {
+        bs[b] = bscale(hdr[b], 0);
+        bcur[b] = build_kk(raw[b], bs[b], 0);
     }
 
     for (int sb = 0; sb < nsb; sb++) {
@@ -652,33 +672,62 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
             issue_a(min(s + 2, nsteps - 1), s + 2);
             issue_raw(min(s + 3, nsteps - 1), s + 3);
             __builtin_amdgcn_sched_barrier(0);
-            // 2. the next step's weight bytes (and header at a superblock's end)
-            uint4 rn[C::NT], hn[C::NT];
-            read_raw(s + 1, rn);
-            if (c == 3) read_hdr(sb + 1, hn);
-            // 3. MFMA on step s, unpacking step s + 1's weights in between
 #pragma unroll
-            for (int b = 0; b < C::NT; b++) build_b(rn[b], c == 3 ? hn[b] : hdr[b], (c + 1) & 3, bv[(c + 1) & 1][b]);
+            for (int a = 0; a < MT; a++)
+                abuf[0][a] = *(const v8h*)(A + x_pos(wm * (32 * MT) + a * 32 + c32, x_piece(0, h)));
+            uint4 rawn[C::NT], hn[C::NT];
+            BScale bsn[C::NT];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                v8h av[MT];
+                // 2. the next slice's activations; the next step's bytes
+                if (kk < 3) {
 #pragma unroll
-                for (int a = 0; a < MT; a++)
-                    av[a] = *(const v8h*)(A + x_pos(wm * (32 * MT) + a * 32 + c32, x_piece(kk, h)));
+                    for (int a = 0; a < MT; a++)
+                        abuf[(kk + 1) & 1][a] =
+                            *(const v8h*)(A + x_pos(wm * (32 * MT) + a * 32 + c32, x_piece(kk + 1, h)));
+                }
+                if (kk == 1) {
+                    read_raw(s + 1, rawn);
+                    if (c == 3) read_hdr(sb + 1, hn);
+                }
+                // the reads above stay ahead of this slice's MFMAs (the
+                // scheduler would otherwise sink them to their use)
+                __builtin_amdgcn_sched_barrier(0);
+                // 3. the next slice's weight operands (the next step's first
+                //    in slice 3)
+                v8h bnext[C::NT];
+#pragma unroll
+                for (int b = 0; b < C::NT; b++) {
+                    if (kk < 3) {
+                        bnext[b] = build_kk(raw[b], bs[b], kk + 1);
+                    } else {
+                        bsn[b] = bscale(c == 3 ? hn[b] : hdr[b], (c + 1) & 3);
+                        bnext[b] = build_kk(rawn[b], bsn[b], 0);
+                    }
+                }
+                // 4. this slice's MFMAs
 #pragma unroll
                 for (int a = 0; a < MT; a++)
 #pragma unroll
                     for (int b = 0; b < C::NT; b++) {
                         if (kk == 0 && c == 0) {
                             const v16f z = {};
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[c & 1][b][kk], z, 0, 0, 0);
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(abuf[kk & 1][a], bcur[b], z, 0, 0, 0);
                         } else {
-                            acc[a][b] =
-                                __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[c & 1][b][kk], acc[a][b], 0, 0, 0);
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(abuf[kk & 1][a], bcur[b],
+                                                                              acc[a][b], 0, 0, 0);
                         }
                     }
+#pragma unroll
+                for (int b = 0; b < C::NT; b++) bcur[b] = bnext[b];
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // 4. superblock epilogue: min term on MFMA, then
+#pragma unroll
+            for (int b = 0; b < C::NT; b++) {
+                raw[b] = rawn[b];
+                bs[b] = bsn[b];
+            }
+            // 5. superblock epilogue: min term on MFMA, then
             //    out += dy * (d * D - dmin * Dmin)
             if (c == 3) {
                 const uint8_t* SB = smem + C::SB_OFF + (sb & 1) * C::SB_BYTES;
@@ -709,7 +758,10 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
 #pragma unroll
                             for (int u = 0; u < 4; u++) {
                                 const int r = 4 * g + u;
-                                out[a][b][r] += dys[u] * (d * acc[a][b][r] - dmin * dm[r]);
+                                // fused: the integer sums are exact, the
+                                // f32 combination is within the tolerance
+                                out[a][b][r] = __builtin_fmaf(
+                                    dys[u], __builtin_fmaf(d, acc[a][b][r], -(dmin * dm[r])), out[a][b][r]);
                             }
                         }
                     }
@@ -717,7 +769,7 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
 #pragma unroll
                 for (int b = 0; b < C::NT; b++) hdr[b] = hn[b];
             }
-            // 5. A(s + 1), raw(s + 2), SB(sb + 1) have landed; every wave is
+            // 6. A(s + 1), raw(s + 2), SB(sb + 1) have landed; every wave is
             //    past its reads of the stage and slot the next step's DMA
             //    overwrites (step s's)
             __builtin_amdgcn_sched_barrier(0);
@@ -734,7 +786,10 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm * (32 * MT) + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < m) store_epi(&Y[(int64_t)row * n + col], out[a][b][r], epi);
+                if (row < m) {
+                    if (epi == EPI_STORE) Y[(int64_t)row * n + col] = out[a][b][r];
+                    else store_epi_slow(&Y[(int64_t)row * n + col], out[a][b][r], epi);
+                }
             }
         }
 }
@@ -748,7 +803,22 @@ static bool fits_32bit(int64_t n, int64_t k, int64_t m) {
            m * (k / 256) * 32 < ((int64_t)1 << 31);
 }
 
+// Q4_K up to 64 rows (measured crossover with the x16 GEMM, whose 128-row
+// tiles leave most CUs idle there), and Q6_K at every size, take the MFMA
+// decode kernel with 64 activation rows per workgroup layer (launch_mq).
+// LLOOM_HIP_MQ_MAX_ROWS overrides the Q4_K limit (read once).
+static int64_t mq_max_rows() {
+    static const int64_t v = [] {
+        const char* e = getenv("LLOOM_HIP_MQ_MAX_ROWS");
+        return e ? (int64_t)atoll(e) : (int64_t)64;
+    }();
+    return v;
+}
+
+static bool use_mq(int type, int64_t m) { return type == T_Q6K || (type == T_Q4K && m <= mq_max_rows()); }
+
 size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
+    if (use_mq(type, m)) return split_q8k_bytes(k, m);
     if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
     return matvec_workspace_bytes(type == T_Q4K ? T_Q6K : type, k, 16);
 }
@@ -772,6 +842,7 @@ static hipError_t launch_x16(const void* w, const X16Ptrs& p, float* y, int64_t 
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, int mode, int epi, hipStream_t s) {
+    if (use_mq(type, m)) return launch_mq(type, w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
@@ -801,8 +872,8 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                            y, (int)m, (int)n, (int)k, epi);
         return hipGetLastError();
     }
-    // Q8_0 / Q6_K (and Q4_K past 32-bit offsets): tiles of 16 activation
-    // rows through the decode kernels
+    // Q8_0 (and Q4_K past 32-bit offsets): tiles of 16 activation rows
+    // through the decode kernels
     for (int64_t r = 0; r < m; r += 16) {
         const int64_t mm = m - r < 16 ? m - r : 16;
         hipError_t e = launch_matvec(type, w, x + r * k, y + r * n, n, k, mm, qbuf, epi, s);

@@ -17,7 +17,8 @@ hipError_t launch_embedding(int type, const void* w, int64_t rows, int64_t hidde
                             void* y, int out_dtype, int* flag, hipStream_t s);
 
 // quant.hip: Q8_K activations in the split layout the MFMA kernels read:
-// qs int8 [m][k] then d f32 [k/256][16] (m padded to 16), 256-byte aligned.
+// qs int8 [m][k] then d f32 [k/256][mp] (m padded to mp, a multiple of 16),
+// 256-byte aligned.
 size_t split_q8k_bytes(int64_t k, int64_t m);
 void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d);
 hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s);
@@ -29,6 +30,11 @@ constexpr int MV_DOT_MAX_ROWS = 2;
 size_t matvec_workspace_bytes(int type, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, int epi, hipStream_t s);
+// matvec.hip: Q4_K / Q6_K with any number of rows on the MFMA decode kernel,
+// 64 activation rows per workgroup layer (the weights are re-read per
+// layer): the workspace quantizer, then one launch.
+hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
+                     int epi, hipStream_t s);
 
 // gemm.hip: m > 16 rows.  Q4_K on MFMA (mode: GEMM_F16, exact integer
 // operands on fp16 MFMA, or GEMM_INT8, two int8 scale planes), the

@@ -210,6 +210,10 @@ __device__ __forceinline__ void store_epi(float* p, float v, int epi) {
     else if (epi == EPI_MUL_INTO) v = *p * v;
     *p = v;
 }
+// The same, out of line: for kernels that store many values per lane, so
+// the SiLU's code is not unrolled into every store.
+__device__ __noinline__ void store_epi_slow(float* p, float v, int epi);
+__device__ __noinline__ inline void store_epi_slow(float* p, float v, int epi) { store_epi(p, v, epi); }
 
 __device__ __forceinline__ float wave_max(float v) {
     v = __builtin_fmaxf(v, dpp<DPP_XOR1>(v));

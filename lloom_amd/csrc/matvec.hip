@@ -426,12 +426,16 @@ __device__ __forceinline__ void mf_compute(const MfW<TYPE>& w, const long (&a)[8
     }
 }
 
-template <int TYPE, int KS, int NT>
+// MA > 1 (prefill): a workgroup layer (grid y) covers MA 16-row activation
+// tiles against the same weight tiles, so each weight superblock is unpacked
+// once for 16 MA activation rows; the activation operands then load at the
+// top of each superblock instead of one superblock ahead.
+template <int TYPE, int KS, int NT, int MA>
 __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                      const float* __restrict__ xd, float* __restrict__ Y, int n,
-                                                     int K, int m, int epi) {
+                                                     int K, int m, int mp, int epi) {
     constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
-    __shared__ float4 part[KS > 1 ? KS - 1 : 1][NT][64];
+    __shared__ float4 part[KS > 1 ? KS - 1 : 1][NT][MA][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int nsb = K >> 8;
@@ -439,77 +443,121 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
     const uint8_t* wrow[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) wrow[t] = W + (int64_t)min(blockIdx.x * 16 * NT + 16 * t + c16, n - 1) * rowbytes;
-    const bool arow_ok = c16 < m;
-    const int8_t* xrow = xq + (int64_t)(arow_ok ? c16 : 0) * K + 64 * g;
-    float out[NT][4];
+    const int mt0 = blockIdx.y * MA;  // first activation tile of this layer
+    bool arow_ok[MA];
+    const int8_t* xrow[MA];
 #pragma unroll
-    for (int t = 0; t < NT; t++) out[t][0] = out[t][1] = out[t][2] = out[t][3] = 0.0f;
+    for (int u = 0; u < MA; u++) {
+        const int ar = 16 * (mt0 + u) + c16;
+        arow_ok[u] = ar < m;
+        xrow[u] = xq + (int64_t)(arow_ok[u] ? ar : 0) * K + 64 * g;
+    }
+    float out[NT][MA][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int u = 0; u < MA; u++) out[t][u][0] = out[t][u][1] = out[t][u][2] = out[t][u][3] = 0.0f;
 
     // registers of the superblock in flight (the row and superblock
     // indices are clamped, so no load sits under a divergent branch)
     MfW<TYPE> wc[NT];
-    uint4 avc[4];
+    uint4 avc[MA == 1 ? 4 : 1];
     float4 dyc;
-    auto issue = [&](int sb, MfW<TYPE>(&w)[NT], uint4(&av)[4], float4& dy) {
+    auto issue = [&](int sb, MfW<TYPE>(&w)[NT], uint4(&av)[MA == 1 ? 4 : 1], float4& dy) {
         const int sbc = min(sb, nsb - 1);
 #pragma unroll
         for (int t = 0; t < NT; t++) mf_load<TYPE>(wrow[t] + (int64_t)sbc * BB, g, w[t]);
+        if constexpr (MA == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) av[i] = *(const uint4*)(xrow + sbc * 256 + 16 * i);
-        dy = *(const float4*)(xd + sbc * 16 + 4 * g);
+            for (int i = 0; i < 4; i++) av[i] = *(const uint4*)(xrow[0] + sbc * 256 + 16 * i);
+            dy = *(const float4*)(xd + (int64_t)sbc * mp + 16 * mt0 + 4 * g);
+        }
     };
     issue(wave, wc, avc, dyc);
     for (int sb = wave; sb < nsb; sb += KS) {
         // the next superblock's loads, when this wave has one (wave-uniform)
         const bool more = sb + KS < nsb;
         MfW<TYPE> wn[NT];
-        uint4 avn[4];
+        uint4 avn[MA == 1 ? 4 : 1];
         float4 dyn;
         if (more) issue(sb + KS, wn, avn, dyn);
-        // activation rows past m are zeroed by select (a load under a
-        // divergent branch would serialize the waits)
-        long a[8];
+        if constexpr (MA == 1) {
+            // activation rows past m are zeroed by select (a load under a
+            // divergent branch would serialize the waits)
+            long a[8];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            a[2 * i] = arow_ok ? (long)(((uint64_t)avc[i].y << 32) | avc[i].x) : 0l;
-            a[2 * i + 1] = arow_ok ? (long)(((uint64_t)avc[i].w << 32) | avc[i].z) : 0l;
+            for (int i = 0; i < 4; i++) {
+                a[2 * i] = arow_ok[0] ? (long)(((uint64_t)avc[i].y << 32) | avc[i].x) : 0l;
+                a[2 * i + 1] = arow_ok[0] ? (long)(((uint64_t)avc[i].w << 32) | avc[i].z) : 0l;
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++) mf_compute<TYPE>(wc[t], a, dyc, g, out[t][0]);
+        } else {
+            uint4 av[MA][4];
+            float4 dy[MA];
+#pragma unroll
+            for (int u = 0; u < MA; u++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) av[u][i] = *(const uint4*)(xrow[u] + sb * 256 + 16 * i);
+                dy[u] = *(const float4*)(xd + (int64_t)sb * mp + 16 * (mt0 + u) + 4 * g);
+            }
+#pragma unroll
+            for (int u = 0; u < MA; u++) {
+                if (16 * (mt0 + u) < m) {  // uniform: a tile wholly past m is skipped
+                    long a[8];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        a[2 * i] = arow_ok[u] ? (long)(((uint64_t)av[u][i].y << 32) | av[u][i].x) : 0l;
+                        a[2 * i + 1] = arow_ok[u] ? (long)(((uint64_t)av[u][i].w << 32) | av[u][i].z) : 0l;
+                    }
+#pragma unroll
+                    for (int t = 0; t < NT; t++) mf_compute<TYPE>(wc[t], a, dy[u], g, out[t][u]);
+                }
+            }
         }
-#pragma unroll
-        for (int t = 0; t < NT; t++) mf_compute<TYPE>(wc[t], a, dyc, g, out[t]);
         if (!more) break;
 #pragma unroll
         for (int t = 0; t < NT; t++) wc[t] = wn[t];
+        if constexpr (MA == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) avc[i] = avn[i];
-        dyc = dyn;
+            for (int i = 0; i < 4; i++) avc[i] = avn[i];
+            dyc = dyn;
+        }
     }
     if (KS > 1) {
         if (wave != 0) {
 #pragma unroll
-            for (int t = 0; t < NT; t++) part[wave - 1][t][lane] = make_float4(out[t][0], out[t][1], out[t][2], out[t][3]);
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int u = 0; u < MA; u++)
+                    part[wave - 1][t][u][lane] = make_float4(out[t][u][0], out[t][u][1], out[t][u][2], out[t][u][3]);
         }
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
         for (int w = 0; w < KS - 1; w++)
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const float4 p = part[w][t][lane];
-                out[t][0] += p.x;
-                out[t][1] += p.y;
-                out[t][2] += p.z;
-                out[t][3] += p.w;
-            }
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int u = 0; u < MA; u++) {
+                    const float4 p = part[w][t][u][lane];
+                    out[t][u][0] += p.x;
+                    out[t][u][1] += p.y;
+                    out[t][u][2] += p.z;
+                    out[t][u][3] += p.w;
+                }
     }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int nrow = blockIdx.x * 16 * NT + 16 * t + c16;
         if (nrow < n) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int mi = 4 * g + u;
-                if (mi < m) store_epi(&Y[(int64_t)mi * n + nrow], out[t][u], epi);
-            }
+            for (int u = 0; u < MA; u++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int mi = 16 * (mt0 + u) + 4 * g + v;
+                    if (mi < m) store_epi(&Y[(int64_t)mi * n + nrow], out[t][u][v], epi);
+                }
         }
     }
 }
@@ -576,20 +624,33 @@ size_t matvec_workspace_bytes(int type, int64_t k, int64_t m) {
     return split_q8k_bytes(k, m);
 }
 
-template <int TYPE>
+template <int TYPE, int MA>
 static hipError_t launch_mv_mfma(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xq,
                                  const float* xd, int epi, hipStream_t s) {
     // 8 waves split K; 2 row tiles per workgroup unless that leaves fewer
     // than ~256 workgroups
     constexpr int KS = 8;
-    if (n >= 2 * 16 * 256) {
-        hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 2>), dim3((unsigned)((n + 31) / 32)), dim3(64 * KS), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, epi);
+    const unsigned layers = (unsigned)((m + 16 * MA - 1) / (16 * MA));
+    const int mp = (int)((m + 15) & ~(int64_t)15);
+    if (MA == 1 && n * layers >= 2 * 16 * 256) {
+        hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 2, MA>), dim3((unsigned)((n + 31) / 32), layers), dim3(64 * KS), 0, s,
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
     } else {
-        hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 1>), dim3((unsigned)((n + 15) / 16)), dim3(64 * KS), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, epi);
+        hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 1, MA>), dim3((unsigned)((n + 15) / 16), layers), dim3(64 * KS), 0, s,
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
     }
     return hipGetLastError();
+}
+
+hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
+                     int epi, hipStream_t s) {
+    int8_t* xq;
+    float* xd;
+    split_q8k_ptrs(ws, k, m, &xq, &xd);
+    hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
+    if (e != hipSuccess) return e;
+    return type == T_Q4K ? launch_mv_mfma<T_Q4K, 4>(w, y, n, k, m, xq, xd, epi, s)
+                         : launch_mv_mfma<T_Q6K, 4>(w, y, n, k, m, xq, xd, epi, s);
 }
 
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
@@ -600,8 +661,8 @@ hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int6
         split_q8k_ptrs(ws, k, m, &xq, &xd);
         hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
         if (e != hipSuccess) return e;
-        return type == T_Q4K ? launch_mv_mfma<T_Q4K>(w, y, n, k, m, xq, xd, epi, s)
-                             : launch_mv_mfma<T_Q6K>(w, y, n, k, m, xq, xd, epi, s);
+        return type == T_Q4K ? launch_mv_mfma<T_Q4K, 1>(w, y, n, k, m, xq, xd, epi, s)
+                             : launch_mv_mfma<T_Q6K, 1>(w, y, n, k, m, xq, xd, epi, s);
     }
     switch (type) {
         case T_Q4K: return launch_type<T_Q4K>(w, x, y, (int)n, (int)k, (int)m, epi, s);

@@ -33,19 +33,18 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
     if (lane == 0) *(float*)b = d;
 }
 
-// Q8_K into the split layout read by the MFMA kernels: d [k/256][16] (m
-// padded to 16) and qs [m][k] with each 256-byte superblock permuted so
-// that element 32j + 8g + b (sub-block j, lane group g, byte b) sits at
-// 64g + 8j + b: an MFMA lane group's 8 bytes of every sub-block are then
-// one contiguous 64-byte run.  One block per wave; the values are those of
-// k_quantize_q8k.
+// Q8_K into the split layout read by the MFMA kernels: d [k/256][mp] (m
+// padded to mp = a multiple of 16) and qs [m][k] with each 256-byte
+// superblock permuted so that element 32j + 8g + b (sub-block j, lane group
+// g, byte b) sits at 64g + 8j + b: an MFMA lane group's 8 bytes of every
+// sub-block are then one contiguous 64-byte run.  One block per wave; the
+// values are those of k_quantize_q8k.
 __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restrict__ x, int8_t* __restrict__ qs,
-                                                            float* __restrict__ dt, int m, int k) {
+                                                            float* __restrict__ dt, int m, int k, int mp) {
     const int lane = threadIdx.x & 63;
     const int nsb = k >> 8;
-    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (blk >= (int64_t)m * nsb) return;
-    const int mi = (int)(blk / nsb), sb = (int)(blk - (int64_t)mi * nsb);
+    const int sb = blockIdx.y * 4 + (threadIdx.x >> 6), mi = blockIdx.x;
+    if (sb >= nsb) return;
     const float4 v = *(const float4*)(x + (int64_t)mi * k + sb * 256 + 4 * lane);
     float d;
     int bs;
@@ -53,12 +52,14 @@ __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restr
     // lane owns elements 4*lane..: sub-block lane/8, group (lane%8)/2, byte 4*(lane%2)
     const int off = 64 * ((lane & 7) >> 1) + 8 * (lane >> 3) + 4 * (lane & 1);
     *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + off) = q;
-    if (lane == 0) dt[sb * 16 + mi] = d;
+    if (lane == 0) dt[(int64_t)sb * mp + mi] = d;
 }
+
+static int64_t pad16(int64_t m) { return (m + 15) & ~(int64_t)15; }
 
 size_t split_q8k_bytes(int64_t k, int64_t m) {
     size_t qb = ((size_t)m * k + 255) & ~(size_t)255;
-    return qb + (size_t)(k / 256) * 16 * sizeof(float);
+    return qb + (size_t)(k / 256) * pad16(m) * sizeof(float);
 }
 
 void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d) {
@@ -68,9 +69,9 @@ void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d) {
 }
 
 hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s) {
-    const int64_t nb = m * (k / 256);
-    hipLaunchKernelGGL(k_quantize_split_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, qs, d, (int)m,
-                       (int)k);
+    const int64_t nsb = k / 256;
+    hipLaunchKernelGGL(k_quantize_split_q8k, dim3((unsigned)m, (unsigned)((nsb + 3) / 4)), dim3(256), 0, s, x, qs, d,
+                       (int)m, (int)k, (int)pad16(m));
     return hipGetLastError();
 }
 
