@@ -303,6 +303,18 @@ def run_details(L, cu, np, torch, dev, args):
                              "unique_expert_bytes": int(byts), "GB/s": round(byts / t / 1e9, 1),
                              "hbm_frac": round(byts / t / 1e9 / 8000.0, 4),
                              "note": "gate+up+down, 3 routed calls on the same graph replay; the 307 MB of touched experts exceed the 256 MB MALL"}
+
+    # the same layer with gate and up as one SwiGLU launch (silu(g) * u
+    # stored once) and the down projection over it
+    def moe_glu():
+        gate.indexed_moe_forward_glu_into(up, x, ids_t, yg)
+        down.indexed_moe_forward_into(yg, ids_t, yd)
+
+    t = time_graph([moe_glu], 5, 1)
+    byts_glu = byts - T * topk * ff * 4  # one [T, topk, ff] store fewer
+    out["c5_moe_glu_layer"] = {"us": round(t * 1e6, 2), "GB/s": round(byts_glu / t / 1e9, 1),
+                               "hbm_frac": round(byts_glu / t / 1e9 / 8000.0, 4),
+                               "note": "silu(gate) * up in one routed launch, then down: 2 routed calls"}
     return out
 
 

@@ -253,6 +253,17 @@ class QTensor:
                                              topk, _ptr(y), 1 if strict else 0, _stream(x)))
         return y
 
+    def indexed_moe_forward_glu_into(self, up, x, ids, y):
+        """indexed_moe_forward_glu_as into a preallocated contiguous f32 y
+        [batch, topk, n]; non-strict and allocation-free (graph-capturable)."""
+        n_experts, n, k = self.shape
+        batch, in_dim1, _ = x.shape
+        topk = ids.shape[1]
+        check(lib().lloom_hip_moe_matmul_glu(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage),
+                                             _ptr(up.storage), n_experts, n, k, _ptr(x), batch, in_dim1, _ptr(ids),
+                                             topk, _ptr(y), 0, _stream(x)))
+        return y
+
     # QTensor::embedding (mod.rs:1101-1137)
     def embedding(self, ids, strict=True, f16=False):
         """Rows ids of a [rows, hidden] weight, dequantized: out shape
