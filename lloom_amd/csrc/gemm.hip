@@ -422,6 +422,7 @@ struct XCfg {
     static constexpr int DMA_AFTER_RAW = A_PER_WAVE + 1;
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(BM <= 256 && S_PER_WAVE >= 1, "row DMA shares");
+    static_assert(A_PER_WAVE % 4 == 0, "activation DMA spread over the four slices of a step");
 };
 
 // Row r of a [rows][64 halves] tile: 8 pieces of 16 bytes, piece p at
@@ -666,12 +667,6 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
         for (int c = 0; c < 4; c++) {
             const int s = 4 * sb + c;
             const uint8_t* A = smem + (s % C::A_STAGES) * C::A_BYTES;
-            // 1. queue: the next superblock's operands (first step), A(s + 2)
-            //    into the stage step s - 1 used, raw(s + 3) into step s - 1's slot
-            if (c == 0) issue_sb(min(sb + 1, nsb - 1));
-            issue_a(min(s + 2, nsteps - 1), s + 2);
-            issue_raw(min(s + 3, nsteps - 1), s + 3);
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int a = 0; a < MT; a++)
                 abuf[0][a] = *(const v8h*)(A + x_pos(wm * (32 * MT) + a * 32 + c32, x_piece(0, h)));
@@ -690,6 +685,20 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
                     read_raw(s + 1, rawn);
                     if (c == 3) read_hdr(sb + 1, hn);
                 }
+                // 1. queue, spread over the slices (a burst of DMA issues
+                //    stalls the wave): the next superblock's operands (first
+                //    step), A(s + 2) into the stage step s - 1 used, raw(s + 3)
+                //    into step s - 1's slot, in that order
+                if (kk == 0 && c == 0) issue_sb(min(sb + 1, nsb - 1));
+                {
+                    uint8_t* Ad = smem + ((s + 2) % C::A_STAGES) * C::A_BYTES;
+                    const uint8_t* ab = (const uint8_t*)x16 + (uint32_t)min(s + 2, nsteps - 1) * (C::BK * 2);
+                    constexpr int PER = C::A_PER_WAVE / 4;
+#pragma unroll
+                    for (int i = kk * PER; i < (kk + 1) * PER; i++)
+                        dma16(ab + aoff[i], lds_addr(Ad + 1024 * (wave * C::A_PER_WAVE + i)));
+                }
+                if (kk == 3) issue_raw(min(s + 3, nsteps - 1), s + 3);
                 // the reads above stay ahead of this slice's MFMAs (the
                 // scheduler would otherwise sink them to their use)
                 __builtin_amdgcn_sched_barrier(0);
@@ -720,6 +729,12 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
                     }
 #pragma unroll
                 for (int b = 0; b < C::NT; b++) bcur[b] = bnext[b];
+                // one MFMA, then three VALU (the next slice's unpack), in turn
+#pragma unroll
+                for (int i = 0; i < MT * C::NT; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
