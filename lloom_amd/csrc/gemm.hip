@@ -399,30 +399,43 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// Tile geometry, MT = 32 x 32 tiles per wave along M (2 or 4): a
-// workgroup covers 64 MT rows x 128 columns.
-template <int MT>
+// Tile geometry: MT = 32 x 32 tiles per wave along M (2 or 4), WNW waves
+// along N (2: 2 x 2 waves, a 64 MT x 128 block; 4: 1 x 4 waves, a 32 MT x 256
+// block).  A wave always owns 32 MT rows x 64 columns.  The 1 x 4 layout
+// moves 2/3 of the 2 x 2 layout's bytes per MFMA (the fp16 activation tile
+// is half as tall for the same work) and unpacks every weight column once
+// instead of in two waves.
+template <int MT, int WNW, int WV = 4>
 struct XCfg {
-    static constexpr int BM = 64 * MT, BN = 128, BK = 64;
-    static constexpr int WAVES = 4, THREADS = 64 * WAVES, NT = 2;
+    static constexpr int WAVES = WV, WMW = WAVES / WNW;
+    static constexpr int BM = 32 * MT * WMW, BN = 64 * WNW, BK = 64;
+    static constexpr int THREADS = 64 * WAVES, NT = 2;
     static constexpr int A_STAGES = 3, R_SLOTS = 4;
     static constexpr int A_BYTES = BM * BK * 2;  // 1 KB DMA chunks
-    static constexpr int R_BYTES = BN * 32;      // the step's qs bytes of 128 rows
+    static constexpr int R_BYTES = BN * 32;      // the step's qs bytes of BN rows
     static constexpr int A_PER_WAVE = A_BYTES / 1024 / WAVES;
+    // weight DMA: 1 KB chunks of 32 columns (the step's bytes, or a
+    // superblock's headers), R_PER_WAVE chunks per wave
+    static constexpr int R_PER_WAVE = BN / 32 / WAVES;
     // per superblock: min operands [BM][32 B], dy [BM] f32 (256 B per
-    // wave), weight headers [BN][16 B] (1 KB per wave: lanes 32..63 reload
+    // wave), weight headers [BN][16 B] (1 KB per chunk: lanes 32..63 reload
     // lanes 0..31's columns into a copy nobody reads, so every wave issues
     // the same loads)
-    static constexpr int S_PER_WAVE = BM * 32 / 1024 / WAVES;
-    static constexpr int SB_AMIN = 0, SB_DY = BM * 32, SB_HDR = SB_DY + 256 * WAVES;
-    static constexpr int SB_BYTES = SB_HDR + 1024 * WAVES;
+    // (with more waves than min-operand chunks, the extra waves' loads go
+    // to a trash chunk, so every wave issues the same number of loads)
+    static constexpr int S_CHUNKS = BM * 32 / 1024;
+    static constexpr int S_PER_WAVE = S_CHUNKS >= WAVES ? S_CHUNKS / WAVES : 1;
+    static constexpr int SB_AMIN = 0, SB_DY = (S_CHUNKS + 1) * 1024, SB_HDR = SB_DY + 256 * WAVES;
+    static constexpr int SB_BYTES = SB_HDR + 1024 * WAVES * R_PER_WAVE;
     static constexpr int R_OFF = A_STAGES * A_BYTES, SB_OFF = R_OFF + R_SLOTS * R_BYTES;
     static constexpr int LDS = SB_OFF + 2 * SB_BYTES;
     // loads per wave and step: SB (first step of a superblock), A(s + 2), raw(s + 3)
-    static constexpr int DMA_AFTER_RAW = A_PER_WAVE + 1;
+    static constexpr int DMA_AFTER_RAW = A_PER_WAVE + R_PER_WAVE;
+    static_assert(R_PER_WAVE >= 1 && BN % (32 * WAVES) == 0, "weight DMA shares");
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    static_assert(BM <= 256 && S_PER_WAVE >= 1, "row DMA shares");
-    static_assert(A_PER_WAVE % 4 == 0, "activation DMA spread over the four slices of a step");
+    static_assert(BM <= 256 && (S_CHUNKS % WAVES == 0 || S_CHUNKS < WAVES), "row DMA shares");
+    static_assert(64 * WAVES >= BM, "dy DMA covers the tile's rows");
+    static_assert(A_PER_WAVE == 2 || A_PER_WAVE % 4 == 0, "activation DMA spread over the four slices of a step");
 };
 
 // Row r of a [rows][64 halves] tile: 8 pieces of 16 bytes, piece p at
@@ -545,16 +558,16 @@ __device__ __forceinline__ v8h build_kk(const uint4& raw, const BScale& bs, int 
     return __builtin_bit_cast(v8h, make_uint4(p0.x, p0.y, p1.x, p1.y));
 }
 
-template <int MT>
-__global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict__ W,
+template <int MT, int WNW, int WV>
+__global__ __launch_bounds__(64 * WV) void k_gemm_q4k_x16(const uint8_t* __restrict__ W,
                                                             const _Float16* __restrict__ x16,
                                                             const _Float16* __restrict__ amin,
                                                             const float* __restrict__ dyt, float* __restrict__ Y,
                                                             int m, int n, int k, int epi) {
-    using C = XCfg<MT>;
+    using C = XCfg<MT, WNW, WV>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, 32 MT x 64 each
+    const int wm = wave / WNW, wn = wave % WNW;  // WMW x WNW waves, 32 MT x 64 each
     const int h = lane >> 5, c32 = lane & 31;
     int bm, bn;
     tile_of((m + C::BM - 1) / C::BM, (n + C::BN - 1) / C::BN, bm, bn);
@@ -575,13 +588,16 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
     // weight-byte DMA: wave w moves columns 32w .. 32w+31; slot (16 B) l
     // holds half l >> 5 of column 32w + (l & 31), so the 32 lanes reading one
     // half read 32 consecutive slots
-    const uint32_t colw = (uint32_t)min(n0 + 32 * wave + c32, n - 1) * rowbytes;
-    const uint32_t roff = colw + 16u + 16u * (uint32_t)h;
+    uint32_t colw[C::R_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < C::R_PER_WAVE; i++)
+        colw[i] = (uint32_t)min(n0 + 32 * (C::R_PER_WAVE * wave + i) + c32, n - 1) * rowbytes;
     // min operands: wave w moves rows 32 (C::S_PER_WAVE w + i) + lane / 2, halves lane & 1
     uint32_t soff[C::S_PER_WAVE];
 #pragma unroll
     for (int i = 0; i < C::S_PER_WAVE; i++)
-        soff[i] = (uint32_t)min(m0 + 32 * (C::S_PER_WAVE * wave + i) + (lane >> 1), m - 1) * (uint32_t)nsb * 32u +
+        soff[i] = (uint32_t)min(m0 + 32 * min(C::S_PER_WAVE * wave + i, C::S_CHUNKS - 1) + (lane >> 1), m - 1) *
+                      (uint32_t)nsb * 32u +
                   16u * (lane & 1);
     const int dyrow = min(m0 + 64 * wave + lane, m - 1);
 
@@ -593,27 +609,30 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
     };
     auto issue_raw = [&](int src, int dst) {
         uint8_t* R = smem + C::R_OFF + (dst % C::R_SLOTS) * C::R_BYTES;
-        const uint8_t* rb = W + (uint32_t)(src >> 2) * Q4K_BYTES + 32u * (src & 3);
-        dma16(rb + roff, lds_addr(R + 1024 * wave));
+        const uint8_t* rb = W + (uint32_t)(src >> 2) * Q4K_BYTES + 32u * (src & 3) + 16u + 16u * (uint32_t)h;
+#pragma unroll
+        for (int i = 0; i < C::R_PER_WAVE; i++) dma16(rb + colw[i], lds_addr(R + 1024 * (C::R_PER_WAVE * wave + i)));
     };
     auto issue_sb = [&](int sb) {
         uint8_t* SB = smem + C::SB_OFF + (sb & 1) * C::SB_BYTES;
 #pragma unroll
         for (int i = 0; i < C::S_PER_WAVE; i++)
             dma16((const uint8_t*)amin + (uint32_t)sb * 32u + soff[i],
-                  lds_addr(SB + C::SB_AMIN + 1024 * (C::S_PER_WAVE * wave + i)));
+                  lds_addr(SB + C::SB_AMIN + 1024 * min(C::S_PER_WAVE * wave + i, C::S_CHUNKS)));
         dma4(dyt + (int64_t)sb * m + dyrow, lds_addr(SB + C::SB_DY + 256 * wave));
-        dma16(W + (uint32_t)sb * Q4K_BYTES + colw, lds_addr(SB + C::SB_HDR + 1024 * wave));
+#pragma unroll
+        for (int i = 0; i < C::R_PER_WAVE; i++)
+            dma16(W + (uint32_t)sb * Q4K_BYTES + colw[i], lds_addr(SB + C::SB_HDR + 1024 * (C::R_PER_WAVE * wave + i)));
     };
     auto read_raw = [&](int step, uint4 (&r)[C::NT]) {
         const uint8_t* R = smem + C::R_OFF + (step % C::R_SLOTS) * C::R_BYTES;
 #pragma unroll
-        for (int b = 0; b < C::NT; b++) r[b] = *(const uint4*)(R + 1024 * (2 * wn + b) + 16 * (32 * h + c32));
+        for (int b = 0; b < C::NT; b++) r[b] = *(const uint4*)(R + 1024 * (C::NT * wn + b) + 16 * (32 * h + c32));
     };
     auto read_hdr = [&](int sb, uint4 (&hd)[C::NT]) {
         const uint8_t* SB = smem + C::SB_OFF + (sb & 1) * C::SB_BYTES + C::SB_HDR;
 #pragma unroll
-        for (int b = 0; b < C::NT; b++) hd[b] = *(const uint4*)(SB + 1024 * (2 * wn + b) + 16 * c32);
+        for (int b = 0; b < C::NT; b++) hd[b] = *(const uint4*)(SB + 1024 * (C::NT * wn + b) + 16 * c32);
     };
 
     v16f acc[MT][C::NT], out[MT][C::NT];
@@ -693,10 +712,10 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_x16(const uint8_t* __restrict_
                 {
                     uint8_t* Ad = smem + ((s + 2) % C::A_STAGES) * C::A_BYTES;
                     const uint8_t* ab = (const uint8_t*)x16 + (uint32_t)min(s + 2, nsteps - 1) * (C::BK * 2);
-                    constexpr int PER = C::A_PER_WAVE / 4;
 #pragma unroll
-                    for (int i = kk * PER; i < (kk + 1) * PER; i++)
-                        dma16(ab + aoff[i], lds_addr(Ad + 1024 * (wave * C::A_PER_WAVE + i)));
+                    for (int i = 0; i < C::A_PER_WAVE; i++)
+                        if (i * 4 / C::A_PER_WAVE == kk)  // compile-time
+                            dma16(ab + aoff[i], lds_addr(Ad + 1024 * (wave * C::A_PER_WAVE + i)));
                 }
                 if (kk == 3) issue_raw(min(s + 3, nsteps - 1), s + 3);
                 // the reads above stay ahead of this slice's MFMAs (the
@@ -838,21 +857,33 @@ size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
     return matvec_workspace_bytes(type == T_Q4K ? T_Q6K : type, k, 16);
 }
 
-template <int MT>
+template <int MT, int WNW, int WV>
 static hipError_t launch_x16(const void* w, const X16Ptrs& p, float* y, int64_t n, int64_t k, int64_t m,
                              int epi, hipStream_t s) {
-    using C = XCfg<MT>;
+    using C = XCfg<MT, WNW, WV>;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e =
-            hipFuncSetAttribute((const void*)k_gemm_q4k_x16<MT>, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k_x16<MT, WNW, WV>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const unsigned grid = (unsigned)(((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN));
-    hipLaunchKernelGGL((k_gemm_q4k_x16<MT>), dim3(grid), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.x16,
-                       p.amin, p.dyt, y, (int)m, (int)n, (int)k, epi);
+    hipLaunchKernelGGL((k_gemm_q4k_x16<MT, WNW, WV>), dim3(grid), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w,
+                       p.x16, p.amin, p.dyt, y, (int)m, (int)n, (int)k, epi);
     return hipGetLastError();
+}
+
+// LLOOM_HIP_X16_TILE (read once) picks the tile for tuning: 0 = 256 x 128,
+// 1 = 128 x 256, 2 = 128 x 128 (4 waves, 128 x 64 or 64 x 64 each), 3 =
+// 128 x 256 with 8 waves of 64 x 64 (two per SIMD); -1 (default) chooses
+// by m.
+static int x16_tile_env() {
+    static const int v = [] {
+        const char* e = getenv("LLOOM_HIP_X16_TILE");
+        return e ? atoi(e) : -1;
+    }();
+    return v;
 }
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
@@ -866,7 +897,14 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         // 256-row tiles once there are enough of them to fill the chip
-        return m >= 1024 ? launch_x16<4>(w, p, y, n, k, m, epi, s) : launch_x16<2>(w, p, y, n, k, m, epi, s);
+        int tile = x16_tile_env();
+        if (tile < 0) tile = m >= 1024 ? 3 : 2;
+        switch (tile) {
+            case 0: return launch_x16<4, 2, 4>(w, p, y, n, k, m, epi, s);
+            case 1: return launch_x16<4, 4, 4>(w, p, y, n, k, m, epi, s);
+            case 3: return launch_x16<2, 4, 8>(w, p, y, n, k, m, epi, s);
+            default: return launch_x16<2, 2, 4>(w, p, y, n, k, m, epi, s);
+        }
     }
     if (type == T_Q4K && fits_32bit(n, k, m)) {
         static bool attr_set = false;
