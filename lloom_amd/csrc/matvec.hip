@@ -358,6 +358,92 @@ __device__ __forceinline__ void mf_load(const uint8_t* __restrict__ b, int g, Mf
     }
 }
 
+// Load format of a superblock.  Q4_K: each lane reads 32 contiguous qs bytes
+// of its row (chunk g: bytes 32g .. 32g+31) and the header, so the wave's
+// loads cover each row's 128 qs bytes contiguously; mf_unpack then hands
+// lane (g, row) the 8-byte piece g of every chunk c through a wave-private
+// LDS tile (a 4 x 4 transpose among the four lanes of a row).  Loading the
+// operand layout directly (four 8-byte pieces 32 bytes apart per lane)
+// made each load instruction touch 16 rows x 32 bytes and cost ~1.5 us of
+// a 6 us call.  Q6_K the same way: 32 contiguous ql bytes and 16 qh bytes a
+// lane (2-byte-aligned blocks: dword loads and a byte realignment).
+template <int TYPE>
+struct MfL;
+template <>
+struct MfL<T_Q4K> {
+    uint4 hdr, a, b;
+};
+template <>
+struct MfL<T_Q6K> {
+    uint4 a, b, h, sc;
+    uint32_t d;
+};
+// LDS bytes per row of the transpose tile: the qs (Q4_K 128, Q6_K 128 ql +
+// 64 qh) plus a 16-byte pad
+template <int TYPE>
+struct MfRs {
+    static constexpr int V = TYPE == T_Q4K ? 144 : 208;
+};
+
+// 32 bytes at a 2-byte-aligned address: nine dword loads from the 4-byte
+// floor and a byte realignment.
+__device__ __forceinline__ void load32_a2(const uint8_t* p, uint4& r0, uint4& r1) {
+    uintptr_t a = (uintptr_t)p;
+    const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const uint4 v0 = *(const uint4*)q, v1 = *(const uint4*)(q + 4);
+    const uint32_t v8 = q[8];
+    r0.x = __builtin_amdgcn_alignbyte(v0.y, v0.x, sh);
+    r0.y = __builtin_amdgcn_alignbyte(v0.z, v0.y, sh);
+    r0.z = __builtin_amdgcn_alignbyte(v0.w, v0.z, sh);
+    r0.w = __builtin_amdgcn_alignbyte(v1.x, v0.w, sh);
+    r1.x = __builtin_amdgcn_alignbyte(v1.y, v1.x, sh);
+    r1.y = __builtin_amdgcn_alignbyte(v1.z, v1.y, sh);
+    r1.z = __builtin_amdgcn_alignbyte(v1.w, v1.z, sh);
+    r1.w = __builtin_amdgcn_alignbyte(v8, v1.w, sh);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void mf_load_l(const uint8_t* __restrict__ b, int g, MfL<TYPE>& l) {
+    if constexpr (TYPE == T_Q4K) {
+        l.hdr = *(const uint4*)b;
+        l.a = *(const uint4*)(b + 16 + 32 * g);
+        l.b = *(const uint4*)(b + 32 + 32 * g);
+    } else {
+        load32_a2(b + 32 * g, l.a, l.b);
+        l.h = load16_a2(b + Q6K_QH + 16 * g);
+        l.sc = load16_a2(b + Q6K_SC);
+        l.d = *(const uint16_t*)(b + Q6K_D);
+    }
+}
+
+// tile: this wave's [16][MfRs] bytes of LDS for this row tile.
+template <int TYPE>
+__device__ __forceinline__ void mf_unpack(const MfL<TYPE>& l, uint8_t* tile, int g, int c16, MfW<TYPE>& w) {
+    uint8_t* row = tile + c16 * MfRs<TYPE>::V;
+    if constexpr (TYPE == T_Q4K) {
+        *(uint4*)(row + 32 * g) = l.a;
+        *(uint4*)(row + 32 * g + 16) = l.b;
+        // the wave's LDS operations complete in order; this also keeps the
+        // compiler from moving the reads above the writes
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int c = 0; c < 4; c++) w.q[c] = *(const uint2*)(row + 32 * c + 8 * g);
+        w.hdr = l.hdr;
+    } else {
+        *(uint4*)(row + 32 * g) = l.a;
+        *(uint4*)(row + 32 * g + 16) = l.b;
+        *(uint4*)(row + 128 + 16 * g) = l.h;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int c = 0; c < 4; c++) w.ql[c] = *(const uint2*)(row + 32 * c + 8 * g);
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) w.qh[hh] = *(const uint2*)(row + 128 + 32 * hh + 8 * g);
+        w.sc = l.sc;
+        w.d = l.d;
+    }
+}
+
 // q6 (0..63) per byte -> q6 - 32 as int8: t = q6 ^ 32 is q6 - 32 in 6-bit
 // two's complement; copying bit 5 into bits 6 and 7 (0x20 * 6 = 0xC0, no
 // carry between bytes) sign-extends it to 8 bits.
@@ -436,6 +522,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
                                                      int K, int m, int mp, int epi) {
     constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float4 part[KS > 1 ? KS - 1 : 1][NT][MA][64];
+    __shared__ __align__(16) uint8_t mft[KS][NT][16 * MfRs<TYPE>::V];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int nsb = K >> 8;
@@ -460,13 +547,13 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
 
     // registers of the superblock in flight (the row and superblock
     // indices are clamped, so no load sits under a divergent branch)
-    MfW<TYPE> wc[NT];
+    MfL<TYPE> wc[NT];
     uint4 avc[MA == 1 ? 4 : 1];
     float4 dyc;
-    auto issue = [&](int sb, MfW<TYPE>(&w)[NT], uint4(&av)[MA == 1 ? 4 : 1], float4& dy) {
+    auto issue = [&](int sb, MfL<TYPE>(&w)[NT], uint4(&av)[MA == 1 ? 4 : 1], float4& dy) {
         const int sbc = min(sb, nsb - 1);
 #pragma unroll
-        for (int t = 0; t < NT; t++) mf_load<TYPE>(wrow[t] + (int64_t)sbc * BB, g, w[t]);
+        for (int t = 0; t < NT; t++) mf_load_l<TYPE>(wrow[t] + (int64_t)sbc * BB, g, w[t]);
         if constexpr (MA == 1) {
 #pragma unroll
             for (int i = 0; i < 4; i++) av[i] = *(const uint4*)(xrow[0] + sbc * 256 + 16 * i);
@@ -477,10 +564,13 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
     for (int sb = wave; sb < nsb; sb += KS) {
         // the next superblock's loads, when this wave has one (wave-uniform)
         const bool more = sb + KS < nsb;
-        MfW<TYPE> wn[NT];
+        MfL<TYPE> wn[NT];
         uint4 avn[MA == 1 ? 4 : 1];
         float4 dyn;
         if (more) issue(sb + KS, wn, avn, dyn);
+        MfW<TYPE> wu[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) mf_unpack<TYPE>(wc[t], &mft[wave][t][0], g, c16, wu[t]);
         if constexpr (MA == 1) {
             // activation rows past m are zeroed by select (a load under a
             // divergent branch would serialize the waits)
@@ -491,7 +581,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
                 a[2 * i + 1] = arow_ok[0] ? (long)(((uint64_t)avc[i].w << 32) | avc[i].z) : 0l;
             }
 #pragma unroll
-            for (int t = 0; t < NT; t++) mf_compute<TYPE>(wc[t], a, dyc, g, out[t][0]);
+            for (int t = 0; t < NT; t++) mf_compute<TYPE>(wu[t], a, dyc, g, out[t][0]);
         } else {
             uint4 av[MA][4];
             float4 dy[MA];
@@ -511,7 +601,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
                         a[2 * i + 1] = arow_ok[u] ? (long)(((uint64_t)av[u][i].w << 32) | av[u][i].z) : 0l;
                     }
 #pragma unroll
-                    for (int t = 0; t < NT; t++) mf_compute<TYPE>(wc[t], a, dy[u], g, out[t][u]);
+                    for (int t = 0; t < NT; t++) mf_compute<TYPE>(wu[t], a, dy[u], g, out[t][u]);
                 }
             }
         }
@@ -632,10 +722,20 @@ static hipError_t launch_mv_mfma(const void* w, float* y, int64_t n, int64_t k, 
     constexpr int KS = 8;
     const unsigned layers = (unsigned)((m + 16 * MA - 1) / (16 * MA));
     const int mp = (int)((m + 15) & ~(int64_t)15);
-    if (MA == 1 && n * layers >= 2 * 16 * 256) {
-        hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 2, MA>), dim3((unsigned)((n + 31) / 32), layers), dim3(64 * KS), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
-    } else {
+    if constexpr (MA == 1) {
+        if (n >= 2 * 16 * 256) {
+            hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 2, MA>), dim3((unsigned)((n + 31) / 32), layers), dim3(64 * KS), 0,
+                               s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
+            return hipGetLastError();
+        }
+        if (n < 16 * 256 && k >= 16 * 256) {
+            // fewer row tiles than CUs and a long K: 16 waves split K
+            hipLaunchKernelGGL((k_mv_mfma<TYPE, 16, 1, MA>), dim3((unsigned)((n + 15) / 16), layers), dim3(64 * 16),
+                               0, s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
+            return hipGetLastError();
+        }
+    }
+    {
         hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 1, MA>), dim3((unsigned)((n + 15) / 16), layers), dim3(64 * KS), 0, s,
                            (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
     }
