@@ -652,6 +652,105 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
     }
 }
 
+// ----------------------------- 3..4 rows in one launch (short K) --
+// The MFMA decode with the activation quantization inside: a workgroup of
+// 16 waves owns 32 weight rows (two 16-row tiles) and K of KS = k / 256
+// superblocks (4 or 8); wave (tile, sb) first issues its superblock's weight
+// loads, then the workgroup quantizes all m x KS blocks of x into LDS in the
+// MFMA operand layout (Q8_K, bit-exact, at most two blocks per wave), and
+// after one barrier each wave runs its superblock's MFMAs; the KS partials
+// of a row meet in LDS.  For m <= 4 this saves the quantizer's launch; with
+// more rows every workgroup re-reading B x k f32 of x costs more than that
+// launch (measured: 6.2 us against 7.3 us at m = 3, 10.3 against 8.4 at
+// m = 16, n = 6144, k = 2048).  Per output the arithmetic is k_mv_mfma's,
+// so the results are bit-identical to it.
+constexpr int FUSED_MAX_ROWS = 4;
+
+template <int TYPE, int KS>
+__global__ __launch_bounds__(128 * KS) void k_mv_fused(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                       float* __restrict__ Y, int n, int m, int epi) {
+    constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int WV = 2 * KS, K = 256 * KS;
+    constexpr int XN = (FUSED_MAX_ROWS * KS + WV - 1) / WV;  // blocks quantized per wave
+    __shared__ __align__(16) int8_t xs[KS][16][256];
+    __shared__ __align__(16) float dl[KS][16];
+    __shared__ __align__(16) uint8_t mft[WV][16 * MfRs<TYPE>::V];
+    __shared__ float4 red[KS - 1][2][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int kw = wave % KS, rt = wave / KS;
+    const int row = (blockIdx.x * 2 + rt) * 16 + c16;
+    const uint8_t* wrow = W + (int64_t)min(row, n - 1) * ((int64_t)KS * BB);
+    MfL<TYPE> wl;
+    mf_load_l<TYPE>(wrow + (int64_t)kw * BB, g, wl);
+    // x blocks q = mi * KS + sb, q = wave + WV * t (a block past the end
+    // reloads block 0 and is not stored)
+    const int nblk = m * KS;
+    float4 xv[XN];
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int q = wave + WV * t;
+        const int qq = q < nblk ? q : 0;
+        xv[t] = *(const float4*)(X + (int64_t)(qq / KS) * K + (qq % KS) * 256 + 4 * lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // element 4*lane.. of a block: sub-block lane / 8, lane group (lane % 8) / 2,
+    // byte 4 * (lane % 2) of the group's 8 (k_quantize_split_q8k's layout)
+    const int off = 64 * ((lane & 7) >> 1) + 8 * (lane >> 3) + 4 * (lane & 1);
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int q = wave + WV * t;
+        float d;
+        int bs;
+        const uint32_t qv = q8k_block_wave(xv[t], &d, &bs);
+        if (q < nblk) {  // wave-uniform
+            *(uint32_t*)(&xs[q % KS][q / KS][off]) = qv;
+            if (lane == 0) dl[q % KS][q / KS] = d;
+        }
+    }
+    MfW<TYPE> wu;
+    mf_unpack<TYPE>(wl, &mft[wave][0], g, c16, wu);
+    __syncthreads();
+    const bool arow_ok = c16 < m;
+    long a[8];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint4 v = *(const uint4*)(&xs[kw][c16][64 * g + 16 * c]);
+        a[2 * c] = arow_ok ? (long)(((uint64_t)v.y << 32) | v.x) : 0l;
+        a[2 * c + 1] = arow_ok ? (long)(((uint64_t)v.w << 32) | v.z) : 0l;
+    }
+    const float4 dy = *(const float4*)(&dl[kw][4 * g]);
+    float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    mf_compute<TYPE>(wu, a, dy, g, out);
+    if (kw) red[kw - 1][rt][lane] = make_float4(out[0], out[1], out[2], out[3]);
+    __syncthreads();
+    if (kw) return;
+#pragma unroll
+    for (int w = 0; w < KS - 1; w++) {
+        const float4 p = red[w][rt][lane];
+        out[0] += p.x;
+        out[1] += p.y;
+        out[2] += p.z;
+        out[3] += p.w;
+    }
+    if (row < n) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (4 * g + u < m) store_epi(&Y[(int64_t)(4 * g + u) * n + row], out[u], epi);
+    }
+}
+
+template <int TYPE>
+static hipError_t launch_fused(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, int epi,
+                               hipStream_t s) {
+    const dim3 grid((unsigned)((n + 31) / 32));
+    if (k == 2048)
+        hipLaunchKernelGGL((k_mv_fused<TYPE, 8>), grid, dim3(1024), 0, s, (const uint8_t*)w, x, y, (int)n, (int)m, epi);
+    else
+        hipLaunchKernelGGL((k_mv_fused<TYPE, 4>), grid, dim3(512), 0, s, (const uint8_t*)w, x, y, (int)n, (int)m, epi);
+    return hipGetLastError();
+}
+
 // Chunk of K staged in LDS at a time: the prologue quantizes at most
 // XQ blocks per wave, m * KC <= XQ * WV * 256 elements.
 static int pick_kc(int type, int64_t K, int m, int wv) {
@@ -755,6 +854,9 @@ hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t 
 
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, int epi, hipStream_t s) {
+    if (type != T_Q8_0 && m > MV_DOT_MAX_ROWS && m <= FUSED_MAX_ROWS && (k == 2048 || k == 1024))
+        return type == T_Q4K ? launch_fused<T_Q4K>(w, x, y, n, k, m, epi, s)
+                             : launch_fused<T_Q6K>(w, x, y, n, k, m, epi, s);
     if (type != T_Q8_0 && m > MV_DOT_MAX_ROWS) {
         int8_t* xq;
         float* xd;

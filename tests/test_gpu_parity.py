@@ -177,7 +177,9 @@ def test_decode_rows_batch_invariant(L, dt):
     """Within one decode kernel every activation row is computed alone, so a
     row's output does not depend on its batch (qmm_batch,
     quantized_tests.rs:239-275, exact on the CPU arm).  Q4_K and Q6_K with
-    3..16 rows run the MFMA kernel, 1..2 the dot4 kernel: each group is
+    3..16 rows run the MFMA kernels (3..4 rows at this k the single-launch
+    variant, whose per-output arithmetic and partial-sum order are the
+    two-launch kernel's), 1..2 the dot4 kernel: each group is
     checked against its own full batch (across the two kernels only the
     tolerance holds, as on the reference's CUDA and Metal arms).  Q8_0 runs
     the 8-wave dot4 kernel for 1..2 rows and the 4-wave one above that (their
