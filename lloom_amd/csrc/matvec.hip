@@ -241,12 +241,14 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         // issue the last weight loads only after x has arrived
         __builtin_amdgcn_sched_barrier(0);
         quantize_lds<Tr::VT, WV, XN>(xv, KC, m, mg, lqs, ld, lbs);
-        // unpack the first round of weights while the other waves finish
-        // their share of the quantization
+        // The quantized x is in LDS once every wave's LDS writes are done:
+        // a bare s_barrier after lgkmcnt(0).  __syncthreads() would also
+        // wait for this wave's weight loads (vmcnt(0)), so every wave would
+        // start its dots only when the slowest wave's weights had landed.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         WPrep<TYPE> wp[R];
 #pragma unroll
         for (int r = 0; r < R; r++) prep_task<TYPE>(td[r], ti % Tr::P, wp[r]);
-        __syncthreads();
         for (; ti < T; ti += 64) {
             const int p = ti % Tr::P, bl = ti / Tr::P;
             if (ti != lane) {
