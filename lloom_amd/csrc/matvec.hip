@@ -228,14 +228,22 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         if (kc0) __syncthreads();  // the previous chunk's readers are done with LDS
         float4 xv[XN];
         prefetch_x<Tr::VT, WV, XN>(X, K, kc0, KC, m, mg, xv);
-        // first round of weight loads (tasks past T load task 0, unused)
-        TaskData td[R];
-        int ti = lane;
-        {
-            const int t0 = ti < T ? ti : 0;
+        // weight loads of the first PF rounds of 64 tasks (tasks past T
+        // load task 0, unused): with one or two rows a wave, rows of several
+        // rounds (long K) keep PF rounds of loads in flight instead of one
+        // (Q6_K's four-group tasks hold too many registers for more than one)
+        constexpr int PF = TYPE == T_Q6K ? 1 : R == 1 ? 4 : R == 2 ? 2 : 1;
+        TaskData td[PF][R];
+        auto issue = [&](int base) {
 #pragma unroll
-            for (int r = 0; r < R; r++) load_task<TYPE>(wrow[r], blk0 + t0 / Tr::P, t0 % Tr::P, td[r]);
-        }
+            for (int j = 0; j < PF; j++) {
+                const int t = base + lane + 64 * j;
+                const int tc = t < T ? t : 0;
+#pragma unroll
+                for (int r = 0; r < R; r++) load_task<TYPE>(wrow[r], blk0 + tc / Tr::P, tc % Tr::P, td[j][r]);
+            }
+        };
+        issue(0);
         // every load above is issued before the quantization starts: the
         // scheduler would otherwise interleave them with the x math and
         // issue the last weight loads only after x has arrived
@@ -246,25 +254,25 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         // wait for this wave's weight loads (vmcnt(0)), so every wave would
         // start its dots only when the slowest wave's weights had landed.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        WPrep<TYPE> wp[R];
+        for (int base = 0; base < T; base += 64 * PF) {
+            if (base) issue(base);
 #pragma unroll
-        for (int r = 0; r < R; r++) prep_task<TYPE>(td[r], ti % Tr::P, wp[r]);
-        for (; ti < T; ti += 64) {
-            const int p = ti % Tr::P, bl = ti / Tr::P;
-            if (ti != lane) {
+            for (int j = 0; j < PF; j++) {
+                const int t = base + lane + 64 * j;
+                if (t < T) {
+                    const int p = t % Tr::P, bl = t / Tr::P;
+                    WPrep<TYPE> wp[R];
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    load_task<TYPE>(wrow[r], blk0 + bl, p, td[r]);
-                    prep_task<TYPE>(td[r], p, wp[r]);
-                }
-            }
+                    for (int r = 0; r < R; r++) prep_task<TYPE>(td[j][r], p, wp[r]);
 #pragma unroll
-            for (int mi = 0; mi < MB; mi++) {
-                if (mi < m) {
-                    XTask<TYPE> xt;
-                    load_x<TYPE>(p, bl, mi, KC, nbc, lqs, ld, lbs, xt);
+                    for (int mi = 0; mi < MB; mi++) {
+                        if (mi < m) {
+                            XTask<TYPE> xt;
+                            load_x<TYPE>(p, bl, mi, KC, nbc, lqs, ld, lbs, xt);
 #pragma unroll
-                    for (int r = 0; r < R; r++) acc[r][mi] += task_dot<TYPE>(wp[r], xt);
+                            for (int r = 0; r < R; r++) acc[r][mi] += task_dot<TYPE>(wp[r], xt);
+                        }
+                    }
                 }
             }
         }
