@@ -435,7 +435,8 @@ struct XCfg {
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(BM <= 256 && (S_CHUNKS % WAVES == 0 || S_CHUNKS < WAVES), "row DMA shares");
     static_assert(64 * WAVES >= BM, "dy DMA covers the tile's rows");
-    static_assert(A_PER_WAVE == 2 || A_PER_WAVE % 4 == 0, "activation DMA spread over the four slices of a step");
+    static_assert(A_PER_WAVE == 1 || A_PER_WAVE == 2 || A_PER_WAVE % 4 == 0,
+                  "activation DMA spread over the four slices of a step");
 };
 
 // Row r of a [rows][64 halves] tile: 8 pieces of 16 bytes, piece p at
