@@ -198,7 +198,7 @@ __device__ __forceinline__ void quantize_lds(const float4 (&xv)[XN], int KC, int
 
 // WV waves of R weight rows each; MB >= m activation rows; XN x blocks
 // quantized per wave per chunk of KC elements of K.
-template <int TYPE, int MB, int R, int WV, int XN>
+template <int TYPE, int MB, int R, int WV, int XN, int PF>
 __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                      float* __restrict__ Y, int n, int K, int m, int KC,
                                                      uint32_t mg, int epi) {
@@ -229,10 +229,9 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         float4 xv[XN];
         prefetch_x<Tr::VT, WV, XN>(X, K, kc0, KC, m, mg, xv);
         // weight loads of the first PF rounds of 64 tasks (tasks past T
-        // load task 0, unused): with one or two rows a wave, rows of several
-        // rounds (long K) keep PF rounds of loads in flight instead of one
-        // (Q6_K's four-group tasks hold too many registers for more than one)
-        constexpr int PF = TYPE == T_Q6K ? 1 : R == 1 ? 4 : R == 2 ? 2 : 1;
+        // load task 0, unused; every load is unconditional, so none sits
+        // under a branch and the waits stay counted): rows of several rounds
+        // (long K) keep PF rounds of loads in flight instead of one
         TaskData td[PF][R];
         auto issue = [&](int base) {
 #pragma unroll
@@ -780,6 +779,15 @@ static size_t lds_bytes(int type, int KC, int m) {
     return b;
 }
 
+template <int TYPE, int MB, int WV, int R, int PF>
+static void launch_xn(int steps, dim3 grid, dim3 block, size_t shm, hipStream_t s, const uint8_t* wb, const float* x,
+                      float* y, int n, int K, int m, int KC, uint32_t mg, int epi) {
+    if (steps <= 1) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 1, PF>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    else if (steps <= 2) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 2, PF>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    else if (steps <= 4) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 4, PF>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    else hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 8, PF>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+}
+
 template <int TYPE, int MB, int WV, int R>
 static hipError_t launch_cfg(const void* w, const float* x, float* y, int n, int K, int m, int epi, hipStream_t s) {
     const int KC = pick_kc(TYPE, K, m, WV);
@@ -790,10 +798,15 @@ static hipError_t launch_cfg(const void* w, const float* x, float* y, int n, int
     const dim3 grid((n + WV * R - 1) / (WV * R)), block(64 * WV);
     const uint8_t* wb = (const uint8_t*)w;
     const uint32_t mg = nbc_magic(KC / (TYPE == T_Q8_0 ? 32 : 256));
-    if (steps <= 1) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 1>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
-    else if (steps <= 2) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 2>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
-    else if (steps <= 4) hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 4>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
-    else hipLaunchKernelGGL((k_matvec<TYPE, MB, R, WV, 8>), grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    // rows of more than one round of 64 tasks keep several rounds of loads
+    // in flight with one or two rows a wave (Q6_K's four-group tasks hold
+    // too many registers for that)
+    const int tasks = (KC / MvTraits<TYPE>::BE) * MvTraits<TYPE>::P;
+    constexpr int PFL = TYPE == T_Q6K ? 1 : R == 1 ? 4 : R == 2 ? 2 : 1;
+    if (PFL > 1 && tasks > 64)
+        launch_xn<TYPE, MB, WV, R, PFL>(steps, grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
+    else
+        launch_xn<TYPE, MB, WV, R, 1>(steps, grid, block, shm, s, wb, x, y, n, K, m, KC, mg, epi);
     return hipGetLastError();
 }
 
