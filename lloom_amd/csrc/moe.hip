@@ -403,42 +403,45 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
         for (int r = 0; r < RR; r++)
 #pragma unroll
             for (int q = 0; q < MOE_PG; q++) acc[r][q] = 0.0f;
-        // tasks in chunks of TPL per lane, every load of a chunk in flight
-        // at once (rows of up to TPL * LPR tasks are a single chunk)
-        for (int c0 = 0; c0 < T; c0 += TPL * LPR) {
-            TaskData td[TPL][RR];
+        // Tasks in chunks of TPL per lane.  Software-pipelined: the next
+        // chunk's loads are issued before this chunk's dots (the last
+        // chunk's "next" reloads chunk 0, from L2, so that no load sits
+        // under a branch and the waits stay counted).
+        auto load_chunk = [&](int c0, TaskData (&td)[TPL][RR]) {
 #pragma unroll
             for (int c = 0; c < TPL; c++) {
                 const int ti = c0 + c * LPR + tl;
-                const int tc = ti < T ? ti : 0;
+                const int tc = ti < T ? ti : tl;
 #pragma unroll
                 for (int r = 0; r < RR; r++) load_task<TYPE>(wrow[r], tc / Tr::P, tc % Tr::P, td[c][r]);
             }
-            if (c0 == 0) {
-                // stage planes g0 .. g0 + pg of this expert (the first
-                // chunk's weights are in flight meanwhile) and the sum of
-                // each 16-element run
-                if (g0) __syncthreads();  // the previous group's readers are done
-                for (int i = threadIdx.x; i < pg * k16; i += 256) {
-                    const int q = i / k16, c = i - q * k16;
-                    const int pl = sorted[p0 + g0 + q];
-                    const int b = pl / topk, t = pl - b * topk;
-                    const float4* xr =
-                        (const float4*)(X + (int64_t)(b * in_dim1 + (in_dim1 == 1 ? 0 : t)) * K + 16 * c);
-                    float4 v[4];
+        };
+        TaskData tda[TPL][RR];
+        load_chunk(0, tda);
+        // stage planes g0 .. g0 + pg of this expert (the first chunk's
+        // weights are in flight meanwhile) and the sum of each 16-element run
+        if (g0) __syncthreads();  // the previous group's readers are done
+        for (int i = threadIdx.x; i < pg * k16; i += 256) {
+            const int q = i / k16, c = i - q * k16;
+            const int pl = sorted[p0 + g0 + q];
+            const int b = pl / topk, t = pl - b * topk;
+            const float4* xr = (const float4*)(X + (int64_t)(b * in_dim1 + (in_dim1 == 1 ? 0 : t)) * K + 16 * c);
+            float4 v[4];
 #pragma unroll
-                    for (int u = 0; u < 4; u++) v[u] = xr[u];
-                    float4* dst = (float4*)(xs + q * KP + 16 * c + 4 * (c >> 2));
-                    float sum = 0.0f;
+            for (int u = 0; u < 4; u++) v[u] = xr[u];
+            float4* dst = (float4*)(xs + q * KP + 16 * c + 4 * (c >> 2));
+            float sum = 0.0f;
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        dst[u] = v[u];
-                        sum += v[u].x + v[u].y + v[u].z + v[u].w;
-                    }
-                    sx[q * k16 + c] = sum;
-                }
-                __syncthreads();
+            for (int u = 0; u < 4; u++) {
+                dst[u] = v[u];
+                sum += v[u].x + v[u].y + v[u].z + v[u].w;
             }
+            sx[q * k16 + c] = sum;
+        }
+        __syncthreads();
+        for (int c0 = 0; c0 < T; c0 += TPL * LPR) {
+            TaskData tdb[TPL][RR];
+            load_chunk(c0 + TPL * LPR, tdb);
 #pragma unroll
             for (int c = 0; c < TPL; c++) {
                 const int ti = c0 + c * LPR + tl;
@@ -447,7 +450,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
 #pragma unroll
                     for (int r = 0; r < RR; r++) {
                         WPrep<TYPE> wp;
-                        prep_task<TYPE>(td[c][r], ti % Tr::P, wp);
+                        prep_task<TYPE>(tda[c][r], ti % Tr::P, wp);
                         task_runs<TYPE>(wp, qv[r], ra[r], rb[r]);
                     }
                     int off[NR];
@@ -483,6 +486,10 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
                     }
                 }
             }
+#pragma unroll
+            for (int c = 0; c < TPL; c++)
+#pragma unroll
+                for (int r = 0; r < RR; r++) tda[c][r] = tdb[c][r];
         }
         // sum over the LPR lanes of the group; lane tl == 0 stores
 #pragma unroll
@@ -514,9 +521,10 @@ struct MoeOut {
 template <int TYPE, int LPR, int R, bool GLU>
 static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
                               int in_dim1, int topk, int max_slots, int pgmax, const MoeOut& o, hipStream_t s) {
-    // two tasks per lane in flight: more waves fit (148 against 183 VGPRs
-    // at four), which the loads need more than a deeper queue per wave
-    constexpr int TPL = 2;
+    // one task per lane and chunk, the next chunk's loads in flight during
+    // this chunk's dots (measured on the C5 gate call: 38.8 us, against 40.1
+    // for two tasks unpipelined and 46.5 for four)
+    constexpr int TPL = 1;
     constexpr int ROWS = 4 * (64 / LPR) * R;
     const size_t shm = (size_t)pgmax * (K + 2 * (K / 16)) * sizeof(float);
     static bool attr_set = false;
