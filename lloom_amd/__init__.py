@@ -8,6 +8,7 @@ tests and the benchmark.  PyTorch only provides device memory and streams.
 There is no CPU fallback: without the built library every call raises.
 """
 from .lib import LloomHipError, lib, lib_path  # noqa: F401
+from . import gguf_file  # noqa: F401
 from .quantized import (  # noqa: F401
     GgmlDType,
     MoeArm,

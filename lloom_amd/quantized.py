@@ -11,6 +11,8 @@ Names, argument meaning and refusals follow lloom-tensor/src/quantized/mod.rs:
   QMatMul.from_qtensor / forward          mod.rs:1698-1729, 2022-2025
   QMatMul.forward_silu / forward_mul_into, MvStore  mod.rs:1667-1696, 2102-2156
   MoeArm               mod.rs:2290-2310
+F32 / F16 / BF16 QTensors (norms and biases a GGUF file holds) are uploaded
+as is and dequantize by reinterpretation; they are not matmul weights here.
 Tensors are torch tensors on the GPU (device memory and streams only); the
 arithmetic is the C ABI's.
 """
@@ -31,13 +33,17 @@ class GgmlDType(enum.IntEnum):
     Q4K = 12
     Q6K = 14
     Q8K = 15
+    BF16 = 30
 
     def block_size(self):
-        return {GgmlDType.F32: 1, GgmlDType.F16: 1, GgmlDType.Q8_0: 32}.get(self, 256)
+        return {GgmlDType.F32: 1, GgmlDType.F16: 1, GgmlDType.BF16: 1, GgmlDType.Q8_0: 32}.get(self, 256)
 
     def type_size(self):
-        return {GgmlDType.F32: 4, GgmlDType.F16: 2, GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144,
+        return {GgmlDType.F32: 4, GgmlDType.F16: 2, GgmlDType.BF16: 2, GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144,
                 GgmlDType.Q6K: 210, GgmlDType.Q8K: 292}[self]
+
+    def is_float(self):
+        return self in (GgmlDType.F32, GgmlDType.F16, GgmlDType.BF16)
 
     def vec_dot_type(self):
         return GgmlDType.Q8_0 if self == GgmlDType.Q8_0 else GgmlDType.Q8K
@@ -109,7 +115,14 @@ class MvStore(enum.IntEnum):
 
 # ------------------------------------------------------------ QTensor ---
 
+_FLOAT_TORCH = {GgmlDType.F32: torch.float32, GgmlDType.F16: torch.float16, GgmlDType.BF16: torch.bfloat16}
+
+
 def _padded_bytes(dtype, n_rows, k):
+    if dtype.is_float():
+        # Unblocked storage (norms, biases): read by reinterpretation, no kernel tail pad.
+        b = n_rows * k * dtype.type_size()
+        return b, b
     packed, alloc = ctypes.c_size_t(), ctypes.c_size_t()
     check(lib().lloom_hip_weight_bytes(int(dtype), n_rows, k, ctypes.byref(packed), ctypes.byref(alloc)))
     return packed.value, alloc.value
@@ -128,7 +141,7 @@ class QTensor:
     @staticmethod
     def quantize(src, dtype):
         dtype = GgmlDType(dtype)
-        if dtype in (GgmlDType.F32, GgmlDType.F16):
+        if dtype.is_float():
             raise LloomHipError(2, f"{dtype.name} is not a block type on the HIP quantized path")
         shape = tuple(src.shape)
         bs = dtype.block_size()
@@ -166,6 +179,10 @@ class QTensor:
         return int(np.prod(self.shape))
 
     def _dequant(self, out_dtype, torch_dtype):
+        if self.dtype.is_float():
+            # F32 / F16 / BF16 storage: a reinterpretation, then a conversion
+            return self.storage[:self.packed_bytes()].view(_FLOAT_TORCH[self.dtype]).reshape(self.shape) \
+                .to(torch_dtype)
         y = torch.empty(self.shape, dtype=torch_dtype, device=self.storage.device)
         check(lib().lloom_hip_dequantize(_ctx(_dev_index(self.storage)), int(self.dtype), _ptr(self.storage),
                                          self.elem_count(), _ptr(y), out_dtype, _stream(self.storage)))
@@ -295,6 +312,9 @@ class QMatMul:
     def __init__(self, qtensor):
         if len(qtensor.shape) != 2:
             raise LloomHipError(3, f"QMatMul weight must be [n, k], got {qtensor.shape}")
+        if qtensor.dtype.is_float() or qtensor.dtype == GgmlDType.Q8K:
+            raise LloomHipError(2, f"QMatMul over a {qtensor.dtype.name} weight is not a quantized matmul "
+                                   f"(the HIP arm multiplies Q8_0, Q4K, Q6K)")
         self.qtensor = qtensor
 
     @staticmethod
