@@ -347,6 +347,7 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 constexpr int MOE_PG = 8;          // planes staged per pass
+constexpr int MOE_FUSE_MAX = 1024;  // planes routed inside k_moe_lds (an LDS list per workgroup)
 constexpr int MOE_LDS = 72 * 1024;  // bytes of staged planes and run sums
 
 // One workgroup (4 waves) per (block of rows, active-expert slot).  In a
@@ -360,15 +361,64 @@ constexpr int MOE_LDS = 72 * 1024;  // bytes of staged planes and run sums
 // element (silu_mul order) over the two sums the pair would store.
 template <int TYPE, int LPR, int R, int TPL, bool GLU>
 __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                 float* __restrict__ Y, const int* __restrict__ ws, int E, int n,
-                                                 int K, int in_dim1, int topk, int pgmax,
-                                                 const uint8_t* __restrict__ W2, float* __restrict__ Y2) {
+                                                 float* __restrict__ Y, int* ws, int E, int n, int K, int in_dim1,
+                                                 int topk, int pgmax, const uint8_t* __restrict__ W2,
+                                                 float* __restrict__ Y2, const uint32_t* __restrict__ ids,
+                                                 int planes, int* sticky, int route) {
     using Tr = MvTraits<TYPE>;
     constexpr int NR = MoeRuns<TYPE>::N;
     constexpr int RR = GLU ? 2 * R : R;  // weight rows a lane holds
+    constexpr int ROWS = 4 * (64 / LPR) * R;  // rows of a workgroup
     if (!GLU && blockIdx.z) {
         W = W2;
         Y = Y2;
+    }
+    // Routing.  With `route` 0 the workgroup of expert blockIdx.y collects
+    // the planes routed to it from ids itself, and the grid layer y = E
+    // zeroes the outputs of out-of-range ids and raises the flags (what
+    // k_moe_route does, without its launch); otherwise k_moe_route has
+    // sorted the planes and y is the active-expert slot.
+    __shared__ int s_list[MOE_FUSE_MAX];
+    __shared__ int s_np;
+    int e, np;
+    const int* list;
+    if (!route) {
+        if ((int)blockIdx.y == E) {
+            const int r0 = blockIdx.x * ROWS, r1 = min(r0 + ROWS, n);
+            int bad = 0;
+            for (int p = threadIdx.x; p < planes; p += 256) {
+                if (ids[p] >= (uint32_t)E) {
+                    bad = 1;
+                    for (int r = r0; r < r1; r++) Y[(int64_t)p * n + r] = 0.0f;
+                }
+            }
+            bad = __syncthreads_or(bad);
+            if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.z == 0) {
+                ws[0] = bad;  // this call: read back by a strict call
+                if (bad) sticky[0] = 1;
+            }
+            return;
+        }
+        e = blockIdx.y;
+        if (threadIdx.x == 0) s_np = 0;
+        __syncthreads();
+        // the list's order follows the LDS atomics; every plane's dot is
+        // computed on its own, so no result depends on it
+        for (int p = threadIdx.x; p < planes; p += 256)
+            if (ids[p] == (uint32_t)e) s_list[atomicAdd(&s_np, 1)] = p;
+        __syncthreads();
+        np = s_np;
+        if (np == 0) return;  // uniform
+        list = s_list;
+    } else {
+        const int* count = ws + 2;
+        const int* start = count + E;
+        const int* active = start + E;
+        const int* sorted = active + E;
+        if ((int)blockIdx.y >= ws[1]) return;  // uniform: fewer active experts than slots
+        e = active[blockIdx.y];
+        np = count[e];
+        list = sorted + start[e];
     }
     // [pgmax][KP] planes, then [pgmax][K / 16] run sums.  A plane stores
     // element e at e + 4 (e / 64): the eight tasks of a superblock read
@@ -377,14 +427,6 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
     extern __shared__ __align__(16) float xs[];
     const int KP = K + K / 16;
     float* sx = xs + pgmax * KP;
-    const int* count = ws + 2;
-    const int* start = count + E;
-    const int* active = start + E;
-    const int* sorted = active + E;
-    const int slot = blockIdx.y;
-    if (slot >= ws[1]) return;  // uniform: fewer active experts than slots
-    const int e = active[slot];
-    const int np = count[e], p0 = start[e];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane / LPR, tl = lane % LPR;
     const int row0 = ((blockIdx.x * 4 + wave) * (64 / LPR) + grp) * R;
@@ -423,7 +465,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
         if (g0) __syncthreads();  // the previous group's readers are done
         for (int i = threadIdx.x; i < pg * k16; i += 256) {
             const int q = i / k16, c = i - q * k16;
-            const int pl = sorted[p0 + g0 + q];
+            const int pl = list[g0 + q];
             const int b = pl / topk, t = pl - b * topk;
             const float4* xr = (const float4*)(X + (int64_t)(b * in_dim1 + (in_dim1 == 1 ? 0 : t)) * K + 16 * c);
             float4 v[4];
@@ -495,7 +537,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
 #pragma unroll
         for (int q = 0; q < MOE_PG; q++) {
             if (q < pg) {
-                const int pl = sorted[p0 + g0 + q];
+                const int pl = list[g0 + q];
 #pragma unroll
                 for (int r = 0; r < R; r++) {
                     float v = group_sum<LPR>(acc[r][q]);
@@ -516,11 +558,15 @@ struct MoeOut {
     int mode;
     const void* w2;
     float* y2;
+    const uint32_t* ids;  // the routing inputs, for a call routed in-kernel
+    int planes;
+    int* sticky;
+    bool route;  // k_moe_route sorted the planes
 };
 
 template <int TYPE, int LPR, int R, bool GLU>
-static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
-                              int in_dim1, int topk, int max_slots, int pgmax, const MoeOut& o, hipStream_t s) {
+static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, int* ws, int E, int n, int K, int in_dim1,
+                              int topk, int max_slots, int pgmax, const MoeOut& o, hipStream_t s) {
     // one task per lane and chunk, the next chunk's loads in flight during
     // this chunk's dots (measured on the C5 gate call: 38.8 us, against 40.1
     // for two tasks unpipelined and 46.5 for four)
@@ -534,9 +580,10 @@ static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, const int
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    dim3 grid((n + ROWS - 1) / ROWS, max_slots, o.mode == MOE_PAIR ? 2 : 1);
+    dim3 grid((n + ROWS - 1) / ROWS, o.route ? max_slots : E + 1, o.mode == MOE_PAIR ? 2 : 1);
     hipLaunchKernelGGL((k_moe_lds<TYPE, LPR, R, TPL, GLU>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ws, E,
-                       n, K, in_dim1, topk, pgmax, (const uint8_t*)o.w2, o.y2);
+                       n, K, in_dim1, topk, pgmax, (const uint8_t*)o.w2, o.y2, o.ids, o.planes, o.sticky,
+                       o.route ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -544,7 +591,7 @@ static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, const int
 // GLU holds each row of both weights: half the rows per lane of the plain
 // kernel, the same registers.
 template <int TYPE, bool GLU>
-static hipError_t moe_lds_type(const void* w, const float* x, float* y, const int* ws, int E, int n, int K,
+static hipError_t moe_lds_type(const void* w, const float* x, float* y, int* ws, int E, int n, int K,
                                int in_dim1, int topk, int max_slots, int pgmax, const MoeOut& o, hipStream_t s) {
     using Tr = MvTraits<TYPE>;
     constexpr int R = (TYPE == T_Q6K || GLU) ? 1 : 2;
@@ -599,11 +646,16 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
                       int64_t in_dim1, const uint32_t* ids, int64_t topk, float* y, int* ws, int* sticky,
                       int mode, const void* w2, float* y2, hipStream_t s) {
     int planes = (int)(batch * topk);
-    // planes of bad ids are zeroed in every output
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 2 * E * sizeof(int), s, ids, planes, (int)E, ws, sticky, y,
-                       mode == MOE_PAIR ? y2 : nullptr, (int)n);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
+    // the staged kernel routes up to MOE_FUSE_MAX planes itself (no routing
+    // launch); otherwise k_moe_route sorts them first.  Planes of bad ids are
+    // zeroed in every output either way.
+    const bool route = !moe_stages(k) || planes > MOE_FUSE_MAX;
+    hipError_t err = hipSuccess;
+    if (route) {
+        hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 2 * E * sizeof(int), s, ids, planes, (int)E, ws, sticky,
+                           y, mode == MOE_PAIR ? y2 : nullptr, (int)n);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
     int max_slots = (int)(E < planes ? E : planes);
     const int64_t per_plane = (k + 2 * (k / 16)) * (int64_t)sizeof(float);
     int pgmax = MOE_LDS / per_plane < MOE_PG ? (int)(MOE_LDS / per_plane) : MOE_PG;
@@ -611,7 +663,7 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
     // average) stages four planes at a time: half the LDS, so more
     // workgroups share a CU (C5: 40 us against 46 us per routed call)
     if (planes <= 4 * max_slots && pgmax > 4) pgmax = 4;
-    const MoeOut o{mode, w2, y2};
+    const MoeOut o{mode, w2, y2, ids, planes, sticky, route};
     const int Ei = (int)E, ni = (int)n, ki = (int)k, d1 = (int)in_dim1, tk = (int)topk;
     if (moe_stages(k)) {
         if (mode == MOE_GLU) {

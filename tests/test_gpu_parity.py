@@ -317,6 +317,57 @@ def test_moe_run_to_run_identical(L):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def test_moe_many_planes_and_magnitudes(L):
+    """Q4_K experts with dense routing (about 24 planes an expert: more than
+    one pass of staged planes) and planes of very different magnitude (the
+    fp16 operand path scales each plane by its own power of two): 1e4-scaled,
+    1e-6-scaled, all-zero, and one element past the fp16 range."""
+    rng = np.random.default_rng(21)
+    E, n, k, batch, topk = 4, 80, 1024, 24, 4
+    w = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((batch, 1, k)).astype(np.float32)
+    x[0] *= np.float32(1e4)
+    x[1] *= np.float32(1e-6)
+    x[2] = 0.0
+    x[3, 0, 5] = 70000.0
+    ids = rng.integers(0, E, (batch, topk)).astype(np.uint32)
+    qt = L.QTensor.quantize(_cuda(w), O.Q4K)
+    got = qt.indexed_moe_forward(_cuda(x), _cuda(ids.astype(np.int32))).cpu().numpy()
+    q = qt.data()
+    want = O.matmul_indexed(O.Q4K, q, E, n, k, x, ids)
+    assert_rows_close(got, want, what="moe many planes")
+    assert np.all(got[2] == 0.0)
+    dense = O.dequantize(O.Q4K, q, w.size).reshape(E, n, k).astype(np.float64)
+    ref = np.stack([np.stack([dense[ids[b, t]] @ x[b, 0].astype(np.float64) for t in range(topk)])
+                    for b in range(batch)])
+    scale = np.abs(ref).max(axis=2, keepdims=True) + 1e-30
+    assert np.max(np.abs(ref - got) / scale) < 1e-5
+
+
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q8_0])
+def test_moe_more_planes_than_one_list(L, dt):
+    """1200 planes: past the in-kernel routing list, so the routing kernel
+    sorts the planes first; a bad id among them is refused and its planes
+    zeroed."""
+    rng = np.random.default_rng(31)
+    E, n, k, batch, topk = 8, 24, 256, 300, 4
+    got, want, _ = _moe_case(L, dt, E, n, k, batch, topk, 1, seed=31)
+    assert_rows_close(got, want, what="moe 1200 planes")
+    w = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), dt)
+    ids = rng.integers(0, E, (batch, topk)).astype(np.int32)
+    ids[7, 2] = E
+    x = _cuda(rng.standard_normal((batch, 1, k)).astype(np.float32))
+    with pytest.raises(L.LloomHipError):
+        qt.indexed_moe_forward(x, _cuda(ids))
+    y = qt.indexed_moe_forward(x, _cuda(ids), strict=False).cpu().numpy()
+    assert np.all(y[7, 2] == 0) and np.any(y[7, 1] != 0)
+    from lloom_amd.quantized import _ctx
+    from lloom_amd.lib import lib
+
+    assert lib().lloom_hip_ctx_sync(_ctx(0)) == 4
+
+
 def test_moe_out_of_range_expert_is_refused(L):
     rng = np.random.default_rng(0)
     w = (rng.standard_normal((4, 8, 256)) * 0.05).astype(np.float32)
