@@ -26,8 +26,11 @@
  *   matmul                : GEMM rows == per-row decode bit for bit
  *                           (:1769-1903), scalar f64 oracle <= 0.02
  *   matmul_indexed        : closed form (dequantized row, sequential f32 dot)
- *   quantized_matmul_*    : StdRng known answers (:1441-1542) are "parity
- *                           unpinned": they need rand 0.9 ChaCha12 bits.
+ *   quantize -> matmul    : the StdRng known answers of quantized_matmul_
+ *                           q4k/q6k/q8k (:1441-1542), with the inputs drawn
+ *                           by tests/stdrng.py (rand 0.9's ChaCha12 StdRng
+ *                           and its f32 sampling, restated and pinned by the
+ *                           same tests' literals)
  */
 #ifndef KQ_ORACLE_H
 #define KQ_ORACLE_H
