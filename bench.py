@@ -182,7 +182,14 @@ def main():
         per_b[str(b)] = {"us": round(t * 1e6, 3), "GB/s": round(algo[b] / t / 1e9, 1),
                          "hbm_frac": round(algo[b] / t / 1e9 / HBM_PEAK_GBS, 4)}
 
-    details = {"c2_q4k_decode_per_batch": per_b, "rotation_copies": len(rot),
+    # the same launches on one copy: weights resident in the 256 MB MALL
+    warm = {}
+    for b in Bs:
+        fns = [launch(b, qt) for _ in range(len(rot))]
+        t = time_graph(fns, 3, 1) / len(fns)
+        warm[str(b)] = {"us": round(t * 1e6, 3), "GB/s": round(algo[b] / t / 1e9, 1)}
+    warm["note"] = "one weight copy replayed: MALL-resident, not an HBM figure"
+    details = {"c2_q4k_decode_per_batch": per_b, "c2_q4k_decode_warm": warm, "rotation_copies": len(rot),
                "rotation_bytes": len(rot) * wbytes}
     # Roofline of the path's dominant kernel: the single-row decode matvec
     # (C2 at B=1, one kernel per call): algorithmic bytes per launch over the
