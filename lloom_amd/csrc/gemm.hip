@@ -829,6 +829,133 @@ __global__ __launch_bounds__(64 * WV) void k_gemm_q4k_x16(const uint8_t* __restr
         }
 }
 
+// ---------------------------------------- few activation rows (17..) --
+// The x16 GEMM's arithmetic (exact integer operands on
+// v_mfma_f32_32x32x16_f16, the same per-superblock epilogue, the same
+// prepared activations) for a few dozen activation rows, where its 128-row
+// LDS tiles leave most CUs idle.  A workgroup owns 32 weight columns and 64
+// activation rows (grid y: the next 64); its KS waves split K (wave w takes
+// superblocks w, w + KS, ...) and load their operands straight from memory
+// into registers (every superblock's loads issued at once, no LDS staging);
+// the waves' partial sums meet in LDS in a fixed order.
+template <int KS, int MT>
+__global__ __launch_bounds__(64 * KS) void k_gemm_q4k_skinny(const uint8_t* __restrict__ W,
+                                                               const _Float16* __restrict__ x16,
+                                                               const _Float16* __restrict__ amin,
+                                                               const float* __restrict__ dyt, float* __restrict__ Y,
+                                                               int m, int n, int k, int epi) {
+    __shared__ float part[KS - 1][MT][16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, c32 = lane & 31;
+    const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32 * MT;
+    const int nsb = k >> 8;
+    const uint8_t* wcol = W + (int64_t)min(n0 + c32, n - 1) * nsb * Q4K_BYTES;
+    int arow[MT];
+#pragma unroll
+    for (int a = 0; a < MT; a++) arow[a] = min(m0 + 32 * a + c32, m - 1);
+
+    v16f out[MT];
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) out[a][r] = 0.0f;
+
+    for (int sb = wave; sb < nsb; sb += KS) {
+        const uint8_t* wb = wcol + (size_t)sb * Q4K_BYTES;
+        const uint4 hdr = *(const uint4*)wb;
+        uint4 raw[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) raw[c] = *(const uint4*)(wb + 16 + 32 * c + 16 * h);
+        // activations one step ahead of the MFMAs that use them (all four
+        // steps at once measured slower: the registers cost waves)
+        auto load_a = [&](int c, v8h (&av)[MT][4]) {
+#pragma unroll
+            for (int a = 0; a < MT; a++)
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+                    av[a][kk] = *(const v8h*)(x16 + (size_t)arow[a] * k + 256 * sb + 64 * c + 8 * x_piece(kk, h));
+        };
+        v8h av[MT][4];
+        load_a(0, av);
+        v16f acc[MT];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            v8h avn[MT][4];
+            if (c < 3) load_a(c + 1, avn);
+            __builtin_amdgcn_sched_barrier(0);
+            const BScale bs = bscale(hdr, c);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const v8h b = build_kk(raw[c], bs, kk);
+#pragma unroll
+                for (int a = 0; a < MT; a++) {
+                    if (c == 0 && kk == 0) {
+                        const v16f z = {};
+                        acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], b, z, 0, 0, 0);
+                    } else {
+                        acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], b, acc[a], 0, 0, 0);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (c < 3) {
+#pragma unroll
+                for (int a = 0; a < MT; a++)
+#pragma unroll
+                    for (int kk = 0; kk < 4; kk++) av[a][kk] = avn[a][kk];
+            }
+        }
+        // superblock epilogue: min term on MFMA, then out += dy (d D - dmin Dmin)
+        const float d = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
+        const uint64_t m8 = (uint64_t)(hdr.z & 0x3F3F3F3Fu) |
+                            ((uint64_t)(((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u)) << 32);
+        v8h bmv;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
+            bmv[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
+        }
+#pragma unroll
+        for (int a = 0; a < MT; a++) {
+            const v8h am = *(const v8h*)(amin + ((size_t)arow[a] * nsb + sb) * 16 + 8 * h);
+            const v16f z = {};
+            const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bmv, z, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = min(m0 + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3), m - 1);
+                const float dy = dyt[(size_t)sb * m + row];
+                out[a][r] = __builtin_fmaf(dy, __builtin_fmaf(d, acc[a][r], -(dmin * dm[r])), out[a][r]);
+            }
+        }
+    }
+    if constexpr (KS > 1) {
+        if (wave) {
+#pragma unroll
+            for (int a = 0; a < MT; a++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) part[wave - 1][a][r][lane] = out[a][r];
+        }
+        __syncthreads();
+        if (wave) return;
+#pragma unroll
+        for (int w = 0; w < KS - 1; w++)
+#pragma unroll
+            for (int a = 0; a < MT; a++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) out[a][r] += part[w][a][r][lane];
+    }
+    const int col = n0 + c32;
+    if (col < n) {
+#pragma unroll
+        for (int a = 0; a < MT; a++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < m) store_epi(&Y[(int64_t)row * n + col], out[a][r], epi);
+            }
+    }
+}
+
 // ------------------------------------------------------------ dispatch --
 
 // The kernels index activations and weights with 32-bit byte offsets.
@@ -838,10 +965,10 @@ static bool fits_32bit(int64_t n, int64_t k, int64_t m) {
            m * (k / 256) * 32 < ((int64_t)1 << 31);
 }
 
-// Q4_K up to 64 rows (measured crossover with the x16 GEMM, whose 128-row
-// tiles leave most CUs idle there), and Q6_K at every size, take the MFMA
-// decode kernel with 64 activation rows per workgroup layer (launch_mq).
-// LLOOM_HIP_MQ_MAX_ROWS overrides the Q4_K limit (read once).
+// Q6_K at every size takes the MFMA decode kernel with 64 activation rows
+// per workgroup layer (launch_mq); Q4_K does only past the skinny kernel's
+// limit and up to LLOOM_HIP_MQ_MAX_ROWS (default 64, read once), or with
+// the int8-plane GEMM selected.
 static int64_t mq_max_rows() {
     static const int64_t v = [] {
         const char* e = getenv("LLOOM_HIP_MQ_MAX_ROWS");
@@ -852,7 +979,9 @@ static int64_t mq_max_rows() {
 
 static bool use_mq(int type, int64_t m) { return type == T_Q6K || (type == T_Q4K && m <= mq_max_rows()); }
 
+static int64_t skinny_max_rows();
 size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
+    if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(0, k, m) && mode != GEMM_INT8) return x16_bytes(m, k);
     if (use_mq(type, m)) return split_q8k_bytes(k, m);
     if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
     return matvec_workspace_bytes(type == T_Q4K ? T_Q6K : type, k, 16);
@@ -887,8 +1016,38 @@ static int x16_tile_env() {
     return v;
 }
 
+// Q4_K from 17 to 128 activation rows takes k_gemm_q4k_skinny (measured
+// on [8192, 2048]: m = 24 11.3 us against 14.8 for the MFMA decode kernel,
+// m = 96 24.6 against 34.8 for the x16 GEMM; from m = 256 its per-column-
+// block re-reads of the activations lose to the GEMM's LDS tiles).
+// LLOOM_HIP_SKINNY_MAX_ROWS overrides the limit (read once).
+static int64_t skinny_max_rows() {
+    static const int64_t v = [] {
+        const char* e = getenv("LLOOM_HIP_SKINNY_MAX_ROWS");
+        return e ? (int64_t)atoll(e) : (int64_t)128;
+    }();
+    return v;
+}
+
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, int mode, int epi, hipStream_t s) {
+    if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(n, k, m) && mode != GEMM_INT8) {
+        X16Ptrs p = x16_ptrs(qbuf, m, k);
+        const int64_t nb = m * (k / 256);
+        hipLaunchKernelGGL(k_gemm_prep_x16, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.x16, p.amin,
+                           p.dyt, (int)m, (int)k);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
+        // one 32-row tile a workgroup (two measured slower: registers)
+        if (k >= 8 * 256)
+            hipLaunchKernelGGL((k_gemm_q4k_skinny<8, 1>), grid, dim3(512), 0, s, (const uint8_t*)w, p.x16, p.amin,
+                               p.dyt, y, (int)m, (int)n, (int)k, epi);
+        else
+            hipLaunchKernelGGL((k_gemm_q4k_skinny<4, 1>), grid, dim3(256), 0, s, (const uint8_t*)w, p.x16, p.amin,
+                               p.dyt, y, (int)m, (int)n, (int)k, epi);
+        return hipGetLastError();
+    }
     if (use_mq(type, m)) return launch_mq(type, w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
@@ -897,9 +1056,12 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                            p.dyt, (int)m, (int)k);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        // 256-row tiles once there are enough of them to fill the chip
+        // 128 x 256 tiles (8 waves) past 512 rows: there the 128 x 128
+        // tiles start a second, mostly empty round of workgroups (measured
+        // on [8192, 2048]: m = 640 53.7 against 70.1 us, m = 512 52.2
+        // against 42.0)
         int tile = x16_tile_env();
-        if (tile < 0) tile = m >= 1024 ? 3 : 2;
+        if (tile < 0) tile = m > 512 ? 3 : 2;
         switch (tile) {
             case 0: return launch_x16<4, 2, 4>(w, p, y, n, k, m, epi, s);
             case 1: return launch_x16<4, 4, 4>(w, p, y, n, k, m, epi, s);
