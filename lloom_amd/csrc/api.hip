@@ -274,8 +274,8 @@ static int qmatmul_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, in
     std::lock_guard<std::mutex> lock(ctx->mu);
     const bool decode = m <= ctx->mv_rows_max;
     void* ws = nullptr;
-    size_t need = decode ? matvec_workspace_bytes(ggml_type, k, m)
-                         : gemm_workspace_bytes(ggml_type, k, m, ctx->prefill_mma);
+    size_t need = decode ? matvec_workspace_bytes(ggml_type, n, k, m)
+                         : gemm_workspace_bytes(ggml_type, n, k, m, ctx->prefill_mma);
     if (need) {
         int rc = ensure_ws(ctx, need, &ws);
         if (rc) return rc;

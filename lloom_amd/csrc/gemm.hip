@@ -980,11 +980,11 @@ static int64_t mq_max_rows() {
 static bool use_mq(int type, int64_t m) { return type == T_Q6K || (type == T_Q4K && m <= mq_max_rows()); }
 
 static int64_t skinny_max_rows();
-size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode) {
+size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode) {
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(0, k, m) && mode != GEMM_INT8) return x16_bytes(m, k);
     if (use_mq(type, m)) return split_q8k_bytes(k, m);
     if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
-    return matvec_workspace_bytes(type == T_Q4K ? T_Q6K : type, k, 16);
+    return matvec_workspace_bytes(type, n, k, 16);
 }
 
 template <int MT, int WNW, int WV>

@@ -27,7 +27,7 @@ hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_
 // kernel; Q4_K with more rows takes the MFMA kernel on a workspace of
 // matvec_workspace_bytes.
 constexpr int MV_DOT_MAX_ROWS = 2;
-size_t matvec_workspace_bytes(int type, int64_t k, int64_t m);
+size_t matvec_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, int epi, hipStream_t s);
 // matvec.hip: Q4_K / Q6_K with any number of rows on the MFMA decode kernel,
@@ -42,7 +42,7 @@ hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t 
 constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, int mode, int epi, hipStream_t s);
-size_t gemm_workspace_bytes(int type, int64_t k, int64_t m, int mode);
+size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode);
 
 // moe.hip
 // The router keeps two ints per expert in LDS.

@@ -400,14 +400,18 @@ __device__ __forceinline__ void mf_compute(const MfW<TYPE>& w, const long (&a)[8
 template <int TYPE, int KS, int NT, int MA>
 __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                      const float* __restrict__ xd, float* __restrict__ Y, int n,
-                                                     int K, int m, int mp, int epi) {
+                                                     int K, int m, int mp, int epi, int sbs,
+                                                     float* __restrict__ psum) {
     constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float4 part[KS > 1 ? KS - 1 : 1][NT][MA][64];
     __shared__ __align__(16) uint8_t mft[KS][NT][16 * MfRs<TYPE>::V];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int nsb = K >> 8;
-    const int64_t rowbytes = (int64_t)nsb * BB;
+    // split K (grid z): this workgroup's superblocks [sb0, nsb), its sums to
+    // psum[z] for k_sum_splits
+    const int nsb_all = K >> 8;
+    const int sb0 = blockIdx.z * sbs, nsb = min(sb0 + sbs, nsb_all);
+    const int64_t rowbytes = (int64_t)nsb_all * BB;
     const uint8_t* wrow[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) wrow[t] = W + (int64_t)min(blockIdx.x * 16 * NT + 16 * t + c16, n - 1) * rowbytes;
@@ -441,8 +445,8 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
             dy = *(const float4*)(xd + (int64_t)sbc * mp + 16 * mt0 + 4 * g);
         }
     };
-    issue(wave, wc, avc, dyc);
-    for (int sb = wave; sb < nsb; sb += KS) {
+    issue(sb0 + wave, wc, avc, dyc);
+    for (int sb = sb0 + wave; sb < nsb; sb += KS) {
         // the next superblock's loads, when this wave has one (wave-uniform)
         const bool more = sb + KS < nsb;
         MfL<TYPE> wn[NT];
@@ -527,7 +531,10 @@ __global__ __launch_bounds__(64 * KS) void k_mv_mfma(const uint8_t* __restrict__
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int mi = 16 * (mt0 + u) + 4 * g + v;
-                    if (mi < m) store_epi(&Y[(int64_t)mi * n + nrow], out[t][u][v], epi);
+                    if (mi < m) {
+                        if (psum) psum[((int64_t)blockIdx.z * m + mi) * n + nrow] = out[t][u][v];
+                        else store_epi(&Y[(int64_t)mi * n + nrow], out[t][u][v], epi);
+                    }
                 }
         }
     }
@@ -709,35 +716,74 @@ static hipError_t launch_type(const void* w, const float* x, float* y, int n, in
     return launch_cfg<TYPE, 16, 4, 2>(w, x, y, n, K, m, epi, s);
 }
 
-size_t matvec_workspace_bytes(int type, int64_t k, int64_t m) {
+// Splits of K across workgroups for the 16-wave shape (fewer 16-row tiles
+// than CUs and a long K): enough to reach ~256 workgroups, at least 16
+// superblocks (one a wave) each.
+static int mv_splits(int64_t n, int64_t k) {
+    const int64_t tiles = (n + 15) / 16, nsb = k / 256;
+    if (n >= 16 * 256 || k < 16 * 256) return 1;
+    int sp = 1;
+    while (sp < 4 && tiles * sp * 2 <= 256 && nsb / (sp * 2) >= 16) sp *= 2;
+    return sp;
+}
+
+size_t matvec_workspace_bytes(int type, int64_t n, int64_t k, int64_t m) {
     if (type == T_Q8_0 || m <= MV_DOT_MAX_ROWS) return 0;
-    return split_q8k_bytes(k, m);
+    const size_t q = (split_q8k_bytes(k, m) + 255) & ~(size_t)255;
+    const int sp = mv_splits(n, k);
+    return q + (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0);
+}
+
+// The split-K partial sums after the quantized activations in the workspace.
+static float* mv_psum(void* ws, int64_t k, int64_t m) {
+    return (float*)((uint8_t*)ws + ((split_q8k_bytes(k, m) + 255) & ~(size_t)255));
+}
+
+// The split-K partial sums of k_mv_mfma, added in split order, then the
+// call's store epilogue.
+__global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ psum, int splits, int64_t mn,
+                                                    float* __restrict__ Y, int epi) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= mn) return;
+    float v = psum[i];
+    for (int z = 1; z < splits; z++) v += psum[z * mn + i];
+    store_epi(&Y[i], v, epi);
 }
 
 template <int TYPE, int MA>
 static hipError_t launch_mv_mfma(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xq,
-                                 const float* xd, int epi, hipStream_t s) {
+                                 const float* xd, int epi, hipStream_t s, float* psum = nullptr) {
     // 8 waves split K; 2 row tiles per workgroup unless that leaves fewer
     // than ~256 workgroups
     constexpr int KS = 8;
     const unsigned layers = (unsigned)((m + 16 * MA - 1) / (16 * MA));
     const int mp = (int)((m + 15) & ~(int64_t)15);
+    const int nsb = (int)(k / 256);
     if constexpr (MA == 1) {
         if (n >= 2 * 16 * 256) {
             hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 2, MA>), dim3((unsigned)((n + 31) / 32), layers), dim3(64 * KS), 0,
-                               s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
+                               s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi, nsb, nullptr);
             return hipGetLastError();
         }
         if (n < 16 * 256 && k >= 16 * 256) {
-            // fewer row tiles than CUs and a long K: 16 waves split K
-            hipLaunchKernelGGL((k_mv_mfma<TYPE, 16, 1, MA>), dim3((unsigned)((n + 15) / 16), layers), dim3(64 * 16),
-                               0, s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
+            // fewer row tiles than CUs and a long K: 16 waves split K, and
+            // with a partial-sum buffer the workgroups split it too
+            const int sp = psum ? mv_splits(n, k) : 1;
+            const int sbs = (nsb + sp - 1) / sp;
+            hipLaunchKernelGGL((k_mv_mfma<TYPE, 16, 1, MA>), dim3((unsigned)((n + 15) / 16), layers, sp),
+                               dim3(64 * 16), 0, s, (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi, sbs,
+                               sp > 1 ? psum : nullptr);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess || sp == 1) return e;
+            const int64_t mn = m * n;
+            hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, psum, sp, mn, y,
+                               epi);
             return hipGetLastError();
         }
     }
     {
         hipLaunchKernelGGL((k_mv_mfma<TYPE, KS, 1, MA>), dim3((unsigned)((n + 15) / 16), layers), dim3(64 * KS), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi);
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)k, (int)m, mp, epi, nsb, nullptr);
     }
     return hipGetLastError();
 }
@@ -764,8 +810,9 @@ hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int6
         split_q8k_ptrs(ws, k, m, &xq, &xd);
         hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
         if (e != hipSuccess) return e;
-        return type == T_Q4K ? launch_mv_mfma<T_Q4K, 1>(w, y, n, k, m, xq, xd, epi, s)
-                             : launch_mv_mfma<T_Q6K, 1>(w, y, n, k, m, xq, xd, epi, s);
+        float* ps = mv_psum(ws, k, m);
+        return type == T_Q4K ? launch_mv_mfma<T_Q4K, 1>(w, y, n, k, m, xq, xd, epi, s, ps)
+                             : launch_mv_mfma<T_Q6K, 1>(w, y, n, k, m, xq, xd, epi, s, ps);
     }
     switch (type) {
         case T_Q4K: return launch_type<T_Q4K>(w, x, y, (int)n, (int)k, (int)m, epi, s);
