@@ -833,126 +833,129 @@ __global__ __launch_bounds__(64 * WV) void k_gemm_q4k_x16(const uint8_t* __restr
 // The x16 GEMM's arithmetic (exact integer operands on
 // v_mfma_f32_32x32x16_f16, the same per-superblock epilogue, the same
 // prepared activations) for a few dozen activation rows, where its 128-row
-// LDS tiles leave most CUs idle.  A workgroup owns 32 weight columns and 64
-// activation rows (grid y: the next 64); its KS waves split K (wave w takes
-// superblocks w, w + KS, ...) and load their operands straight from memory
-// into registers (every superblock's loads issued at once, no LDS staging);
-// the waves' partial sums meet in LDS in a fixed order.
-template <int KS, int MT>
+// LDS tiles leave most CUs idle.  A workgroup owns 32 activation rows (grid
+// y) and NT tiles of 32 weight columns (grid x); its KS waves split K (wave
+// w takes superblocks w, w + KS, ...) and load their operands straight from
+// memory into registers, the next step's activations in flight during this
+// step's MFMAs; each activation operand serves the NT weight tiles (the
+// activations re-read per column block are this kernel's main traffic).
+// The waves' partial sums meet in LDS in a fixed order.
+template <int KS, int NT>
 __global__ __launch_bounds__(64 * KS) void k_gemm_q4k_skinny(const uint8_t* __restrict__ W,
                                                                const _Float16* __restrict__ x16,
                                                                const _Float16* __restrict__ amin,
                                                                const float* __restrict__ dyt, float* __restrict__ Y,
                                                                int m, int n, int k, int epi) {
-    __shared__ float part[KS - 1][MT][16][64];
+    __shared__ float part[KS - 1][NT][16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = lane >> 5, c32 = lane & 31;
-    const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32 * MT;
+    const int n0 = blockIdx.x * 32 * NT, m0 = blockIdx.y * 32;
     const int nsb = k >> 8;
-    const uint8_t* wcol = W + (int64_t)min(n0 + c32, n - 1) * nsb * Q4K_BYTES;
-    int arow[MT];
+    const uint8_t* wcol[NT];
 #pragma unroll
-    for (int a = 0; a < MT; a++) arow[a] = min(m0 + 32 * a + c32, m - 1);
+    for (int b = 0; b < NT; b++) wcol[b] = W + (int64_t)min(n0 + 32 * b + c32, n - 1) * nsb * Q4K_BYTES;
+    const int arow = min(m0 + c32, m - 1);
 
-    v16f out[MT];
+    v16f out[NT];
 #pragma unroll
-    for (int a = 0; a < MT; a++)
+    for (int b = 0; b < NT; b++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) out[a][r] = 0.0f;
+        for (int r = 0; r < 16; r++) out[b][r] = 0.0f;
 
     for (int sb = wave; sb < nsb; sb += KS) {
-        const uint8_t* wb = wcol + (size_t)sb * Q4K_BYTES;
-        const uint4 hdr = *(const uint4*)wb;
-        uint4 raw[4];
+        uint4 hdr[NT], raw[NT][4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) raw[c] = *(const uint4*)(wb + 16 + 32 * c + 16 * h);
+        for (int b = 0; b < NT; b++) {
+            const uint8_t* wb = wcol[b] + (size_t)sb * Q4K_BYTES;
+            hdr[b] = *(const uint4*)wb;
+#pragma unroll
+            for (int c = 0; c < 4; c++) raw[b][c] = *(const uint4*)(wb + 16 + 32 * c + 16 * h);
+        }
         // activations one step ahead of the MFMAs that use them (all four
         // steps at once measured slower: the registers cost waves)
-        auto load_a = [&](int c, v8h (&av)[MT][4]) {
+        auto load_a = [&](int c, v8h (&av)[4]) {
 #pragma unroll
-            for (int a = 0; a < MT; a++)
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++)
-                    av[a][kk] = *(const v8h*)(x16 + (size_t)arow[a] * k + 256 * sb + 64 * c + 8 * x_piece(kk, h));
+            for (int kk = 0; kk < 4; kk++)
+                av[kk] = *(const v8h*)(x16 + (size_t)arow * k + 256 * sb + 64 * c + 8 * x_piece(kk, h));
         };
-        v8h av[MT][4];
+        v8h av[4];
         load_a(0, av);
-        v16f acc[MT];
+        v16f acc[NT];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            v8h avn[MT][4];
+            v8h avn[4];
             if (c < 3) load_a(c + 1, avn);
             __builtin_amdgcn_sched_barrier(0);
-            const BScale bs = bscale(hdr, c);
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const v8h b = build_kk(raw[c], bs, kk);
+            for (int b = 0; b < NT; b++) {
+                const BScale bs = bscale(hdr[b], c);
 #pragma unroll
-                for (int a = 0; a < MT; a++) {
+                for (int kk = 0; kk < 4; kk++) {
+                    const v8h bw = build_kk(raw[b][c], bs, kk);
                     if (c == 0 && kk == 0) {
                         const v16f z = {};
-                        acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], b, z, 0, 0, 0);
+                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[kk], bw, z, 0, 0, 0);
                     } else {
-                        acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a][kk], b, acc[a], 0, 0, 0);
+                        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[kk], bw, acc[b], 0, 0, 0);
                     }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
             if (c < 3) {
 #pragma unroll
-                for (int a = 0; a < MT; a++)
-#pragma unroll
-                    for (int kk = 0; kk < 4; kk++) av[a][kk] = avn[a][kk];
+                for (int kk = 0; kk < 4; kk++) av[kk] = avn[kk];
             }
         }
         // superblock epilogue: min term on MFMA, then out += dy (d D - dmin Dmin)
-        const float d = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
-        const uint64_t m8 = (uint64_t)(hdr.z & 0x3F3F3F3Fu) |
-                            ((uint64_t)(((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u)) << 32);
-        v8h bmv;
+        const v8h am = *(const v8h*)(amin + ((size_t)arow * nsb + sb) * 16 + 8 * h);
+        float dys[16];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
-            bmv[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
-        }
+        for (int r = 0; r < 16; r++) dys[r] = dyt[(size_t)sb * m + min(m0 + 8 * (r >> 2) + 4 * h + (r & 3), m - 1)];
 #pragma unroll
-        for (int a = 0; a < MT; a++) {
-            const v8h am = *(const v8h*)(amin + ((size_t)arow[a] * nsb + sb) * 16 + 8 * h);
+        for (int b = 0; b < NT; b++) {
+            const float d = f16_to_f32(hdr[b].x & 0xffffu), dmin = f16_to_f32(hdr[b].x >> 16);
+            const uint64_t m8 =
+                (uint64_t)(hdr[b].z & 0x3F3F3F3Fu) |
+                ((uint64_t)(((hdr[b].w >> 4) & 0x0F0F0F0Fu) | ((hdr[b].z >> 2) & 0x30303030u)) << 32);
+            v8h bmv;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
+                bmv[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
+            }
             const v16f z = {};
             const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bmv, z, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = min(m0 + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3), m - 1);
-                const float dy = dyt[(size_t)sb * m + row];
-                out[a][r] = __builtin_fmaf(dy, __builtin_fmaf(d, acc[a][r], -(dmin * dm[r])), out[a][r]);
-            }
+            for (int r = 0; r < 16; r++)
+                out[b][r] = __builtin_fmaf(dys[r], __builtin_fmaf(d, acc[b][r], -(dmin * dm[r])), out[b][r]);
         }
     }
     if constexpr (KS > 1) {
         if (wave) {
 #pragma unroll
-            for (int a = 0; a < MT; a++)
+            for (int b = 0; b < NT; b++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) part[wave - 1][a][r][lane] = out[a][r];
+                for (int r = 0; r < 16; r++) part[wave - 1][b][r][lane] = out[b][r];
         }
         __syncthreads();
         if (wave) return;
 #pragma unroll
         for (int w = 0; w < KS - 1; w++)
 #pragma unroll
-            for (int a = 0; a < MT; a++)
+            for (int b = 0; b < NT; b++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) out[a][r] += part[w][a][r][lane];
+                for (int r = 0; r < 16; r++) out[b][r] += part[w][b][r][lane];
     }
-    const int col = n0 + c32;
-    if (col < n) {
 #pragma unroll
-        for (int a = 0; a < MT; a++)
+    for (int b = 0; b < NT; b++) {
+        const int col = n0 + 32 * b + c32;
+        if (col < n) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = m0 + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < m) store_epi(&Y[(int64_t)row * n + col], out[a][r], epi);
+                const int row = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < m) store_epi(&Y[(int64_t)row * n + col], out[b][r], epi);
             }
+        }
     }
 }
 
@@ -1038,14 +1041,25 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                            p.dyt, (int)m, (int)k);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((m + 31) / 32));
-        // one 32-row tile a workgroup (two measured slower: registers)
-        if (k >= 8 * 256)
-            hipLaunchKernelGGL((k_gemm_q4k_skinny<8, 1>), grid, dim3(512), 0, s, (const uint8_t*)w, p.x16, p.amin,
-                               p.dyt, y, (int)m, (int)n, (int)k, epi);
+        // NT column tiles a workgroup: as many as keep ~256 workgroups
+        // (each activation operand then serves NT tiles); K split over 8
+        // waves with one tile, 4 with more (their registers)
+        const int64_t layers = (m + 31) / 32, ctiles = (n + 31) / 32;
+        const int nt = ctiles * layers >= 4 * 256 ? 4 : ctiles * layers >= 2 * 256 ? 2 : 1;
+        const dim3 grid((unsigned)((ctiles + nt - 1) / nt), (unsigned)layers);
+        const uint8_t* wb = (const uint8_t*)w;
+        if (nt == 4)
+            hipLaunchKernelGGL((k_gemm_q4k_skinny<4, 4>), grid, dim3(256), 0, s, wb, p.x16, p.amin, p.dyt, y, (int)m,
+                               (int)n, (int)k, epi);
+        else if (nt == 2)
+            hipLaunchKernelGGL((k_gemm_q4k_skinny<4, 2>), grid, dim3(256), 0, s, wb, p.x16, p.amin, p.dyt, y, (int)m,
+                               (int)n, (int)k, epi);
+        else if (k >= 8 * 256)
+            hipLaunchKernelGGL((k_gemm_q4k_skinny<8, 1>), grid, dim3(512), 0, s, wb, p.x16, p.amin, p.dyt, y, (int)m,
+                               (int)n, (int)k, epi);
         else
-            hipLaunchKernelGGL((k_gemm_q4k_skinny<4, 1>), grid, dim3(256), 0, s, (const uint8_t*)w, p.x16, p.amin,
-                               p.dyt, y, (int)m, (int)n, (int)k, epi);
+            hipLaunchKernelGGL((k_gemm_q4k_skinny<4, 1>), grid, dim3(256), 0, s, wb, p.x16, p.amin, p.dyt, y, (int)m,
+                               (int)n, (int)k, epi);
         return hipGetLastError();
     }
     if (use_mq(type, m)) return launch_mq(type, w, x, y, n, k, m, qbuf, epi, s);
