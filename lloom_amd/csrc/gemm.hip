@@ -515,14 +515,14 @@ __device__ __forceinline__ uint2 nib4_to_h(uint32_t w, h2 sc, h2 off) {
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
 }
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
-                 "s"(__builtin_amdgcn_readfirstlane(lds))
+// From a wave-uniform base (SGPRs) plus a 32-bit per-lane offset, to a
+// wave-uniform LDS destination: the per-step address arithmetic is scalar.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
                  : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
-                 "s"(__builtin_amdgcn_readfirstlane(lds))
+__device__ __forceinline__ void dma4s(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
                  : "memory", "m0");
 }
 
@@ -600,30 +600,37 @@ __global__ __launch_bounds__(64 * WV) void k_gemm_q4k_x16(const uint8_t* __restr
         soff[i] = (uint32_t)min(m0 + 32 * min(C::S_PER_WAVE * wave + i, C::S_CHUNKS - 1) + (lane >> 1), m - 1) *
                       (uint32_t)nsb * 32u +
                   16u * (lane & 1);
-    const int dyrow = min(m0 + 64 * wave + lane, m - 1);
+    const uint32_t dyoff = (uint32_t)min(m0 + 64 * wave + lane, m - 1) * 4u;
+    // the wave index as a scalar: the DMA destinations are then SGPR math
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds0 = lds_addr(smem);
+    uint32_t colwh[C::R_PER_WAVE];  // the lane's half (16 h) of the step's 32 bytes
+#pragma unroll
+    for (int i = 0; i < C::R_PER_WAVE; i++) colwh[i] = colw[i] + 16u * (uint32_t)h;
 
     auto issue_a = [&](int src, int dst) {
-        uint8_t* A = smem + (dst % C::A_STAGES) * C::A_BYTES;
+        const uint32_t A = lds0 + (dst % C::A_STAGES) * C::A_BYTES;
         const uint8_t* ab = (const uint8_t*)x16 + (uint32_t)src * (C::BK * 2);
 #pragma unroll
-        for (int i = 0; i < C::A_PER_WAVE; i++) dma16(ab + aoff[i], lds_addr(A + 1024 * (wave * C::A_PER_WAVE + i)));
+        for (int i = 0; i < C::A_PER_WAVE; i++) dma16s(ab, aoff[i], A + 1024 * (wv * C::A_PER_WAVE + i));
     };
     auto issue_raw = [&](int src, int dst) {
-        uint8_t* R = smem + C::R_OFF + (dst % C::R_SLOTS) * C::R_BYTES;
-        const uint8_t* rb = W + (uint32_t)(src >> 2) * Q4K_BYTES + 32u * (src & 3) + 16u + 16u * (uint32_t)h;
+        const uint32_t R = lds0 + C::R_OFF + (dst % C::R_SLOTS) * C::R_BYTES;
+        const uint8_t* rb = W + (uint32_t)(src >> 2) * Q4K_BYTES + 32u * (src & 3) + 16u;
 #pragma unroll
-        for (int i = 0; i < C::R_PER_WAVE; i++) dma16(rb + colw[i], lds_addr(R + 1024 * (C::R_PER_WAVE * wave + i)));
+        for (int i = 0; i < C::R_PER_WAVE; i++) dma16s(rb, colwh[i], R + 1024 * (C::R_PER_WAVE * wv + i));
     };
     auto issue_sb = [&](int sb) {
-        uint8_t* SB = smem + C::SB_OFF + (sb & 1) * C::SB_BYTES;
+        const uint32_t SB = lds0 + C::SB_OFF + (sb & 1) * C::SB_BYTES;
 #pragma unroll
         for (int i = 0; i < C::S_PER_WAVE; i++)
-            dma16((const uint8_t*)amin + (uint32_t)sb * 32u + soff[i],
-                  lds_addr(SB + C::SB_AMIN + 1024 * min(C::S_PER_WAVE * wave + i, C::S_CHUNKS)));
-        dma4(dyt + (int64_t)sb * m + dyrow, lds_addr(SB + C::SB_DY + 256 * wave));
+            dma16s((const uint8_t*)amin + (uint32_t)sb * 32u, soff[i],
+                   SB + C::SB_AMIN + 1024 * min(C::S_PER_WAVE * wv + i, C::S_CHUNKS));
+        dma4s(dyt + (int64_t)sb * m, dyoff, SB + C::SB_DY + 256 * wv);
+        const uint8_t* hb = W + (uint32_t)sb * Q4K_BYTES;
 #pragma unroll
         for (int i = 0; i < C::R_PER_WAVE; i++)
-            dma16(W + (uint32_t)sb * Q4K_BYTES + colw[i], lds_addr(SB + C::SB_HDR + 1024 * (C::R_PER_WAVE * wave + i)));
+            dma16s(hb, colw[i], SB + C::SB_HDR + 1024 * (C::R_PER_WAVE * wv + i));
     };
     auto read_raw = [&](int step, uint4 (&r)[C::NT]) {
         const uint8_t* R = smem + C::R_OFF + (step % C::R_SLOTS) * C::R_BYTES;
@@ -711,12 +718,12 @@ __global__ __launch_bounds__(64 * WV) void k_gemm_q4k_x16(const uint8_t* __restr
                 //    into step s - 1's slot, in that order
                 if (kk == 0 && c == 0) issue_sb(min(sb + 1, nsb - 1));
                 {
-                    uint8_t* Ad = smem + ((s + 2) % C::A_STAGES) * C::A_BYTES;
+                    const uint32_t Ad = lds0 + ((s + 2) % C::A_STAGES) * C::A_BYTES;
                     const uint8_t* ab = (const uint8_t*)x16 + (uint32_t)min(s + 2, nsteps - 1) * (C::BK * 2);
 #pragma unroll
                     for (int i = 0; i < C::A_PER_WAVE; i++)
                         if (i * 4 / C::A_PER_WAVE == kk)  // compile-time
-                            dma16(ab + aoff[i], lds_addr(Ad + 1024 * (wave * C::A_PER_WAVE + i)));
+                            dma16s(ab, aoff[i], Ad + 1024 * (wv * C::A_PER_WAVE + i));
                 }
                 if (kk == 3) issue_raw(min(s + 3, nsteps - 1), s + 3);
                 // the reads above stay ahead of this slice's MFMAs (the
