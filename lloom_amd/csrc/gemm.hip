@@ -538,17 +538,37 @@ __device__ __forceinline__ int x_piece(int kk, int h) { return (kk & 1) + 4 * (k
 struct BScale {
     h2 scl, sch, offl, offh;
 };
+// (c is a compile-time step index at every call.)  The pair's two 6-bit
+// scales go under the fp16 exponent byte 0x64 by one v_perm_b32 (1024 + sc,
+// exact) and one packed subtract leaves [sc0, sc1]; the halves are then
+// broadcast into the packed fma's operands.
 __device__ __forceinline__ BScale bscale(const uint4& hdr, int c) {
-    const uint64_t sc8 = (uint64_t)(hdr.y & 0x3F3F3F3Fu) |
-                         ((uint64_t)((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u)) << 32);
-    const uint32_t scp = (uint32_t)(sc8 >> (16 * c));
-    const _Float16 s0 = (_Float16)(float)(scp & 0xffu), s1 = (_Float16)(float)((scp >> 8) & 0xffu);
+    const uint32_t w = c < 2 ? (hdr.y & 0x3F3F3F3Fu) : ((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u));
+    const uint32_t sel = (c & 1) ? 0x04030402u : 0x04010400u;  // bytes 2(c&1), 2(c&1)+1
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const h2 p = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, sel)) - k1024;
+    const h2 o = p * (_Float16)(-1024.0f);
     BScale b;
-    b.scl = h2{s0, s0};
-    b.sch = h2{s1, s1};
-    b.offl = h2{(_Float16)(-1024.0f) * s0, (_Float16)(-1024.0f) * s0};
-    b.offh = h2{(_Float16)(-1024.0f) * s1, (_Float16)(-1024.0f) * s1};
+    b.scl = __builtin_shufflevector(p, p, 0, 0);
+    b.sch = __builtin_shufflevector(p, p, 1, 1);
+    b.offl = __builtin_shufflevector(o, o, 0, 0);
+    b.offh = __builtin_shufflevector(o, o, 1, 1);
     return b;
+}
+// The min-term weight operand of a column (lane half h): its eight 6-bit
+// mins m_j as fp16, times 64 for h = 0 (the operand pairs them with the
+// activation sums' S_hi, then S_lo), by the same v_perm_b32 exponent trick.
+__device__ __forceinline__ v8h bmins(const uint4& hdr, int h) {
+    const uint32_t ml = hdr.z & 0x3F3F3F3Fu, mh = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const _Float16 f = h == 0 ? (_Float16)64.0f : (_Float16)1.0f;
+    const h2 fs = {f, f};
+    const h2 p0 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, ml, 0x04010400u)) - k1024) * fs;
+    const h2 p1 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, ml, 0x04030402u)) - k1024) * fs;
+    const h2 p2 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, mh, 0x04010400u)) - k1024) * fs;
+    const h2 p3 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, mh, 0x04030402u)) - k1024) * fs;
+    return __builtin_bit_cast(v8h, make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                              __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)));
 }
 __device__ __forceinline__ v8h build_kk(const uint4& raw, const BScale& bs, int kk) {
     const uint32_t w0 = kk & 1 ? raw.z : raw.x, w1 = kk & 1 ? raw.w : raw.y;
@@ -777,15 +797,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemm_q4k_x16(const uint8_t* __restr
                 for (int b = 0; b < C::NT; b++) {
                     // this lane's column: d, dmin and the mins as [64 m | m]
                     const float d = f16_to_f32(hdr[b].x & 0xffffu), dmin = f16_to_f32(hdr[b].x >> 16);
-                    const uint64_t m8 =
-                        (uint64_t)(hdr[b].z & 0x3F3F3F3Fu) |
-                        ((uint64_t)(((hdr[b].w >> 4) & 0x0F0F0F0Fu) | ((hdr[b].z >> 2) & 0x30303030u)) << 32);
-                    v8h bmv;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
-                        bmv[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
-                    }
+                    const v8h bmv = bmins(hdr[b], h);
 #pragma unroll
                     for (int a = 0; a < MT; a++) {
                         const int row = wm * (32 * MT) + a * 32 + c32;
@@ -921,15 +933,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemm_q4k_skinny(const uint8_t* __re
 #pragma unroll
         for (int b = 0; b < NT; b++) {
             const float d = f16_to_f32(hdr[b].x & 0xffffu), dmin = f16_to_f32(hdr[b].x >> 16);
-            const uint64_t m8 =
-                (uint64_t)(hdr[b].z & 0x3F3F3F3Fu) |
-                ((uint64_t)(((hdr[b].w >> 4) & 0x0F0F0F0Fu) | ((hdr[b].z >> 2) & 0x30303030u)) << 32);
-            v8h bmv;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float mj = (float)(uint32_t)((m8 >> (8 * j)) & 0x3fu);
-                bmv[j] = (_Float16)(h == 0 ? 64.0f * mj : mj);
-            }
+            const v8h bmv = bmins(hdr[b], h);
             const v16f z = {};
             const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bmv, z, 0, 0, 0);
 #pragma unroll
