@@ -6,8 +6,8 @@ configs[1]: x f32 [B, 2048] ~N(0,1) for B in {1,2,4,8,16}, W [6144, 2048]
 ~N(0,0.02) quantized to Q4_K.  One "step" is one pass of the sweep (five
 qmatmul calls, each on the next of R distinct weight copies, R * 7.08 MB >=
 512 MB so the 256 MB Infinity Cache cannot hold them).  `value` is the
-algorithmic bytes of the timed steps (weights + x f32 + y f32, as BASELINE.md
-counts them) divided by the timed region, in GB/s.  The launches of the
+algorithmic bytes of the timed steps (weights + x f32 + y f32) divided by the
+timed region, in GB/s.  The launches of the
 timed steps are replayed from one HIP graph (decode launches are a few
 microseconds each; the graph keeps host launch overhead out), bracketed by
 HIP events on the stream they run on.
@@ -111,7 +111,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one "
-                                   "MI355X; the multi-GPU layout is described in DESIGN.md"}))
+                                   "MI355X; the path would shard by weight rows (or experts), one GPU a shard"}))
         sys.exit(2)
     import numpy as np
     import torch

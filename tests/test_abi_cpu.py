@@ -36,7 +36,7 @@ def test_weight_bytes_and_refusals():
 
     packed, alloc = ctypes.c_size_t(), ctypes.c_size_t()
     assert lib().lloom_hip_weight_bytes(12, 6144, 2048, ctypes.byref(packed), ctypes.byref(alloc)) == 0
-    assert packed.value == 7077888 and alloc.value > packed.value  # SURVEY/BASELINE figure
+    assert packed.value == 7077888 and alloc.value > packed.value  # W [6144, 2048] Q4_K: 6144 rows x 8 superblocks x 144 B
     assert lib().lloom_hip_weight_bytes(8, 8192, 2048, ctypes.byref(packed), ctypes.byref(alloc)) == 0
     assert packed.value == 17825792
     assert lib().lloom_hip_weight_bytes(14, 2048, 8192, ctypes.byref(packed), ctypes.byref(alloc)) == 0
