@@ -26,33 +26,16 @@
 //   B (weights):     lane l holds q[n = l%32][32j + 16(l/32) + 0..15]
 //   D:               lane l, reg r holds D[m = 8(r/4) + 4(l/32) + r%4][n = l%32]
 #include <cstdlib>
+#include <type_traits>
 
 #include "kq_common.hpp"
 #include "kq_quant.hpp"
 #include "kernels.hpp"
+#include "kq_gemm.hpp"
 
 namespace lloom {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-// Tile order.  Workgroups are dealt round-robin to the 8 XCDs; renumber them
-// XCD-major so each XCD gets a contiguous range, then walk that range in
-// groups of GM m-blocks (column-major inside a group): the ~32 workgroups an
-// XCD runs at once cover a 4 x 8 block of tiles whose activation and weight
-// tiles fit its 4 MB L2, instead of re-reading them for every tile.
-__device__ __forceinline__ void tile_of(int nbm, int nbn, int& bm, int& bn) {
-    constexpr int GM = 4;
-    int pid = blockIdx.x;
-    if ((gridDim.x & 7) == 0) pid = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
-    const int per_group = GM * nbn;
-    const int group = pid / per_group;
-    const int first = group * GM;
-    const int gsz = min(nbm - first, GM);
-    const int in = pid - group * per_group;
-    bm = first + in % gsz;
-    bn = in / gsz;
-}
 
 // --------------------------------------------------- activation prep --
 // Q8_K of every (row, superblock) block, bit-exact, into:
@@ -505,25 +488,6 @@ __device__ __forceinline__ uint2 nib4_to_h(uint32_t w, h2 sc, h2 off) {
     const h2 ve = __builtin_elementwise_fma(__builtin_bit_cast(h2, e), sc, off);
     const h2 vo = __builtin_elementwise_fma(__builtin_bit_cast(h2, o), sc, off);
     return make_uint2(__builtin_bit_cast(uint32_t, ve), __builtin_bit_cast(uint32_t, vo));
-}
-
-// global_load_lds written as the instruction: the compiler does not see
-// these LDS writes, so it adds no vmcnt(0) in front of later LDS reads it
-// cannot prove disjoint from them; the kernel orders them itself (counted
-// vmcnt waits, then s_barrier).  m0 holds the wave's LDS destination and is
-// set right before each load; nothing else in the kernel uses m0.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
-}
-// From a wave-uniform base (SGPRs) plus a 32-bit per-lane offset, to a
-// wave-uniform LDS destination: the per-step address arithmetic is scalar.
-__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma4s(const void* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-                 : "memory", "m0");
 }
 
 // MFMA slice kk of a step, lane half h: piece (kk & 1) + 4 (kk >> 1) + 2h,
@@ -993,10 +957,12 @@ static int64_t mq_max_rows() {
 
 static bool use_mq(int type, int64_t m) { return type == T_Q6K || (type == T_Q4K && m <= mq_max_rows()); }
 
+
 static int64_t skinny_max_rows();
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode) {
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(0, k, m) && mode != GEMM_INT8) return x16_bytes(m, k);
     if (use_mq(type, m)) return split_q8k_bytes(k, m);
+    if (type == T_Q8_0 && q8_gemm_fits(n, k, m)) return q8_gemm_workspace_bytes(m, k);
     if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
     return matvec_workspace_bytes(type, n, k, 16);
 }
@@ -1113,6 +1079,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                            y, (int)m, (int)n, (int)k, epi);
         return hipGetLastError();
     }
+    if (type == T_Q8_0 && q8_gemm_fits(n, k, m)) return launch_q8_gemm(w, x, y, n, k, m, qbuf, epi, s);
     // Q8_0 (and Q4_K past 32-bit offsets): tiles of 16 activation rows
     // through the decode kernels
     for (int64_t r = 0; r < m; r += 16) {

@@ -1,0 +1,288 @@
+// gemm_q8.hip -- Q8_0 prefill-shaped matmul (m > 16 activation rows) on
+// int8 MFMA.  Built with the MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
+// every result is read by the VALU epilogue right away, and from AGPRs each
+// read would cost one more instruction.
+#include <cstdlib>
+#include <type_traits>
+
+#include "kq_common.hpp"
+#include "kq_gemm.hpp"
+#include "kq_quant.hpp"
+#include "kernels.hpp"
+
+namespace lloom {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------ Q8_0 GEMM ----
+// y[m, n] = sum_b (sum_{k in b} x8[m,k] w8[n,k]) * dx[m,b] * dw[n,b] over
+// 32-element blocks b: k_quants' Q8_0 x Q8_0 dot (vec_dot_unopt,
+// k_quants.rs:800-818) with the activations quantized by
+// BlockQ8_0::from_float (k_quants.rs:738-767) and both scales taken as
+// f32(f16 d), as the reference does.  One v_mfma_i32_32x32x32_i8 is one block
+// of one 32 x 32 tile (its K is the block's 32), so every block's integer sum
+// is exact and the scales apply per block in f32: out += f32(S) * (dx * dw),
+// three VALU instructions per output and block, which bound this kernel
+// (the MFMAs take a sixth of that time).
+//
+// Activation prep (bit-exact Q8_0, the weights' own block layout stays):
+//   xq  int8 [m][k]
+//   dxt f32  [k/32][mp]   mp = m rounded up to 4, then 128 floats of pad
+struct Q8Ptrs {
+    int8_t* xq;
+    float* dxt;
+    int64_t mp;
+};
+
+static Q8Ptrs q8_ptrs(void* base, int64_t m, int64_t k) {
+    Q8Ptrs p;
+    p.xq = (int8_t*)base;
+    p.dxt = (float*)((uint8_t*)base + (((size_t)m * k + 255) & ~(size_t)255));
+    p.mp = (m + 3) & ~(int64_t)3;
+    return p;
+}
+
+size_t q8_gemm_workspace_bytes(int64_t m, int64_t k) {
+    const int64_t mp = (m + 3) & ~(int64_t)3;
+    return (((size_t)m * k + 255) & ~(size_t)255) + ((size_t)(k / 32) * mp + 128) * sizeof(float);
+}
+
+// One wave a (row, 256 elements): eight blocks of eight lanes.
+__global__ __launch_bounds__(256) void k_gemm_prep_q8_0(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                        float* __restrict__ dxt, int m, int k, int mp) {
+    const int lane = threadIdx.x & 63;
+    const int nc = k >> 8;
+    const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (c >= (int64_t)m * nc) return;
+    const int mi = (int)(c / nc), cc = (int)(c - (int64_t)mi * nc);
+    const int64_t off = (int64_t)mi * k + 256 * cc + 4 * lane;
+    const float4 v = *(const float4*)(x + off);
+    uint16_t d16;
+    const uint32_t q = q8_0_block_8lanes(v, &d16);
+    *(uint32_t*)(xq + off) = q;
+    if ((lane & 7) == 0) dxt[(int64_t)(8 * cc + (lane >> 3)) * mp + mi] = f16_to_f32(d16);
+}
+
+// Tiling: 2 x WN waves (WN 2 or 4: one or two a SIMD), a 128 x 128 block of
+// y, each wave 64 rows x 128 / WN columns (2 x 4 / WN tiles of 32 x 32).  K moves in steps of 256 (eight blocks, 272 weight
+// bytes a row: 16-byte aligned, as a row of blocks is 2176 bytes), one LDS
+// stage a step, double buffered, every byte by global_load_lds:
+//   A  [128][256] int8, piece p (16 B) of row r at p ^ (r & 7)
+//   B  [128][272] the raw Q8_0 bytes of the step (17 pieces a row; odd, so
+//      eight consecutive rows reading one piece hit eight bank groups)
+//   DX [8][128] f32, the step's activation scales
+// MFMA operands (the same k-set for A and B in a lane): lane l holds row
+// (or column) l % 32, elements 16 (l / 32) .. +15 of the block.  A block's
+// 32 quants start 2 bytes into its 34, so a lane reads the aligned 32-byte
+// window around its 16 bytes and shifts them out with v_alignbyte.
+constexpr int Q8G_BM = 128, Q8G_BN = 128;
+constexpr int Q8G_A = Q8G_BM * 256;                  // 32768
+constexpr int Q8G_B = Q8G_BN * 272;                  // 34816
+constexpr int Q8G_DX = 8 * Q8G_BM * 4;               // 4096
+constexpr int Q8G_STAGE = Q8G_A + Q8G_B + Q8G_DX;    // 71680
+constexpr int Q8G_LDS = 2 * Q8G_STAGE;               // 143360
+constexpr int Q8G_B_CHUNKS = Q8G_B / 1024;           // 34
+
+// The lane's 16 quants of block j (h: which half) from row base rb (LDS),
+// a 16-byte-aligned window: the block's quants start at 34 j + 2.
+template <int J>
+__device__ __forceinline__ v4i q8_operand(const uint8_t* rb, int h) {
+    constexpr int START = 34 * J + 2, BASE = START & ~15, SH = START - BASE, Q = SH >> 2, R = SH & 3;
+    const uint8_t* p = rb + BASE + 16 * h;
+    const uint4 lo = *(const uint4*)p;
+    if constexpr (SH == 0) {
+        return __builtin_bit_cast(v4i, lo);
+    } else {
+        const uint4 hi = *(const uint4*)(p + 16);
+        const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        v4i r;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            r[i] = R == 0 ? (int)w[Q + i] : (int)__builtin_amdgcn_alignbyte(w[Q + i + 1], w[Q + i], R);
+        return r;
+    }
+}
+
+template <int WN>
+__global__ __launch_bounds__(128 * WN) void k_gemm_q8_0(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                   const float* __restrict__ dxt, float* __restrict__ Y, int m, int n,
+                                                   int k, int mp, int epi) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    constexpr int WAVES = 2 * WN, NT = 4 / WN;
+    constexpr int A_PER_WAVE = Q8G_A / 1024 / WAVES;
+    constexpr int B_PER_WAVE = (Q8G_B_CHUNKS + WAVES - 1) / WAVES;  // the last of some waves repeats a chunk
+    const int wm = wave / WN, wn = wave % WN;
+    const int h = lane >> 5, c32 = lane & 31;
+    int bm, bn;
+    tile_of((m + Q8G_BM - 1) / Q8G_BM, (n + Q8G_BN - 1) / Q8G_BN, bm, bn);
+    const int m0 = bm * Q8G_BM, n0 = bn * Q8G_BN;
+    const int nsteps = k >> 8;
+    const uint32_t rowbytes = (uint32_t)(k / 32) * Q8_0_BYTES;
+
+    // per-lane byte offsets of this wave's DMA share, fixed for the K loop
+    uint32_t aoff[A_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < A_PER_WAVE; i++) {
+        const int q = wave * A_PER_WAVE + i;
+        const int row = 4 * q + (lane >> 4);
+        const int piece = (lane & 15) ^ (row & 7);
+        aoff[i] = (uint32_t)min(m0 + row, m - 1) * (uint32_t)k + 16u * piece;
+    }
+    uint32_t boff[B_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < B_PER_WAVE; i++) {
+        const int q = min(wave + WAVES * i, Q8G_B_CHUNKS - 1);
+        const int pc = 64 * q + lane;
+        const int row = pc / 17, piece = pc - row * 17;
+        boff[i] = (uint32_t)min(n0 + row, n - 1) * rowbytes + 16u * piece;
+    }
+    // DX: wave w < 4 moves blocks 2w, 2w + 1 of the step, 128 rows each
+    const uint32_t dxoff = ((uint32_t)(2 * (wave & 3) + (lane >> 5)) * (uint32_t)mp + (uint32_t)(m0 + 4 * c32)) * 4u;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds0 = lds_addr(smem);
+
+    auto issue = [&](int s) {
+        const uint32_t st = lds0 + (s & 1) * Q8G_STAGE;
+        const uint8_t* ab = (const uint8_t*)xq + (uint32_t)s * 256u;
+#pragma unroll
+        for (int i = 0; i < A_PER_WAVE; i++) dma16s(ab, aoff[i], st + 1024 * (wv * A_PER_WAVE + i));
+        const uint8_t* bb = W + (uint32_t)s * 272u;
+#pragma unroll
+        for (int i = 0; i < B_PER_WAVE; i++)
+            dma16s(bb, boff[i], st + Q8G_A + 1024 * min(wv + WAVES * i, Q8G_B_CHUNKS - 1));
+        if (wv < 4) dma16s((const uint8_t*)(dxt + (int64_t)s * 8 * mp), dxoff, st + Q8G_A + Q8G_B + 1024 * wv);
+    };
+
+    float out[2][NT][16];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < NT; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
+
+    issue(0);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+
+    for (int s = 0; s < nsteps; s++) {
+        // the next step into the other stage (its readers passed the last
+        // barrier); a step past the end reloads the last one, unread
+        issue(min(s + 1, nsteps - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* A = smem + (s & 1) * Q8G_STAGE;
+        const uint8_t* B = A + Q8G_A;
+        const float* DX = (const float*)(B + Q8G_B);
+        const uint8_t* brow[NT];
+#pragma unroll
+        for (int b = 0; b < NT; b++) brow[b] = B + (wn * 32 * NT + b * 32 + c32) * 272;
+        auto block = [&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            v4i av[2], bv[NT];
+            float dw[NT];
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                const int row = wm * 64 + a * 32 + c32;
+                av[a] = *(const v4i*)(A + row * 256 + 16 * ((2 * j + h) ^ (row & 7)));
+            }
+#pragma unroll
+            for (int b = 0; b < NT; b++) {
+                bv[b] = q8_operand<j>(brow[b], h);
+                dw[b] = f16_to_f32(*(const uint16_t*)(brow[b] + 34 * j));
+            }
+            v16i d[2][NT];
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < NT; b++) {
+                    const v16i z = {};
+                    d[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bv[b], z, 0, 0, 0);
+                }
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                const float* dxp = DX + j * Q8G_BM + wm * 64 + a * 32 + 4 * h;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 d4 = *(const float4*)(dxp + 8 * g);
+                    const float dxs[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int r = 4 * g + u;
+#pragma unroll
+                        for (int b = 0; b < NT; b++)
+                            out[a][b][r] = __builtin_fmaf((float)d[a][b][r], dxs[u] * dw[b], out[a][b][r]);
+                    }
+                }
+            }
+        };
+        block(std::integral_constant<int, 0>{});
+        block(std::integral_constant<int, 1>{});
+        block(std::integral_constant<int, 2>{});
+        block(std::integral_constant<int, 3>{});
+        block(std::integral_constant<int, 4>{});
+        block(std::integral_constant<int, 5>{});
+        block(std::integral_constant<int, 6>{});
+        block(std::integral_constant<int, 7>{});
+        // the next step has landed (this wave's share) and every wave is
+        // done reading this one
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+    }
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < NT; b++) {
+            const int col = n0 + wn * 32 * NT + b * 32 + c32;
+            if (col >= n) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < m) {
+                    if (epi == EPI_STORE) Y[(int64_t)row * n + col] = out[a][b][r];
+                    else store_epi_slow(&Y[(int64_t)row * n + col], out[a][b][r], epi);
+                }
+            }
+        }
+}
+
+
+// K in whole 256-element steps and 32-bit DMA offsets.
+bool q8_gemm_fits(int64_t n, int64_t k, int64_t m) {
+    return k % 256 == 0 && n * (k / 32) * Q8_0_BYTES < ((int64_t)1 << 32) && m * k < ((int64_t)1 << 32);
+}
+
+hipError_t launch_q8_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
+                          int epi, hipStream_t s) {
+    static const int wn = [] {
+        const char* e = getenv("LLOOM_HIP_Q8_WN");
+        return e && atoi(e) == 2 ? 2 : 4;
+    }();
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e =
+            hipFuncSetAttribute((const void*)k_gemm_q8_0<2>, hipFuncAttributeMaxDynamicSharedMemorySize, Q8G_LDS);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_gemm_q8_0<4>, hipFuncAttributeMaxDynamicSharedMemorySize, Q8G_LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const Q8Ptrs p = q8_ptrs(qbuf, m, k);
+    const int64_t nc = m * (k / 256);
+    hipLaunchKernelGGL(k_gemm_prep_q8_0, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, s, x, p.xq, p.dxt, (int)m,
+                       (int)k, (int)p.mp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const unsigned grid = (unsigned)(((m + Q8G_BM - 1) / Q8G_BM) * ((n + Q8G_BN - 1) / Q8G_BN));
+    if (wn == 2)
+        hipLaunchKernelGGL(k_gemm_q8_0<2>, dim3(grid), dim3(256), Q8G_LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
+                           (int)m, (int)n, (int)k, (int)p.mp, epi);
+    else
+        hipLaunchKernelGGL(k_gemm_q8_0<4>, dim3(grid), dim3(512), Q8G_LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
+                           (int)m, (int)n, (int)k, (int)p.mp, epi);
+    return hipGetLastError();
+}
+
+}  // namespace lloom

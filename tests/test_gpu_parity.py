@@ -161,6 +161,40 @@ def test_prefill_gemm_q4k_shapes(L, m, n, k, mma):
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"gemm {mma} m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 96), (300, 70, 160)])
+def test_prefill_gemm_q8_0_shapes(L, m, n, k):
+    """The Q8_0 prefill GEMM (K in whole 256-element steps) on ragged tiles,
+    an all-zero activation block and a block holding one huge value; K
+    not a multiple of 256 takes the 16-row decode tiles instead."""
+    rng = np.random.default_rng(m * 5 + n)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[min(3, n - 1), :32] *= 50.0  # one weight block with a much larger scale
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1, :32] = 0.0  # an all-zero activation block (d = 0)
+    x[min(2, m - 1), 37] = 1e4
+    y, q = _qmm(L, O.Q8_0, w, x)
+    assert_rows_close(y, O.matmul(O.Q8_0, x, q, n), what=f"q8_0 gemm m={m} n={n} k={k}")
+
+
+def test_prefill_gemm_q8_0_epilogues(L):
+    """SiLU and multiply-into stores on the Q8_0 GEMM route."""
+    rng = np.random.default_rng(21)
+    m, n, k = 150, 200, 512
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    g = rng.standard_normal((m, n)).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), O.Q8_0)
+    mm = L.QMatMul.from_qtensor(qt)
+    plain = mm.forward(_cuda(x)).cpu().numpy()
+    want = O.matmul(O.Q8_0, x, qt.data(), n)
+    assert_rows_close(plain, want, what="q8_0 plain")
+    silu = mm.forward_silu(_cuda(x)).cpu().numpy()
+    np.testing.assert_allclose(silu, _silu32(plain), rtol=2e-6, atol=1e-7)
+    gg = _cuda(g)
+    mm.forward_mul_into(_cuda(x), gg)
+    assert np.array_equal(gg.cpu().numpy().view(np.uint32), (g * plain).astype(np.float32).view(np.uint32))
+
+
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
 def test_qmatmul_closed_form_inputs(L, dt):
     """The reference's closed-form GEMM inputs (quantized_tests.rs:1769-1903)."""
