@@ -63,25 +63,39 @@ __global__ __launch_bounds__(256) void k_gemm_prep_q8_0(const float* __restrict_
     if ((lane & 7) == 0) dxt[(int64_t)(8 * cc + (lane >> 3)) * mp + mi] = f16_to_f32(d16);
 }
 
-// Tiling: 2 x WN waves (WN 2 or 4: one or two a SIMD), a 128 x 128 block of
-// y, each wave 64 rows x 128 / WN columns (2 x 4 / WN tiles of 32 x 32).  K moves in steps of 256 (eight blocks, 272 weight
-// bytes a row: 16-byte aligned, as a row of blocks is 2176 bytes), one LDS
-// stage a step, double buffered, every byte by global_load_lds:
-//   A  [128][256] int8, piece p (16 B) of row r at p ^ (r & 7)
-//   B  [128][272] the raw Q8_0 bytes of the step (17 pieces a row; odd, so
+// Tiling: WM x WN waves, each MT x NT tiles of 32 x 32: a BM x BN block of
+// y (BM = 32 WM MT, BN = 32 WN NT).  K moves in steps of 256 (eight blocks,
+// 272 weight bytes a row: 16-byte aligned, as a row of blocks is 2176
+// bytes), one LDS stage a step, a ring of S stages, every byte by
+// global_load_lds:
+//   A  [BM][256] int8, piece p (16 B) of row r at p ^ (r & 7)
+//   B  [BN][272] the raw Q8_0 bytes of the step (17 pieces a row; odd, so
 //      eight consecutive rows reading one piece hit eight bank groups)
-//   DX [8][128] f32, the step's activation scales
+//   DX [8][BM] f32, the step's activation scales
+// Every wave issues the same number of loads a stage (a wave past the
+// last chunk of a part repeats one: the same bytes to the same place), so
+// a counted vmcnt wait before each barrier leaves exactly the later stages
+// in flight.
 // MFMA operands (the same k-set for A and B in a lane): lane l holds row
 // (or column) l % 32, elements 16 (l / 32) .. +15 of the block.  A block's
 // 32 quants start 2 bytes into its 34, so a lane reads the aligned 32-byte
 // window around its 16 bytes and shifts them out with v_alignbyte.
-constexpr int Q8G_BM = 128, Q8G_BN = 128;
-constexpr int Q8G_A = Q8G_BM * 256;                  // 32768
-constexpr int Q8G_B = Q8G_BN * 272;                  // 34816
-constexpr int Q8G_DX = 8 * Q8G_BM * 4;               // 4096
-constexpr int Q8G_STAGE = Q8G_A + Q8G_B + Q8G_DX;    // 71680
-constexpr int Q8G_LDS = 2 * Q8G_STAGE;               // 143360
-constexpr int Q8G_B_CHUNKS = Q8G_B / 1024;           // 34
+template <int WM_, int WN_, int MT_, int NT_, int S_>
+struct Q8Cfg {
+    static constexpr int WM = WM_, WN = WN_, MT = MT_, NT = NT_, S = S_;
+    static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
+    static constexpr int BM = 32 * WM * MT, BN = 32 * WN * NT;
+    static constexpr int A = BM * 256, B = BN * 272, DX = 8 * BM * 4;
+    static constexpr int STAGE = A + B + DX, LDS = S * STAGE;
+    static constexpr int A_CHUNKS = A / 1024, B_CHUNKS = (B + 1023) / 1024, DX_CHUNKS = DX / 1024;
+    static constexpr int A_PER_WAVE = A_CHUNKS / WAVES;
+    static constexpr int B_PER_WAVE = (B_CHUNKS + WAVES - 1) / WAVES;
+    static constexpr int DX_PER_WAVE = (DX_CHUNKS + WAVES - 1) / WAVES;
+    static constexpr int DMA = A_PER_WAVE + B_PER_WAVE + DX_PER_WAVE;  // loads a wave issues a stage
+    static_assert(A_CHUNKS % WAVES == 0 && B % 1024 == 0 && DX % 1024 == 0, "stage parts in whole 1 KB chunks");
+    static_assert((S - 2) * DMA <= 63, "vmcnt counts to 63");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
 
 // The lane's 16 quants of block j (h: which half) from row base rb (LDS),
 // a 16-byte-aligned window: the block's quants start at 34 j + 2.
@@ -103,106 +117,122 @@ __device__ __forceinline__ v4i q8_operand(const uint8_t* rb, int h) {
     }
 }
 
-template <int WN>
-__global__ __launch_bounds__(128 * WN) void k_gemm_q8_0(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
-                                                   const float* __restrict__ dxt, float* __restrict__ Y, int m, int n,
-                                                   int k, int mp, int epi) {
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <class C>
+__global__ __launch_bounds__(C::THREADS) void k_gemm_q8_0(const uint8_t* __restrict__ W,
+                                                            const int8_t* __restrict__ xq,
+                                                            const float* __restrict__ dxt, float* __restrict__ Y,
+                                                            int m, int n, int k, int mp, int epi) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    constexpr int WAVES = 2 * WN, NT = 4 / WN;
-    constexpr int A_PER_WAVE = Q8G_A / 1024 / WAVES;
-    constexpr int B_PER_WAVE = (Q8G_B_CHUNKS + WAVES - 1) / WAVES;  // the last of some waves repeats a chunk
-    const int wm = wave / WN, wn = wave % WN;
+    const int wm = wave / C::WN, wn = wave % C::WN;
     const int h = lane >> 5, c32 = lane & 31;
     int bm, bn;
-    tile_of((m + Q8G_BM - 1) / Q8G_BM, (n + Q8G_BN - 1) / Q8G_BN, bm, bn);
-    const int m0 = bm * Q8G_BM, n0 = bn * Q8G_BN;
+    tile_of((m + C::BM - 1) / C::BM, (n + C::BN - 1) / C::BN, bm, bn);
+    const int m0 = bm * C::BM, n0 = bn * C::BN;
     const int nsteps = k >> 8;
     const uint32_t rowbytes = (uint32_t)(k / 32) * Q8_0_BYTES;
 
     // per-lane byte offsets of this wave's DMA share, fixed for the K loop
-    uint32_t aoff[A_PER_WAVE];
+    uint32_t aoff[C::A_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < A_PER_WAVE; i++) {
-        const int q = wave * A_PER_WAVE + i;
+    for (int i = 0; i < C::A_PER_WAVE; i++) {
+        const int q = wave * C::A_PER_WAVE + i;
         const int row = 4 * q + (lane >> 4);
         const int piece = (lane & 15) ^ (row & 7);
         aoff[i] = (uint32_t)min(m0 + row, m - 1) * (uint32_t)k + 16u * piece;
     }
-    uint32_t boff[B_PER_WAVE];
+    uint32_t boff[C::B_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < B_PER_WAVE; i++) {
-        const int q = min(wave + WAVES * i, Q8G_B_CHUNKS - 1);
+    for (int i = 0; i < C::B_PER_WAVE; i++) {
+        const int q = min(wave + C::WAVES * i, C::B_CHUNKS - 1);
         const int pc = 64 * q + lane;
         const int row = pc / 17, piece = pc - row * 17;
         boff[i] = (uint32_t)min(n0 + row, n - 1) * rowbytes + 16u * piece;
     }
-    // DX: wave w < 4 moves blocks 2w, 2w + 1 of the step, 128 rows each
-    const uint32_t dxoff = ((uint32_t)(2 * (wave & 3) + (lane >> 5)) * (uint32_t)mp + (uint32_t)(m0 + 4 * c32)) * 4u;
+    // DX chunk c: BM / 4 lanes a block (four rows each), 256 / BM blocks
+    uint32_t dxoff[C::DX_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < C::DX_PER_WAVE; i++) {
+        constexpr int LPB = C::BM / 4;
+        const int c = min(wave + C::WAVES * i, C::DX_CHUNKS - 1);
+        const int blk = c * (64 / LPB) + lane / LPB;
+        dxoff[i] = ((uint32_t)blk * (uint32_t)mp + (uint32_t)(m0 + 4 * (lane % LPB))) * 4u;
+    }
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t lds0 = lds_addr(smem);
 
-    auto issue = [&](int s) {
-        const uint32_t st = lds0 + (s & 1) * Q8G_STAGE;
+    auto issue = [&](int s, int slot) {
+        const uint32_t st = lds0 + slot * C::STAGE;
         const uint8_t* ab = (const uint8_t*)xq + (uint32_t)s * 256u;
 #pragma unroll
-        for (int i = 0; i < A_PER_WAVE; i++) dma16s(ab, aoff[i], st + 1024 * (wv * A_PER_WAVE + i));
+        for (int i = 0; i < C::A_PER_WAVE; i++) dma16s(ab, aoff[i], st + 1024 * (wv * C::A_PER_WAVE + i));
         const uint8_t* bb = W + (uint32_t)s * 272u;
 #pragma unroll
-        for (int i = 0; i < B_PER_WAVE; i++)
-            dma16s(bb, boff[i], st + Q8G_A + 1024 * min(wv + WAVES * i, Q8G_B_CHUNKS - 1));
-        if (wv < 4) dma16s((const uint8_t*)(dxt + (int64_t)s * 8 * mp), dxoff, st + Q8G_A + Q8G_B + 1024 * wv);
+        for (int i = 0; i < C::B_PER_WAVE; i++)
+            dma16s(bb, boff[i], st + C::A + 1024 * min(wv + C::WAVES * i, C::B_CHUNKS - 1));
+        const uint8_t* db = (const uint8_t*)(dxt + (int64_t)s * 8 * mp);
+#pragma unroll
+        for (int i = 0; i < C::DX_PER_WAVE; i++)
+            dma16s(db, dxoff[i], st + C::A + C::B + 1024 * min(wv + C::WAVES * i, C::DX_CHUNKS - 1));
     };
 
-    float out[2][NT][16];
+    float out[C::MT][C::NT][16];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < C::MT; a++)
 #pragma unroll
-        for (int b = 0; b < NT; b++)
+        for (int b = 0; b < C::NT; b++)
 #pragma unroll
             for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
 
-    issue(0);
+    // prologue: stages 0 .. S-2 (steps past the end reload the last one
+    // into a slot nobody reads, so the counts never change)
+#pragma unroll
+    for (int i = 0; i < C::S - 1; i++) issue(min(i, nsteps - 1), i);
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    vm_wait<(C::S - 2) * C::DMA>();
     __builtin_amdgcn_s_barrier();
 
     for (int s = 0; s < nsteps; s++) {
-        // the next step into the other stage (its readers passed the last
-        // barrier); a step past the end reloads the last one, unread
-        issue(min(s + 1, nsteps - 1));
+        // step s + S - 1 into the slot step s - 1 used (its readers passed
+        // the last barrier)
+        issue(min(s + C::S - 1, nsteps - 1), (s + C::S - 1) % C::S);
         __builtin_amdgcn_sched_barrier(0);
-        const uint8_t* A = smem + (s & 1) * Q8G_STAGE;
-        const uint8_t* B = A + Q8G_A;
-        const float* DX = (const float*)(B + Q8G_B);
-        const uint8_t* brow[NT];
+        const uint8_t* A = smem + (s % C::S) * C::STAGE;
+        const uint8_t* B = A + C::A;
+        const float* DX = (const float*)(B + C::B);
+        const uint8_t* brow[C::NT];
 #pragma unroll
-        for (int b = 0; b < NT; b++) brow[b] = B + (wn * 32 * NT + b * 32 + c32) * 272;
+        for (int b = 0; b < C::NT; b++) brow[b] = B + (wn * 32 * C::NT + b * 32 + c32) * 272;
         auto block = [&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            v4i av[2], bv[NT];
-            float dw[NT];
+            v4i av[C::MT], bv[C::NT];
+            float dw[C::NT];
 #pragma unroll
-            for (int a = 0; a < 2; a++) {
-                const int row = wm * 64 + a * 32 + c32;
+            for (int a = 0; a < C::MT; a++) {
+                const int row = wm * 32 * C::MT + a * 32 + c32;
                 av[a] = *(const v4i*)(A + row * 256 + 16 * ((2 * j + h) ^ (row & 7)));
             }
 #pragma unroll
-            for (int b = 0; b < NT; b++) {
+            for (int b = 0; b < C::NT; b++) {
                 bv[b] = q8_operand<j>(brow[b], h);
                 dw[b] = f16_to_f32(*(const uint16_t*)(brow[b] + 34 * j));
             }
-            v16i d[2][NT];
+            v16i d[C::MT][C::NT];
 #pragma unroll
-            for (int a = 0; a < 2; a++)
+            for (int a = 0; a < C::MT; a++)
 #pragma unroll
-                for (int b = 0; b < NT; b++) {
+                for (int b = 0; b < C::NT; b++) {
                     const v16i z = {};
                     d[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bv[b], z, 0, 0, 0);
                 }
 #pragma unroll
-            for (int a = 0; a < 2; a++) {
-                const float* dxp = DX + j * Q8G_BM + wm * 64 + a * 32 + 4 * h;
+            for (int a = 0; a < C::MT; a++) {
+                const float* dxp = DX + j * C::BM + wm * 32 * C::MT + a * 32 + 4 * h;
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
                     const float4 d4 = *(const float4*)(dxp + 8 * g);
@@ -211,7 +241,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_q8_0(const uint8_t* __restric
                     for (int u = 0; u < 4; u++) {
                         const int r = 4 * g + u;
 #pragma unroll
-                        for (int b = 0; b < NT; b++)
+                        for (int b = 0; b < C::NT; b++)
                             out[a][b][r] = __builtin_fmaf((float)d[a][b][r], dxs[u] * dw[b], out[a][b][r]);
                     }
                 }
@@ -225,21 +255,21 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_q8_0(const uint8_t* __restric
         block(std::integral_constant<int, 5>{});
         block(std::integral_constant<int, 6>{});
         block(std::integral_constant<int, 7>{});
-        // the next step has landed (this wave's share) and every wave is
-        // done reading this one
+        // step s + 1 has landed (this wave's share; S - 2 later stages stay
+        // in flight) and every wave is done reading step s
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        vm_wait<(C::S - 2) * C::DMA>();
         __builtin_amdgcn_s_barrier();
     }
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < C::MT; a++)
 #pragma unroll
-        for (int b = 0; b < NT; b++) {
-            const int col = n0 + wn * 32 * NT + b * 32 + c32;
+        for (int b = 0; b < C::NT; b++) {
+            const int col = n0 + wn * 32 * C::NT + b * 32 + c32;
             if (col >= n) continue;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int row = m0 + wm * 32 * C::MT + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (row < m) {
                     if (epi == EPI_STORE) Y[(int64_t)row * n + col] = out[a][b][r];
                     else store_epi_slow(&Y[(int64_t)row * n + col], out[a][b][r], epi);
@@ -248,41 +278,61 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_q8_0(const uint8_t* __restric
         }
 }
 
-
 // K in whole 256-element steps and 32-bit DMA offsets.
 bool q8_gemm_fits(int64_t n, int64_t k, int64_t m) {
     return k % 256 == 0 && n * (k / 32) * Q8_0_BYTES < ((int64_t)1 << 32) && m * k < ((int64_t)1 << 32);
 }
 
-hipError_t launch_q8_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
-                          int epi, hipStream_t s) {
-    static const int wn = [] {
-        const char* e = getenv("LLOOM_HIP_Q8_WN");
-        return e && atoi(e) == 2 ? 2 : 4;
-    }();
+template <class C>
+static hipError_t launch_q8_cfg(const void* w, const Q8Ptrs& p, float* y, int64_t n, int64_t k, int64_t m, int epi,
+                                hipStream_t s) {
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e =
-            hipFuncSetAttribute((const void*)k_gemm_q8_0<2>, hipFuncAttributeMaxDynamicSharedMemorySize, Q8G_LDS);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_gemm_q8_0<4>, hipFuncAttributeMaxDynamicSharedMemorySize, Q8G_LDS);
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q8_0<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           C::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
+    const unsigned grid = (unsigned)(((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN));
+    hipLaunchKernelGGL(k_gemm_q8_0<C>, dim3(grid), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
+                       (int)m, (int)n, (int)k, (int)p.mp, epi);
+    return hipGetLastError();
+}
+
+// LLOOM_HIP_Q8_TILE (read once) picks the tile for tuning; -1 (default)
+// chooses by m.
+static int q8_tile_env() {
+    static const int v = [] {
+        const char* e = getenv("LLOOM_HIP_Q8_TILE");
+        return e ? atoi(e) : -1;
+    }();
+    return v;
+}
+
+hipError_t launch_q8_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
+                          int epi, hipStream_t s) {
     const Q8Ptrs p = q8_ptrs(qbuf, m, k);
     const int64_t nc = m * (k / 256);
     hipLaunchKernelGGL(k_gemm_prep_q8_0, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, s, x, p.xq, p.dxt, (int)m,
                        (int)k, (int)p.mp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const unsigned grid = (unsigned)(((m + Q8G_BM - 1) / Q8G_BM) * ((n + Q8G_BN - 1) / Q8G_BN));
-    if (wn == 2)
-        hipLaunchKernelGGL(k_gemm_q8_0<2>, dim3(grid), dim3(256), Q8G_LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
-                           (int)m, (int)n, (int)k, (int)p.mp, epi);
-    else
-        hipLaunchKernelGGL(k_gemm_q8_0<4>, dim3(grid), dim3(512), Q8G_LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
-                           (int)m, (int)n, (int)k, (int)p.mp, epi);
-    return hipGetLastError();
+    // by m (measured on [8192, 2048], graph replay with the prep launch):
+    // m <= 64 32 x 64 tiles, 4 stages (m = 64 26.6 us against 38.4 for
+    // 128 x 128); to 128 64 x 64 (28.3 against 38.8); to 384 64 x 128 with
+    // 8 waves (m = 256 34.2 against 41.2); past that 128 x 128 with 8 waves
+    // (m = 512 46.2, 1024 87.0, 2048 166.6 us)
+    int tile = q8_tile_env();
+    if (tile < 0) tile = m <= 64 ? 3 : m <= 128 ? 2 : m <= 384 ? 6 : 0;
+    switch (tile) {
+        case 1: return launch_q8_cfg<Q8Cfg<2, 2, 2, 2, 2>>(w, p, y, n, k, m, epi, s);   // 128 x 128, 4 waves
+        case 2: return launch_q8_cfg<Q8Cfg<2, 2, 1, 1, 4>>(w, p, y, n, k, m, epi, s);   // 64 x 64, 4 stages
+        case 3: return launch_q8_cfg<Q8Cfg<1, 2, 1, 1, 4>>(w, p, y, n, k, m, epi, s);   // 32 x 64, 4 stages
+        case 4: return launch_q8_cfg<Q8Cfg<1, 4, 2, 1, 2>>(w, p, y, n, k, m, epi, s);   // 64 x 128
+        case 5: return launch_q8_cfg<Q8Cfg<1, 4, 2, 1, 3>>(w, p, y, n, k, m, epi, s);   // 64 x 128, 3 stages
+        case 6: return launch_q8_cfg<Q8Cfg<2, 4, 1, 1, 3>>(w, p, y, n, k, m, epi, s);   // 64 x 128, 8 waves, 3 stages
+        default: return launch_q8_cfg<Q8Cfg<2, 4, 2, 1, 2>>(w, p, y, n, k, m, epi, s);  // 128 x 128, 8 waves
+    }
 }
 
 }  // namespace lloom
