@@ -272,9 +272,9 @@ static int qmatmul_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, in
     HIP_OK(hipSetDevice(ctx->device));
     hipStream_t s = pick_stream(ctx, stream);
     std::lock_guard<std::mutex> lock(ctx->mu);
-    // Q8_0 from 9 rows takes the GEMM (its decode kernel's time grows with
-    // the rows: m = 9 39.9 us and m = 16 51 us against 25 us for the GEMM on
-    // [8192, 2048]; m = 8 22.1 us)
+    // Q8_0 from 5 rows takes the GEMM (the decode kernel's time grows with
+    // the rows, 10.6 us at m = 4 and 22.1 at m = 8 on [8192, 2048]; the
+    // split-K GEMM with its activation prep is 11.1 us from m = 3 to 9)
     const bool decode = m <= ctx->mv_rows_max &&
                         !(ggml_type == T_Q8_0 && m >= Q8_GEMM_MIN_ROWS && q8_gemm_fits(n, k, m));
     void* ws = nullptr;

@@ -278,6 +278,198 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_q8_0(const uint8_t* __restr
         }
 }
 
+// ------------------------------------------------- few rows: split K --
+// For a few dozen activation rows the tiles above leave most CUs idle and
+// each wave's block chain (LDS reads, MFMA, epilogue) runs unhidden.  Here a
+// workgroup owns a BM x BN block of y (MT x NT tiles of 32 x 32) and its KS
+// waves split K: wave w takes steps w, w + KS, ..., each through its own
+// ring of S stages (no barrier inside the loop), and the KS partial sums
+// meet in LDS in wave order at the end.  Per step and block the arithmetic
+// is k_gemm_q8_0's.
+template <int KS_, int MT_, int NT_, int S_>
+struct Q8KCfg {
+    static constexpr int KS = KS_, MT = MT_, NT = NT_, S = S_;
+    static constexpr int THREADS = 64 * KS;
+    static constexpr int BM = 32 * MT, BN = 32 * NT;
+    static constexpr int A = BM * 256, B = ((BN * 272 + 1023) / 1024) * 1024, DX = 8 * BM * 4;
+    static constexpr int STAGE = A + B + DX;
+    static constexpr int A_CHUNKS = A / 1024, B_CHUNKS = B / 1024, DX_CHUNKS = DX / 1024;
+    static constexpr int DMA = A_CHUNKS + B_CHUNKS + DX_CHUNKS;  // loads a wave issues a stage
+    static constexpr int RED = KS * MT * NT * 16 * 64 * 4;       // the partial sums
+    static constexpr int LDS = KS * S * STAGE > RED ? KS * S * STAGE : RED;
+    static_assert(DX % 1024 == 0, "DX in whole chunks");
+    static_assert((S - 1) * DMA <= 63, "vmcnt counts to 63");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <class C>
+__global__ __launch_bounds__(C::THREADS) void k_gemm_q8_0_splitk(const uint8_t* __restrict__ W,
+                                                                   const int8_t* __restrict__ xq,
+                                                                   const float* __restrict__ dxt,
+                                                                   float* __restrict__ Y, int m, int n, int k, int mp,
+                                                                   int epi) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int h = lane >> 5, c32 = lane & 31;
+    const int m0 = blockIdx.y * C::BM, n0 = blockIdx.x * C::BN;
+    const int nsteps = k >> 8;
+    const uint32_t rowbytes = (uint32_t)(k / 32) * Q8_0_BYTES;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int mine = nsteps > wv ? (nsteps - wv + C::KS - 1) / C::KS : 0;  // this wave's steps (uniform)
+
+    // per-lane byte offsets of a stage (the wave loads the whole stage)
+    uint32_t aoff[C::A_CHUNKS];
+#pragma unroll
+    for (int q = 0; q < C::A_CHUNKS; q++) {
+        const int row = 4 * q + (lane >> 4);
+        const int piece = (lane & 15) ^ (row & 7);
+        aoff[q] = (uint32_t)min(m0 + row, m - 1) * (uint32_t)k + 16u * piece;
+    }
+    uint32_t boff[C::B_CHUNKS];
+#pragma unroll
+    for (int q = 0; q < C::B_CHUNKS; q++) {
+        const int pc = min(64 * q + lane, C::BN * 17 - 1);  // lanes past the last piece repeat it
+        const int row = pc / 17, piece = pc - row * 17;
+        boff[q] = (uint32_t)min(n0 + row, n - 1) * rowbytes + 16u * piece;
+    }
+    uint32_t dxoff[C::DX_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < C::DX_CHUNKS; c++) {
+        constexpr int LPB = C::BM / 4;
+        const int blk = c * (64 / LPB) + lane / LPB;
+        dxoff[c] = ((uint32_t)blk * (uint32_t)mp + (uint32_t)(m0 + 4 * (lane % LPB))) * 4u;
+    }
+    const uint32_t ring = lds_addr(smem) + (uint32_t)wv * (C::S * C::STAGE);
+    const uint8_t* ringp = smem + wave * (C::S * C::STAGE);
+
+    // the wave's i-th step into slot i % S (past its last step: the last one again)
+    auto issue = [&](int i) {
+        const int s = wv + C::KS * min(i, mine - 1);
+        const uint32_t st = ring + (i % C::S) * C::STAGE;
+        const uint8_t* ab = (const uint8_t*)xq + (uint32_t)s * 256u;
+#pragma unroll
+        for (int q = 0; q < C::A_CHUNKS; q++) dma16s(ab, aoff[q], st + 1024 * q);
+        const uint8_t* bb = W + (uint32_t)s * 272u;
+#pragma unroll
+        for (int q = 0; q < C::B_CHUNKS; q++) dma16s(bb, boff[q], st + C::A + 1024 * q);
+        const uint8_t* db = (const uint8_t*)(dxt + (int64_t)s * 8 * mp);
+#pragma unroll
+        for (int c = 0; c < C::DX_CHUNKS; c++) dma16s(db, dxoff[c], st + C::A + C::B + 1024 * c);
+    };
+
+    float out[C::MT][C::NT][16];
+#pragma unroll
+    for (int a = 0; a < C::MT; a++)
+#pragma unroll
+        for (int b = 0; b < C::NT; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
+
+    if (mine > 0) {
+#pragma unroll
+        for (int i = 0; i < C::S - 1; i++) issue(i);
+        for (int i = 0; i < mine; i++) {
+            issue(i + C::S - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            vm_wait<(C::S - 1) * C::DMA>();
+            const uint8_t* A = ringp + (i % C::S) * C::STAGE;
+            const uint8_t* B = A + C::A;
+            const float* DX = (const float*)(B + C::B);
+            const uint8_t* brow[C::NT];
+#pragma unroll
+            for (int b = 0; b < C::NT; b++) brow[b] = B + (b * 32 + c32) * 272;
+            auto block = [&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                v4i av[C::MT], bv[C::NT];
+                float dw[C::NT];
+#pragma unroll
+                for (int a = 0; a < C::MT; a++) {
+                    const int row = a * 32 + c32;
+                    av[a] = *(const v4i*)(A + row * 256 + 16 * ((2 * j + h) ^ (row & 7)));
+                }
+#pragma unroll
+                for (int b = 0; b < C::NT; b++) {
+                    bv[b] = q8_operand<j>(brow[b], h);
+                    dw[b] = f16_to_f32(*(const uint16_t*)(brow[b] + 34 * j));
+                }
+                v16i d[C::MT][C::NT];
+#pragma unroll
+                for (int a = 0; a < C::MT; a++)
+#pragma unroll
+                    for (int b = 0; b < C::NT; b++) {
+                        const v16i z = {};
+                        d[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bv[b], z, 0, 0, 0);
+                    }
+#pragma unroll
+                for (int a = 0; a < C::MT; a++) {
+                    const float* dxp = DX + j * C::BM + a * 32 + 4 * h;
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const float4 d4 = *(const float4*)(dxp + 8 * g);
+                        const float dxs[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const int r = 4 * g + u;
+#pragma unroll
+                            for (int b = 0; b < C::NT; b++)
+                                out[a][b][r] = __builtin_fmaf((float)d[a][b][r], dxs[u] * dw[b], out[a][b][r]);
+                        }
+                    }
+                }
+            };
+            block(std::integral_constant<int, 0>{});
+            block(std::integral_constant<int, 1>{});
+            block(std::integral_constant<int, 2>{});
+            block(std::integral_constant<int, 3>{});
+            block(std::integral_constant<int, 4>{});
+            block(std::integral_constant<int, 5>{});
+            block(std::integral_constant<int, 6>{});
+            block(std::integral_constant<int, 7>{});
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        vm_wait<0>();  // the repeated loads past the last step
+    }
+    // partial sums meet in LDS (over the stages: every wave is past them)
+    __syncthreads();
+    float* red = (float*)smem;
+#pragma unroll
+    for (int a = 0; a < C::MT; a++)
+#pragma unroll
+        for (int b = 0; b < C::NT; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) red[(((wave * C::MT + a) * C::NT + b) * 16 + r) * 64 + lane] = out[a][b][r];
+    __syncthreads();
+    // wave w stores tiles w, w + KS, ... of the MT x NT, adding the waves in order
+    for (int tt = wave; tt < C::MT * C::NT; tt += C::KS) {
+        const int a = tt / C::NT, b = tt % C::NT;
+        const int col = n0 + b * 32 + c32;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < C::KS; w++) v += red[(((w * C::MT + a) * C::NT + b) * 16 + r) * 64 + lane];
+            const int row = m0 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row < m && col < n) store_epi(&Y[(int64_t)row * n + col], v, epi);
+        }
+    }
+}
+
+template <class C>
+static hipError_t launch_q8k_cfg(const void* w, const Q8Ptrs& p, float* y, int64_t n, int64_t k, int64_t m, int epi,
+                                 hipStream_t s) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q8_0_splitk<C>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const dim3 grid((unsigned)((n + C::BN - 1) / C::BN), (unsigned)((m + C::BM - 1) / C::BM));
+    hipLaunchKernelGGL(k_gemm_q8_0_splitk<C>, grid, dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
+                       (int)m, (int)n, (int)k, (int)p.mp, epi);
+    return hipGetLastError();
+}
+
 // K in whole 256-element steps and 32-bit DMA offsets.
 bool q8_gemm_fits(int64_t n, int64_t k, int64_t m) {
     return k % 256 == 0 && n * (k / 32) * Q8_0_BYTES < ((int64_t)1 << 32) && m * k < ((int64_t)1 << 32);
@@ -318,13 +510,21 @@ hipError_t launch_q8_gemm(const void* w, const float* x, float* y, int64_t n, in
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // by m (measured on [8192, 2048], graph replay with the prep launch):
-    // m <= 64 32 x 64 tiles, 4 stages (m = 64 26.6 us against 38.4 for
-    // 128 x 128); to 128 64 x 64 (28.3 against 38.8); to 384 64 x 128 with
-    // 8 waves (m = 256 34.2 against 41.2); past that 128 x 128 with 8 waves
-    // (m = 512 46.2, 1024 87.0, 2048 166.6 us)
+    // to 32 rows 32 x 32 blocks with K split over 8 waves (m = 9..32
+    // 11.5-12.7 us, against 25-26 for the best output tiling); to 144 the
+    // same over 4 waves (m = 64 15.3, m = 128 24.0 against 26.6 and 28.3;
+    // m = 160 30.5 against ~33);
+    // to 384 64 x 128 tiles with 8 waves (m = 256 34.2 against 41.4); past
+    // that 128 x 128 with 8 waves (m = 512 46.2, 1024 87.0, 2048 166.6 us)
     int tile = q8_tile_env();
-    if (tile < 0) tile = m <= 64 ? 3 : m <= 128 ? 2 : m <= 384 ? 6 : 0;
+    if (tile < 0) tile = m <= 32 ? 10 : m <= 144 ? 15 : m <= 384 ? 6 : 0;
     switch (tile) {
+        case 10: return launch_q8k_cfg<Q8KCfg<8, 1, 1, 1>>(w, p, y, n, k, m, epi, s);
+        case 11: return launch_q8k_cfg<Q8KCfg<4, 1, 1, 2>>(w, p, y, n, k, m, epi, s);
+        case 12: return launch_q8k_cfg<Q8KCfg<4, 1, 2, 1>>(w, p, y, n, k, m, epi, s);
+        case 13: return launch_q8k_cfg<Q8KCfg<4, 2, 1, 1>>(w, p, y, n, k, m, epi, s);
+        case 14: return launch_q8k_cfg<Q8KCfg<2, 1, 1, 3>>(w, p, y, n, k, m, epi, s);
+        case 15: return launch_q8k_cfg<Q8KCfg<4, 1, 1, 1>>(w, p, y, n, k, m, epi, s);
         case 1: return launch_q8_cfg<Q8Cfg<2, 2, 2, 2, 2>>(w, p, y, n, k, m, epi, s);   // 128 x 128, 4 waves
         case 2: return launch_q8_cfg<Q8Cfg<2, 2, 1, 1, 4>>(w, p, y, n, k, m, epi, s);   // 64 x 64, 4 stages
         case 3: return launch_q8_cfg<Q8Cfg<1, 2, 1, 1, 4>>(w, p, y, n, k, m, epi, s);   // 32 x 64, 4 stages

@@ -44,7 +44,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                        void* qbuf, int mode, int epi, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode);
 // gemm_q8.hip: Q8_0 from Q8_GEMM_MIN_ROWS rows (K in 256-element steps).
-constexpr int Q8_GEMM_MIN_ROWS = 9;
+constexpr int Q8_GEMM_MIN_ROWS = 5;
 bool q8_gemm_fits(int64_t n, int64_t k, int64_t m);
 size_t q8_gemm_workspace_bytes(int64_t m, int64_t k);
 hipError_t launch_q8_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,

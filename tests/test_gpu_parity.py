@@ -219,14 +219,16 @@ def test_decode_rows_batch_invariant(L, dt):
     tolerance holds, as on the reference's CUDA and Metal arms).  Q8_0 runs
     the 8-wave dot4 kernel for 1..2 rows and the 4-wave one above that (their
     lane partials meet in different reduction trees), and keeps one K-chunk
-    (so one task set per lane) up to 4 rows at k = 1024."""
+    (so one task set per lane) up to 4 rows at k = 1024; from 5 to 32 rows
+    it runs the split-K GEMM (one configuration: the same sum order for
+    every row)."""
     rng = np.random.default_rng(3)
     n, k = 96, 1024
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
-    x = rng.standard_normal((16, k)).astype(np.float32)
+    x = rng.standard_normal((32, k)).astype(np.float32)
     qt = L.QTensor.quantize(_cuda(w), dt)
     mm = L.QMatMul.from_qtensor(qt)
-    groups = [(2, (1,)), (16, (3, 5, 8, 13))] if dt != O.Q8_0 else [(2, (1,)), (4, (3,))]
+    groups = [(2, (1,)), (16, (3, 5, 8, 13))] if dt != O.Q8_0 else [(2, (1,)), (4, (3,)), (32, (5, 9, 17))]
     for full_m, ms in groups:
         full = mm.forward(_cuda(x[:full_m])).cpu().numpy()
         for m in ms:
