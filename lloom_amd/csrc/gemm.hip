@@ -943,8 +943,8 @@ static bool fits_32bit(int64_t n, int64_t k, int64_t m) {
            m * (k / 256) * 32 < ((int64_t)1 << 31);
 }
 
-// Q6_K at every size takes the MFMA decode kernel with 64 activation rows
-// per workgroup layer (launch_mq); Q4_K does only past the skinny kernel's
+// Q6_K below k_gemm_q6k's row count takes the MFMA decode kernel with 64
+// activation rows per workgroup layer (launch_mq); Q4_K does only past the skinny kernel's
 // limit and up to LLOOM_HIP_MQ_MAX_ROWS (default 64, read once), or with
 // the int8-plane GEMM selected.
 static int64_t mq_max_rows() {
@@ -957,10 +957,20 @@ static int64_t mq_max_rows() {
 
 static bool use_mq(int type, int64_t m) { return type == T_Q6K || (type == T_Q4K && m <= mq_max_rows()); }
 
+// Q6_K from this many rows takes k_gemm_q6k (LLOOM_HIP_Q6_MIN_ROWS, read
+// once, overrides the default)
+static int64_t q6_min_rows() {
+    static const int64_t v = [] {
+        const char* e = getenv("LLOOM_HIP_Q6_MIN_ROWS");
+        return e ? (int64_t)atoll(e) : (int64_t)Q6_GEMM_MIN_ROWS;
+    }();
+    return v;
+}
 
 static int64_t skinny_max_rows();
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode) {
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(0, k, m) && mode != GEMM_INT8) return x16_bytes(m, k);
+    if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m)) return q6_gemm_workspace_bytes(n, k, m);
     if (use_mq(type, m)) return split_q8k_bytes(k, m);
     if (type == T_Q8_0 && q8_gemm_fits(n, k, m)) return q8_gemm_workspace_bytes(m, k);
     if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
@@ -1039,6 +1049,8 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                                (int)n, (int)k, epi);
         return hipGetLastError();
     }
+    if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m))
+        return launch_q6_gemm(w, x, y, n, k, m, qbuf, epi, s);
     if (use_mq(type, m)) return launch_mq(type, w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);

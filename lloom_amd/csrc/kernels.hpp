@@ -43,6 +43,14 @@ constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, int mode, int epi, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode);
+// gemm_q6.hip: Q6_K from Q6_GEMM_MIN_ROWS rows (below, k_mv_mfma with 64
+// activation rows a layer: m = 32 22.6 / 17.0 us against 21.7 for the GEMM
+// on [2048, 8192] / [8192, 2048]; m = 64 31.2 / 23.3 against 22.3 / 23.2).
+constexpr int Q6_GEMM_MIN_ROWS = 48;
+bool q6_gemm_fits(int64_t n, int64_t k, int64_t m);
+size_t q6_gemm_workspace_bytes(int64_t n, int64_t k, int64_t m);
+hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
+                          int epi, hipStream_t s);
 // gemm_q8.hip: Q8_0 from Q8_GEMM_MIN_ROWS rows (K in 256-element steps).
 constexpr int Q8_GEMM_MIN_ROWS = 5;
 bool q8_gemm_fits(int64_t n, int64_t k, int64_t m);

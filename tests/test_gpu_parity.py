@@ -176,6 +176,22 @@ def test_prefill_gemm_q8_0_shapes(L, m, n, k):
     assert_rows_close(y, O.matmul(O.Q8_0, x, q, n), what=f"q8_0 gemm m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 768), (300, 70, 1280), (200, 100, 8448), (129, 64, 4096)])
+def test_prefill_gemm_q6k_shapes(L, m, n, k):
+    """The Q6_K prefill GEMM on ragged tiles, an odd number of superblocks a
+    row (rows then start 2 bytes off a 4-byte boundary), K split over
+    workgroups (few tiles, long K: 33 superblocks in 7 splits of 5), an
+    all-zero activation block and a weight row of extreme scales."""
+    rng = np.random.default_rng(m * 3 + n)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[min(3, n - 1), :256] *= 80.0
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1, :256] = 0.0  # an all-zero activation block (d = 0)
+    x[min(2, m - 1), 37] = 1e4
+    y, q = _qmm(L, O.Q6K, w, x)
+    assert_rows_close(y, O.matmul(O.Q6K, x, q, n), what=f"q6k gemm m={m} n={n} k={k}")
+
+
 def test_prefill_gemm_q8_0_epilogues(L):
     """SiLU and multiply-into stores on the Q8_0 GEMM route."""
     rng = np.random.default_rng(21)
