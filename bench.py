@@ -17,7 +17,7 @@ B=1), algorithmic bytes per launch over its average launch time.
 
 `details` adds the other BASELINE configs (C1 Q8_0 decode, C3 Q4_K prefill
 TFLOP/s, C4 decoder-layer decode, C5 routed experts) measured the same way,
-and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
+plus the prefill of the Q8_0 and Q6_K weights on their own GEMMs, and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
 (oracle/kq_cpubase.c) on the same weights on a bounded sample.
 """
 import argparse
@@ -276,6 +276,24 @@ def run_details(L, cu, np, torch, dev, args):
     set_prefill_mma(MMA_F16)
     del rot3
     torch.cuda.empty_cache()
+    # prefill of the other weight types on their GEMMs (not a BASELINE
+    # config; the C1 Q8_0 weight and the C4 Q6_K down projection, same method)
+    for name, dt, n, k in (("q8_0", L.GgmlDType.Q8_0, 8192, 2048), ("q6k", L.GgmlDType.Q6K, 2048, 8192)):
+        qt = L.QTensor.quantize(cu(L.synth_normal(5, n * k, 0.0, 0.02)).view(n, k), dt)
+        rot = Rotation(qt, copies_for(qt.packed_bytes()))
+        pf = {}
+        for m in (64, 512, 2048):
+            x = cu(L.synth_normal(2000 + m, m * k)).view(m, k)
+            y = torch.empty((m, n), device=dev)
+            calls = rot.tensors if m < 2048 else rot.tensors[:16]
+            fns = [lambda t=t: L.QMatMul(t).forward_into(x, y) for t in calls]
+            t = time_graph(fns, 3 if m < 2048 else 2, 1) / len(fns)
+            ops = 2.0 * m * n * k
+            pf[str(m)] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 2),
+                          "i8_peak_frac": round(ops / t / 1e12 / I8_PEAK_TOPS, 4)}
+        out["prefill_" + name + "_%dx%d" % (n, k)] = pf
+        del rot
+        torch.cuda.empty_cache()
     # C4 decoder layer decode (q,k,v,o,gate,up in Q4_K; down in Q6_K)
     shapes = [("q", 2048, 2048, 12), ("k", 512, 2048, 12), ("v", 512, 2048, 12), ("o", 2048, 2048, 12),
               ("gate", 8192, 2048, 12), ("up", 8192, 2048, 12), ("down", 2048, 8192, 14)]
