@@ -47,6 +47,9 @@ def parse():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="launch only the roofline kernel (C2 at B=1, eagerly, on cold weight copies) and a "
                          "64 MiB device copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
+    ap.add_argument("--pmc-probe-type", default="q4k", choices=["q4k", "q8_0", "q6k"],
+                    help="weight type of --pmc-probe-prefill (q4k: C3's [8192, 2048]; q8_0 [8192, 2048]; "
+                         "q6k [2048, 8192])")
     ap.add_argument("--pmc-probe-prefill", action="store_true",
                     help="launch only the C3 prefill GEMM at m=2048 (5 calls), for rocprofv3 --pmc runs on the "
                          "MFMA kernel")
@@ -142,14 +145,15 @@ def main():
         return lambda: L.QMatMul(qtensor).forward_into(xs[b], ys[b])
 
     if args.pmc_probe_prefill:
-        n3, k3, m3 = 8192, 2048, 2048
-        qt3 = L.QTensor.quantize(cu(L.synth_normal(2, n3 * k3, 0.0, 0.02)).view(n3, k3), L.GgmlDType.Q4K)
+        dt3 = {"q4k": L.GgmlDType.Q4K, "q8_0": L.GgmlDType.Q8_0, "q6k": L.GgmlDType.Q6K}[args.pmc_probe_type]
+        n3, k3, m3 = (2048, 8192, 2048) if args.pmc_probe_type == "q6k" else (8192, 2048, 2048)
+        qt3 = L.QTensor.quantize(cu(L.synth_normal(2, n3 * k3, 0.0, 0.02)).view(n3, k3), dt3)
         x3 = cu(L.synth_normal(2000 + m3, m3 * k3)).view(m3, k3)
         y3 = torch.empty((m3, n3), device=dev)
         for _ in range(5):
             L.QMatMul(qt3).forward_into(x3, y3)
         torch.cuda.synchronize()
-        print(json.dumps({"pmc_probe": "c3_m2048", "ops_per_call": 2 * m3 * n3 * k3}))
+        print(json.dumps({"pmc_probe": "prefill_%s_m2048" % args.pmc_probe_type, "ops_per_call": 2 * m3 * n3 * k3}))
         return
 
     if args.pmc_probe:

@@ -70,21 +70,26 @@ __global__ __launch_bounds__(256) void k_gemm_prep_q6(const float* __restrict__ 
 // 32 WN NT).  K moves one superblock a step through a ring of S LDS stages,
 // every byte by global_load_lds:
 //   A  [BM][256] int8, sub-block j (16 B) of row r at position j ^ (r & 15)
-//   B  [BN][224] the 16-byte-aligned window around each weight row's
+//   B  [BN][240] the 16-byte-aligned window around each weight row's
 //      superblock: Q6_K rows are 210 bytes a superblock, so the block sits
-//      (row start + 210 sb) mod 16 bytes into its window (an even number)
+//      (row start + 210 sb) mod 16 bytes into its window (an even number);
+//      224 bytes would hold it, 240 (15 pieces) puts the rows 60 dwords
+//      apart, so 32 lanes reading one offset of their columns hit 16 banks
+//      rather than 8 (LDS bank conflicts at m = 2048: 35 % of the cycles)
 //   DY [BM] f32, the step's activation scales (one 1 KB chunk)
 // Every wave issues the same number of loads a stage (a wave past the last
 // chunk of a part repeats one), so a counted vmcnt wait before each
 // barrier leaves exactly the later stages in flight.
 // MFMA operands (the same k-set for A and B in a lane): lane l holds row
 // (or column) l % 32, elements 8 (l / 32) .. +7 of the sub-block.
+constexpr int Q6_PIECES = 15, Q6_WIN = 16 * Q6_PIECES;  // a row's window in LDS
+
 template <int WM_, int WN_, int MT_, int NT_, int S_>
 struct Q6Cfg {
     static constexpr int WM = WM_, WN = WN_, MT = MT_, NT = NT_, S = S_;
     static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
     static constexpr int BM = 32 * WM * MT, BN = 32 * WN * NT;
-    static constexpr int A = BM * 256, B = ((BN * 224 + 1023) / 1024) * 1024, DY = 1024;
+    static constexpr int A = BM * 256, B = ((BN * Q6_WIN + 1023) / 1024) * 1024, DY = 1024;
     static constexpr int STAGE = A + B + DY, LDS = S * STAGE;
     static constexpr int A_CHUNKS = A / 1024, B_CHUNKS = B / 1024;
     static constexpr int A_PER_WAVE = A_CHUNKS / WAVES;
@@ -146,10 +151,10 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_q6k(const uint8_t* __restri
 #pragma unroll
     for (int i = 0; i < C::B_PER_WAVE; i++) {
         const int q = min(wave + C::WAVES * i, C::B_CHUNKS - 1);
-        const int pc = min(64 * q + lane, C::BN * 14 - 1);
-        const int row = pc / 14;
+        const int pc = min(64 * q + lane, C::BN * Q6_PIECES - 1);
+        const int row = pc / Q6_PIECES;
         brs[i] = (uint32_t)min(n0 + row, n - 1) * rowbytes;
-        bpc[i] = 16u * (uint32_t)(pc - row * 14);
+        bpc[i] = 16u * (uint32_t)(pc - row * Q6_PIECES);
     }
     const uint32_t dyoff = (uint32_t)(m0 + 4 * min(lane, C::BM / 4 - 1)) * 4u;
     const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -202,7 +207,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_q6k(const uint8_t* __restri
 #pragma unroll
         for (int b = 0; b < C::NT; b++) {
             const uint32_t sh = (crs[b] + (uint32_t)(s0 + s) * Q6K_BYTES) & 15u;
-            const uint8_t* win = B + (wn * 32 * C::NT + b * 32 + c32) * 224 + (sh & ~3u);
+            const uint8_t* win = B + (wn * 32 * C::NT + b * 32 + c32) * Q6_WIN + (sh & ~3u);
             const uint32_t r2 = sh & 3u;
 #pragma unroll
             for (int i = 0; i < 8; i++) qlw[b][i] = lds8_shift(win + 64 * (i >> 2) + 32 * ((i >> 1) & 1) + 16 * (i & 1) + 8 * h, r2);
