@@ -23,9 +23,9 @@ size_t split_q8k_bytes(int64_t k, int64_t m);
 void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d);
 hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s);
 
-// matvec.hip: m <= 16.  Rows up to MV_DOT_MAX_ROWS take the fused dot4
-// kernel; Q4_K with more rows takes the MFMA kernel on a workspace of
-// matvec_workspace_bytes.
+// matvec.hip: m <= 16.  Rows up to MV_DOT_MAX_ROWS (Q4_K on a weight of at
+// most 2048^2 elements: up to 4) take the fused dot4 kernel; more rows take
+// the MFMA kernels on a workspace of matvec_workspace_bytes.
 constexpr int MV_DOT_MAX_ROWS = 2;
 size_t matvec_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,

@@ -23,6 +23,8 @@
 #include "kq_quant.hpp"
 #include "kq_tasks.hpp"
 #include "kq_mfma.hpp"
+#include <cstdlib>
+
 #include "kernels.hpp"
 
 namespace lloom {
@@ -711,6 +713,10 @@ template <int TYPE>
 static hipError_t launch_type(const void* w, const float* x, float* y, int n, int K, int m, int epi, hipStream_t s) {
     if (m <= 1) return launch_small<TYPE, 1>(w, x, y, n, K, m, epi, s);
     if (m <= 2) return launch_small<TYPE, 2>(w, x, y, n, K, m, epi, s);
+    if constexpr (TYPE == T_Q4K) {
+        if (m <= 3) return launch_small<TYPE, 3>(w, x, y, n, K, m, epi, s);
+        return launch_small<TYPE, 4>(w, x, y, n, K, m, epi, s);
+    }
     if (m <= 4) return launch_cfg<TYPE, 4, 4, 2>(w, x, y, n, K, m, epi, s);
     if (m <= 8) return launch_cfg<TYPE, 8, 4, 2>(w, x, y, n, K, m, epi, s);
     return launch_cfg<TYPE, 16, 4, 2>(w, x, y, n, K, m, epi, s);
@@ -799,12 +805,20 @@ hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t 
                          : launch_mv_mfma<T_Q6K, 4>(w, y, n, k, m, xq, xd, epi, s);
 }
 
+// Rows of Q4_K / Q6_K on the dot4 kernel: one or two, and Q4_K with 3-4
+// rows on a small weight (n k <= 2048^2: [2048, 2048] at m = 4 5.04 us
+// against 6.23 for the fused MFMA kernel; on [6144, 2048] 7.63 against
+// 6.49, and Q6_K [2048, 8192] 15.8 against 12.0).
+static bool mv_dot(int type, int64_t n, int64_t k, int64_t m) {
+    return m <= MV_DOT_MAX_ROWS || (type == T_Q4K && m <= 4 && n * k <= 2048 * 2048);
+}
+
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, int epi, hipStream_t s) {
-    if (type != T_Q8_0 && m > MV_DOT_MAX_ROWS && m <= FUSED_MAX_ROWS && (k == 2048 || k == 1024))
+    if (type != T_Q8_0 && !mv_dot(type, n, k, m) && m <= FUSED_MAX_ROWS && (k == 2048 || k == 1024))
         return type == T_Q4K ? launch_fused<T_Q4K>(w, x, y, n, k, m, epi, s)
                              : launch_fused<T_Q6K>(w, x, y, n, k, m, epi, s);
-    if (type != T_Q8_0 && m > MV_DOT_MAX_ROWS) {
+    if (type != T_Q8_0 && !mv_dot(type, n, k, m)) {
         int8_t* xq;
         float* xd;
         split_q8k_ptrs(ws, k, m, &xq, &xd);

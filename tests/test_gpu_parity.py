@@ -228,9 +228,10 @@ def test_decode_rows_batch_invariant(L, dt):
     """Within one decode kernel every activation row is computed alone, so a
     row's output does not depend on its batch (qmm_batch,
     quantized_tests.rs:239-275, exact on the CPU arm).  Q4_K and Q6_K with
-    3..16 rows run the MFMA kernels (3..4 rows at this k the single-launch
-    variant, whose per-output arithmetic and partial-sum order are the
-    two-launch kernel's), 1..2 the dot4 kernel: each group is
+    up to 16 rows run the MFMA kernels (3..4 rows at this k the
+    single-launch variant, whose per-output arithmetic and partial-sum order
+    are the two-launch kernel's) above the dot4 kernel's rows (1..2; Q4_K on
+    a weight this small 1..4): each group is
     checked against its own full batch (across the two kernels only the
     tolerance holds, as on the reference's CUDA and Metal arms).  Q8_0 runs
     the 8-wave dot4 kernel for 1..2 rows and the 4-wave one above that (their
@@ -244,7 +245,8 @@ def test_decode_rows_batch_invariant(L, dt):
     x = rng.standard_normal((32, k)).astype(np.float32)
     qt = L.QTensor.quantize(_cuda(w), dt)
     mm = L.QMatMul.from_qtensor(qt)
-    groups = [(2, (1,)), (16, (3, 5, 8, 13))] if dt != O.Q8_0 else [(2, (1,)), (4, (3,)), (32, (5, 9, 17))]
+    groups = {O.Q4K: [(4, (1, 2, 3)), (16, (5, 8, 13))], O.Q6K: [(2, (1,)), (16, (3, 5, 8, 13))],
+              O.Q8_0: [(2, (1,)), (4, (3,)), (32, (5, 9, 17))]}[dt]
     for full_m, ms in groups:
         full = mm.forward(_cuda(x[:full_m])).cpu().numpy()
         for m in ms:
