@@ -300,23 +300,39 @@ struct MoeRuns<T_Q8_0> {
 template <int TYPE>
 __device__ __forceinline__ void task_runs(const WPrep<TYPE>& w, float (&q)[MoeRuns<TYPE>::N][16],
                                           float (&a)[MoeRuns<TYPE>::N], float (&b)[MoeRuns<TYPE>::N]) {
+    // (the empty asm hides the words' known-zero bits: with them visible
+    // the compiler converts each byte with a bit-field extract and
+    // v_cvt_f32_ubyte0 instead of one v_cvt_f32_ubyteN)
     if constexpr (TYPE == T_Q4K) {
         a[0] = w.d * (float)w.sc0;
         b[0] = w.dmin * (float)w.m0;
         a[1] = w.d * (float)w.sc1;
         b[1] = w.dmin * (float)w.m1;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = w.lo[i];
+            hi[i] = w.hi[i];
+            asm("" : "+v"(lo[i]), "+v"(hi[i]));
+        }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            q[0][i] = (float)byte_of(w.lo[i >> 2], i & 3);
-            q[1][i] = (float)byte_of(w.hi[i >> 2], i & 3);
+            q[0][i] = (float)byte_of(lo[i >> 2], i & 3);
+            q[1][i] = (float)byte_of(hi[i >> 2], i & 3);
         }
     } else if constexpr (TYPE == T_Q6K) {
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             a[g] = w.d * (float)w.sc[g];
             b[g] = 32.0f * a[g];
+            uint32_t qw[4];
 #pragma unroll
-            for (int i = 0; i < 16; i++) q[g][i] = (float)byte_of(w.q[g][i >> 2], i & 3);
+            for (int i = 0; i < 4; i++) {
+                qw[i] = w.q[g][i];
+                asm("" : "+v"(qw[i]));
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) q[g][i] = (float)byte_of(qw[i >> 2], i & 3);
         }
     } else {
         a[0] = a[1] = w.d;
