@@ -452,7 +452,7 @@ def _silu32(v):
 
 
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
-@pytest.mark.parametrize("m", [1, 2, 5, 16, 40])
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 40, 64, 200])
 def test_forward_silu_and_mul_into(L, dt, m):
     """QMatMul::forward_silu / forward_mul_into (mod.rs:2102-2156): the
     stored value is silu(v) (resp. gate * v) of the product the plain
@@ -599,3 +599,20 @@ def test_refusals_are_named(L):
     y = torch.empty((1, 4), device=DEV)
     rc = lib().lloom_hip_qmatmul(_ctx(0), 15, _ptr(qt.storage), 4, 256, _ptr(x), 0, 1, _ptr(y), 0, _stream(x))
     assert rc == 2 and b"Q8K" in lib().lloom_hip_last_error()
+
+
+@pytest.mark.parametrize("dt,m,n,k", [(O.Q8_0, 9, 300, 2048), (O.Q8_0, 100, 300, 2048), (O.Q8_0, 600, 300, 1024),
+                                      (O.Q6K, 64, 200, 8192), (O.Q6K, 300, 256, 8192), (O.Q4K, 40, 300, 2048),
+                                      (O.Q4K, 700, 300, 2048)])
+def test_prefill_repeatable(L, dt, m, n, k):
+    """Every prefill route sums in a fixed order (K split over waves or
+    workgroups included: the partial sums meet in wave or split order), so a
+    repeated call is bit-identical."""
+    rng = np.random.default_rng(m + n)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = _cuda(rng.standard_normal((m, k)).astype(np.float32))
+    mm = L.QMatMul.from_qtensor(L.QTensor.quantize(_cuda(w), dt))
+    a = mm.forward(x).cpu().numpy()
+    b = mm.forward(x).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
