@@ -299,26 +299,36 @@ struct MoeRuns<T_Q8_0> {
 
 template <int TYPE>
 __device__ __forceinline__ void task_runs(const WPrep<TYPE>& w, float (&q)[MoeRuns<TYPE>::N][16],
-                                          float (&a)[MoeRuns<TYPE>::N], float (&b)[MoeRuns<TYPE>::N]) {
-    // (the empty asm hides the words' known-zero bits: with them visible
+                                          float (&a)[MoeRuns<TYPE>::N], float (&b)[MoeRuns<TYPE>::N],
+                                          float fp8_inv) {
+    // Q4_K: a nibble byte q (0..15) read as an FP8 E4M3 value is exactly
+    // q * u (the exponent field is 0 or 1, so the value is linear in q), and
+    // v_cvt_pk_f32_fp8 converts two bytes an instruction; the unit u (a power
+    // of two, measured once by the kernel as fp8_inv = 1 / u) moves into the
+    // scale: (a / u) * sum((q u) x) is a * sum(q x) bit for bit.
+    // Q6_K: the empty asm hides the words' known-zero bits (with them visible
     // the compiler converts each byte with a bit-field extract and
-    // v_cvt_f32_ubyte0 instead of one v_cvt_f32_ubyteN)
+    // v_cvt_f32_ubyte0 instead of one v_cvt_f32_ubyteN).
     if constexpr (TYPE == T_Q4K) {
-        a[0] = w.d * (float)w.sc0;
+        a[0] = w.d * (float)w.sc0 * fp8_inv;
         b[0] = w.dmin * (float)w.m0;
-        a[1] = w.d * (float)w.sc1;
+        a[1] = w.d * (float)w.sc1 * fp8_inv;
         b[1] = w.dmin * (float)w.m1;
-        uint32_t lo[4], hi[4];
+        typedef float f2 __attribute__((ext_vector_type(2)));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            lo[i] = w.lo[i];
-            hi[i] = w.hi[i];
-            asm("" : "+v"(lo[i]), "+v"(hi[i]));
-        }
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            q[0][i] = (float)byte_of(lo[i >> 2], i & 3);
-            q[1][i] = (float)byte_of(hi[i >> 2], i & 3);
+            const f2 l0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.lo[i], false);
+            const f2 l1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.lo[i], true);
+            const f2 h0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.hi[i], false);
+            const f2 h1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.hi[i], true);
+            q[0][4 * i] = l0.x;
+            q[0][4 * i + 1] = l0.y;
+            q[0][4 * i + 2] = l1.x;
+            q[0][4 * i + 3] = l1.y;
+            q[1][4 * i] = h0.x;
+            q[1][4 * i + 1] = h0.y;
+            q[1][4 * i + 2] = h1.x;
+            q[1][4 * i + 3] = h1.y;
         }
     } else if constexpr (TYPE == T_Q6K) {
 #pragma unroll
@@ -452,6 +462,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
     for (int r = 0; r < RR; r++)
         wrow[r] = (r < R ? W : W2) + ((int64_t)e * n + min(row0 + r % R, n - 1)) * rowbytes;
     const int T = (K / Tr::BE) * Tr::P;
+    const float fp8_inv = 1.0f / __builtin_amdgcn_cvt_f32_fp8(1, 0);  // 1 / (FP8 byte 1), a power of two
     const int k16 = K >> 4;
 
     for (int g0 = 0; g0 < np; g0 += pgmax) {
@@ -509,7 +520,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
                     for (int r = 0; r < RR; r++) {
                         WPrep<TYPE> wp;
                         prep_task<TYPE>(tda[c][r], ti % Tr::P, wp);
-                        task_runs<TYPE>(wp, qv[r], ra[r], rb[r]);
+                        task_runs<TYPE>(wp, qv[r], ra[r], rb[r], fp8_inv);
                     }
                     int off[NR];
 #pragma unroll
