@@ -15,6 +15,7 @@
 //     k_moe_rows (activations read from L2 per row) is kept for rows too long
 //     to stage.
 #include "kq_common.hpp"
+#include "kq_mfma.hpp"
 #include "kq_tasks.hpp"
 #include "kernels.hpp"
 
@@ -579,6 +580,339 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
     }
 }
 
+// ------------------------------------------- Q4_K experts on fp16 MFMA --
+// The same contract (f32 activations, exactly dequantized weights, f32
+// accumulation) on v_mfma_f32_16x16x32_f16.  A workgroup (4 waves) owns
+// 64 NT weight rows of one expert; each wave NT 16-row tiles over all of K.
+// Operands of the MFMA for sub-block j of superblock sb (g = lane / 16):
+//   A (planes):  lane l holds x'[plane l%16][256 sb + 32 j + 8 g + 0..7]
+//   B (weights): lane l holds sc_j * q[row l%16][the same 8 elements]
+//   D:           lane l holds D[plane 4 g + v][row l%16], v = 0..3
+// * The planes are staged in LDS once per workgroup, each scaled by a power
+//   of two (x' = x * 2^s, max |x'| in [2^13, 2^14): exact) and split into
+//   fp16 hi + lo (x' = hi + lo to about 2^-22 relative); the two halves take
+//   one MFMA each into the same f32 accumulator.  sc_j * q <= 945 is an exact
+//   fp16 integer, so every product is exact and only the f32 sums round, as
+//   in the VALU kernel.  MFMA rows past the staged planes repeat the last one
+//   and are not stored.
+// * Per superblock: acc = sum_j sc_j * S_j (16 MFMAs); the min term
+//   sum_j m_j * X_j (X_j: sub-block sums of x', / 32 so they stay in fp16
+//   range, hi and lo side by side in K) is one more MFMA against the mins;
+//   out += d * acc - 32 dmin * accm.  The output is out * 2^-s.
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mh2 __attribute__((ext_vector_type(2)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+
+// Four nibbles (one per byte, 0..15) times sc as fp16, in element order:
+// v_perm_b32 puts each nibble under the exponent byte 0x64 (fp16 1024 + q),
+// one packed fma gives (1024 + q) * sc - 1024 * sc = q * sc, exact.
+__device__ __forceinline__ uint2 moe_nib4(uint32_t w, mh2 sc, mh2 off) {
+    const uint32_t e = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);  // [q0, q1]
+    const uint32_t o = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);  // [q2, q3]
+    const mh2 ve = __builtin_elementwise_fma(__builtin_bit_cast(mh2, e), sc, off);
+    const mh2 vo = __builtin_elementwise_fma(__builtin_bit_cast(mh2, o), sc, off);
+    return make_uint2(__builtin_bit_cast(uint32_t, ve), __builtin_bit_cast(uint32_t, vo));
+}
+
+// Byte i of each of four bytes (each 0..63) as fp16, packed two a dword.
+__device__ __forceinline__ uint2 moe_b4_h(uint32_t w) {
+    const mh2 k = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+    const mh2 e = __builtin_bit_cast(mh2, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) + k;
+    const mh2 o = __builtin_bit_cast(mh2, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) + k;
+    return make_uint2(__builtin_bit_cast(uint32_t, e), __builtin_bit_cast(uint32_t, o));
+}
+
+constexpr int MOEM_LDS = 96 * 1024;  // bytes of staged planes a pass
+constexpr int MOE_MFMA_DENSITY = 8;  // planes per active expert (at least) for the MFMA kernel
+constexpr int MOEM_FUSE_MAX = 1024;  // planes routed inside the kernel (an LDS list per workgroup)
+#ifndef MOEM_WAVES_EU
+#define MOEM_WAVES_EU 2
+#endif
+
+// LDS bytes of a pass of pg planes: hi and lo [K/8][pg][8] fp16, the sums
+// [K/256][pg][16] fp16; then scales and the waves' transpose tiles.
+__host__ __device__ inline int moem_plane_bytes(int K) { return 4 * K + 32 * (K / 256); }
+__host__ __device__ inline int moem_fixed_bytes(int waves) { return 256 + waves * 16 * MfRs<T_Q4K>::V; }
+
+// One workgroup (4 waves) per (64 GW RG weight rows, expert).  A wave owns
+// GW row groups of 16 RG rows (RG = 2 row tiles, or for GLU one tile of the
+// gate and the same tile of the up weight) and streams its items (row
+// group, superblock) over all of K with DEPTH items of weight loads in
+// flight; the planes are staged in LDS once per workgroup and pass.
+// Routing: with `route` 0 the workgroup of expert blockIdx.y collects the
+// planes routed to it from ids itself (planes <= MOEM_FUSE_MAX), and the
+// extra grid layer y = E zeroes the outputs of out-of-range ids and raises
+// the flags; otherwise k_moe_route has sorted the planes and y is the
+// active-expert slot.
+template <int DEPTH, bool GLU>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MOEM_WAVES_EU))) void k_moe_mfma(
+    const uint8_t* __restrict__ W, const float* __restrict__ X, float* __restrict__ Y,
+    const uint32_t* __restrict__ ids, int planes, int* ws, int* sticky, int E, int n, int K, int in_dim1, int topk,
+    int pgmax, const uint8_t* __restrict__ W2, float* __restrict__ Y2, int route, int gw) {
+    constexpr int RT = 2;                 // weight tiles an item holds
+    constexpr int RG = GLU ? 16 : 32;     // rows of a row group
+    if (!GLU && blockIdx.z) {
+        W = W2;
+        Y = Y2;
+    }
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_list[MOEM_FUSE_MAX];
+    __shared__ int s_np;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int wrow0 = (blockIdx.x * 4 + wave) * gw * RG;  // this wave's first row
+    const int brow0 = blockIdx.x * 4 * gw * RG, brow1 = min(brow0 + 4 * gw * RG, n);
+
+    int e, np;
+    const int* list;
+    if (!route) {
+        if ((int)blockIdx.y == E) {
+            // out-of-range ids: their planes are zero in every output
+            int bad = 0;
+            for (int p = tid; p < planes; p += 256) {
+                if (ids[p] >= (uint32_t)E) {
+                    bad = 1;
+                    for (int r = brow0; r < brow1; r++) Y[(int64_t)p * n + r] = 0.0f;
+                }
+            }
+            bad = __syncthreads_or(bad);
+            if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) {
+                ws[0] = bad;  // this call: read back by a strict call
+                if (bad) sticky[0] = 1;
+            }
+            return;
+        }
+        e = blockIdx.y;
+        if (tid == 0) s_np = 0;
+        __syncthreads();
+        // the list's order follows the LDS atomics; every plane's dot is
+        // computed on its own, so no result depends on it
+        for (int p = tid; p < planes; p += 256)
+            if (ids[p] == (uint32_t)e) s_list[atomicAdd(&s_np, 1)] = p;
+        __syncthreads();
+        np = s_np;
+        if (np == 0) return;  // uniform
+        list = s_list;
+    } else {
+        const int* count = ws + 2;
+        const int* start = count + E;
+        const int* active = start + E;
+        const int* sorted = active + E;
+        if ((int)blockIdx.y >= ws[1]) return;  // uniform
+        e = active[blockIdx.y];
+        np = count[e];
+        list = sorted + start[e];
+    }
+
+    const int nsb = K >> 8, k8 = K >> 3;
+    const int nitems = gw * nsb;
+    const int64_t rowbytes = (int64_t)nsb * Q4K_BYTES;
+    const uint8_t* wbase = W + (int64_t)e * n * rowbytes;
+    const uint8_t* wbase2 = (GLU ? W2 : W) + (int64_t)e * n * rowbytes;
+    // item i: row group i / nsb, superblock i % nsb (indices past the end
+    // reload the last item: no load sits under a branch)
+    auto load_item = [&](int i, MfL<T_Q4K>(&b)[RT]) {
+        i = min(i, nitems - 1);
+        const int rg = i / nsb, sb = i - rg * nsb;
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            const int row = min(wrow0 + rg * RG + (GLU ? 0 : 16 * t) + c16, n - 1);
+            mf_load_l<T_Q4K>((GLU && t ? wbase2 : wbase) + row * rowbytes + (int64_t)sb * Q4K_BYTES, g, b[t]);
+        }
+    };
+
+    _Float16* xh = (_Float16*)smem;
+    uint32_t* pmax = (uint32_t*)(smem + (size_t)pgmax * moem_plane_bytes(K));
+    float* pscale = (float*)(pmax + 16);
+    float* pinv = pscale + 16;
+    uint8_t* tile = smem + (size_t)pgmax * moem_plane_bytes(K) + 256 + wave * 16 * MfRs<T_Q4K>::V;
+
+    auto xoff = [&](int q) {
+        const int pl = list[q];
+        const int b = pl / topk, t = pl - b * topk;
+        return (int64_t)(b * in_dim1 + (in_dim1 == 1 ? 0 : t)) * K;
+    };
+
+    for (int g0 = 0; g0 < np; g0 += pgmax) {
+        const int pg = min(pgmax, np - g0);
+        _Float16* xl = xh + (size_t)pg * K;
+        _Float16* xs = xl + (size_t)pg * K;
+        // the first items' weights are in flight during the staging
+        MfL<T_Q4K> buf[DEPTH][RT];
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) load_item(d, buf[d]);
+
+        if (g0) __syncthreads();  // the previous pass's readers are done
+        if (tid < 16) pmax[tid] = 0u;
+        __syncthreads();
+        // 1. max |x| of each plane (non-negative floats order as their bits)
+        for (int i = tid; i < pg * k8; i += 256) {
+            const int q = i / k8, G = i - q * k8;
+            const float4* xr = (const float4*)(X + xoff(g0 + q) + 8 * G);
+            const float4 a = xr[0], b = xr[1];
+            const float mx = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                   fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+            atomicMax(&pmax[q], __float_as_uint(mx));
+        }
+        __syncthreads();
+        if (tid < pg) {
+            const float mx = __uint_as_float(pmax[tid]);
+            const bool fin = mx > 0.0f && mx <= 3.4028234e38f;
+            int ex = 0;
+            if (fin) (void)frexpf(mx, &ex);
+            const int sh = fin ? 14 - ex : 0;  // max |x'| in [2^13, 2^14)
+            pscale[tid] = ldexpf(1.0f, sh);
+            pinv[tid] = ldexpf(1.0f, -sh);
+        }
+        __syncthreads();
+        // 2. x' = x * 2^s as hi + lo, and the sub-block sums of x' / 32
+        //    (a quad of lanes holds the four 8-element groups of a sub-block)
+        for (int i = tid; i < pg * k8; i += 256) {
+            const int q = i / k8, G = i - q * k8;
+            const float4* xr = (const float4*)(X + xoff(g0 + q) + 8 * G);
+            const float4 a = xr[0], b = xr[1];
+            const float sc = pscale[q];
+            const float v[8] = {a.x * sc, a.y * sc, a.z * sc, a.w * sc, b.x * sc, b.y * sc, b.z * sc, b.w * sc};
+            mh8 hv, lv;
+            float sum = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const _Float16 hu = (_Float16)v[u];
+                hv[u] = hu;
+                lv[u] = (_Float16)(v[u] - (float)hu);
+                sum += v[u];
+            }
+            *(mh8*)(xh + ((size_t)G * pg + q) * 8) = hv;
+            *(mh8*)(xl + ((size_t)G * pg + q) * 8) = lv;
+            sum += __shfl_xor(sum, 1, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            if ((G & 3) == 0) {
+                const float s32 = sum * 0.03125f;
+                const _Float16 sh = (_Float16)s32;
+                _Float16* d = xs + ((size_t)(G >> 5) * pg + q) * 16 + ((G >> 2) & 7);
+                d[0] = sh;
+                d[8] = (_Float16)(s32 - (float)sh);
+            }
+        }
+        __syncthreads();
+
+        const int pc = min(c16, pg - 1);  // this lane's A row
+        mf4 out[RT];
+#pragma unroll
+        for (int t = 0; t < RT; t++) out[t] = mf4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int it = 0; it < nitems; it++) {
+            MfL<T_Q4K> nxt[RT];
+            load_item(it + DEPTH, nxt);
+            const int rg = it / nsb, sb = it - rg * nsb;
+            {
+            // min-term operand: K 0..7 the sums' hi, 8..15 their lo (lanes
+            // g >= 2 repeat them against zero weights)
+            const mh8 am = *(const mh8*)(xs + ((size_t)sb * pg + pc) * 16 + 8 * (g & 1));
+            // the tiles' weights and scales, then the sub-blocks (one pair of
+            // activation operands serves both tiles)
+            MfW<T_Q4K> wu[RT];
+            mh2 scp[RT][4];
+            mf4 acc[RT];
+#pragma unroll
+            for (int t = 0; t < RT; t++) {
+                mf_unpack<T_Q4K>(buf[0][t], tile, g, c16, wu[t]);
+                const uint4 hd = wu[t].hdr;
+                const uint32_t scl = hd.y & 0x3F3F3F3Fu, sch = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+                const uint2 sl = moe_b4_h(scl), shh = moe_b4_h(sch);
+                scp[t][0] = __builtin_bit_cast(mh2, sl.x);
+                scp[t][1] = __builtin_bit_cast(mh2, sl.y);
+                scp[t][2] = __builtin_bit_cast(mh2, shh.x);
+                scp[t][3] = __builtin_bit_cast(mh2, shh.y);
+                acc[t] = mf4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int G = 32 * sb + 4 * j + g;
+                const mh8 ah = *(const mh8*)(xh + ((size_t)G * pg + pc) * 8);
+                const mh8 al = *(const mh8*)(xl + ((size_t)G * pg + pc) * 8);
+                const int c = j >> 1, sh = 4 * (j & 1);
+#pragma unroll
+                for (int t = 0; t < RT; t++) {
+                    const uint32_t lo = (wu[t].q[c].x >> sh) & 0x0F0F0F0Fu, hi = (wu[t].q[c].y >> sh) & 0x0F0F0F0Fu;
+                    const _Float16 s1 = scp[t][j >> 1][j & 1];
+                    const mh2 sv = {s1, s1};
+                    const mh2 of = sv * (_Float16)(-1024.0f);
+                    const uint2 p0 = moe_nib4(lo, sv, of), p1 = moe_nib4(hi, sv, of);
+                    const mh8 bw = __builtin_bit_cast(mh8, make_uint4(p0.x, p0.y, p1.x, p1.y));
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, acc[t], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < RT; t++) {
+                const uint4 hd = wu[t].hdr;
+                const float d = f16_to_f32(hd.x & 0xffffu), dmin = f16_to_f32(hd.x >> 16);
+                const uint32_t mnl = hd.z & 0x3F3F3F3Fu,
+                               mnh = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+                const uint2 ml = moe_b4_h(mnl), mh = moe_b4_h(mnh);
+                const mh8 bm = g < 2 ? __builtin_bit_cast(mh8, make_uint4(ml.x, ml.y, mh.x, mh.y)) : mh8{};
+                const mf4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const mf4 accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm, z, 0, 0, 0);
+                const float dm32 = 32.0f * dmin;
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    out[t][v] = __builtin_fmaf(d, acc[t][v], __builtin_fmaf(-dm32, accm[v], out[t][v]));
+            }
+            // the row group is complete after its last superblock: store it
+            if (sb == nsb - 1) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int q = 4 * g + v;
+                    if (q < pg) {
+                        const int pl = list[g0 + q];
+                        const float inv = pinv[q];
+                        const int row = wrow0 + rg * RG + c16;
+                        if constexpr (GLU) {
+                            const float y = out[0][v] * inv, u = out[1][v] * inv;
+                            if (row < n) Y[(int64_t)pl * n + row] = y / (1.0f + expf(-y)) * u;
+                        } else {
+                            if (row < n) Y[(int64_t)pl * n + row] = out[0][v] * inv;
+                            if (row + 16 < n) Y[(int64_t)pl * n + row + 16] = out[1][v] * inv;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < RT; t++) out[t] = mf4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            }
+#pragma unroll
+            for (int d = 0; d + 1 < DEPTH; d++)
+#pragma unroll
+                for (int t = 0; t < RT; t++) buf[d][t] = buf[d + 1][t];
+#pragma unroll
+            for (int t = 0; t < RT; t++) buf[DEPTH - 1][t] = nxt[t];
+        }
+    }
+}
+
+template <int DEPTH, bool GLU>
+static hipError_t moe_mfma_cfg(const void* w, const float* x, float* y, const uint32_t* ids, int planes, int* ws,
+                               int* sticky, int E, int n, int K, int in_dim1, int topk, int max_slots, int pgmax,
+                               const void* w2, float* y2, int mode, bool route, int gw, hipStream_t s) {
+    const size_t shm = (size_t)pgmax * moem_plane_bytes(K) + moem_fixed_bytes(4);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_moe_mfma<DEPTH, GLU>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int rows_wg = 4 * gw * (GLU ? 16 : 32);
+    dim3 grid((n + rows_wg - 1) / rows_wg, route ? max_slots : E + 1, mode == MOE_PAIR ? 2 : 1);
+    hipLaunchKernelGGL((k_moe_mfma<DEPTH, GLU>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ids, planes, ws,
+                       sticky, E, n, K, in_dim1, topk, pgmax, (const uint8_t*)w2, y2, route ? 1 : 0, gw);
+    return hipGetLastError();
+}
+
+static bool moe_mfma_fits(int64_t k) {
+    return (k % 256) == 0 && moem_plane_bytes((int)k) + moem_fixed_bytes(4) <= MOEM_LDS + 4096;
+}
+
 // The weights of one call: w alone (MOE_ONE), w and w2 into y and y2
 // (MOE_PAIR), or silu(w . x) * (w2 . x) into y (MOE_GLU).
 struct MoeOut {
@@ -690,6 +1024,24 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
     // average) stages four planes at a time: half the LDS, so more
     // workgroups share a CU (C5: 40 us against 46 us per routed call)
     if (planes <= 4 * max_slots && pgmax > 4) pgmax = 4;
+    // Dense routing (prefill: many planes per expert) takes the fp16-MFMA
+    // kernel, 16 planes a pass; decode-like routing keeps the VALU kernel
+    // (C5, two planes an expert: 44 against 52 us for the MFMA kernel)
+    if (type == T_Q4K && moe_mfma_fits(k) && planes >= MOE_MFMA_DENSITY * max_slots) {
+        int pgm = MOEM_LDS / moem_plane_bytes((int)k);
+        pgm = pgm > 16 ? 16 : pgm < 1 ? 1 : pgm;
+        const bool mroute = planes > MOEM_FUSE_MAX;
+        if (mroute && !route) {
+            hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 2 * E * sizeof(int), s, ids, planes, (int)E, ws,
+                               sticky, y, mode == MOE_PAIR ? y2 : nullptr, (int)n);
+            if ((err = hipGetLastError()) != hipSuccess) return err;
+        }
+        if (mode == MOE_GLU)
+            return moe_mfma_cfg<2, true>(w, x, y, ids, planes, ws, sticky, (int)E, (int)n, (int)k, (int)in_dim1,
+                                         (int)topk, max_slots, pgm, w2, y2, mode, mroute, 2, s);
+        return moe_mfma_cfg<2, false>(w, x, y, ids, planes, ws, sticky, (int)E, (int)n, (int)k, (int)in_dim1,
+                                      (int)topk, max_slots, pgm, w2, y2, mode, mroute, 2, s);
+    }
     const MoeOut o{mode, w2, y2, ids, planes, sticky, route};
     const int Ei = (int)E, ni = (int)n, ki = (int)k, d1 = (int)in_dim1, tk = (int)topk;
     if (moe_stages(k)) {

@@ -540,6 +540,57 @@ def test_moe_pair_bad_id_zeroes_both(L):
         qg.indexed_moe_forward_pair(L.QTensor.quantize(_cuda(w[:, :4]), L.GgmlDType.Q4K), x, bad)
 
 
+@pytest.mark.parametrize("n,k,in_dim1_is_topk,batch", [(100, 768, True, 20), (37, 2048, False, 20),
+                                                     (256, 512, True, 300)])
+def test_moe_dense_routing(L, n, k, in_dim1_is_topk, batch):
+    """Q4_K experts with prefill-dense routing (at least 8 planes an active
+    expert: the fp16-MFMA kernel, 16 planes a pass; 1200 planes route
+    through the sorting launch): the down projection's shape (k = 768, a
+    plane per slot), ragged n, against the oracle and a float64 dense
+    reference."""
+    topk = 4
+    got, want, ref = _moe_case(L, O.Q4K, 4, n, k, batch, topk, topk if in_dim1_is_topk else 1, seed=n + k)
+    assert_rows_close(got, want, what=f"moe dense n={n} k={k}")
+    scale = np.abs(ref).max(axis=2, keepdims=True) + 1e-30
+    assert np.max(np.abs(ref - got) / scale) < 1e-5
+
+
+def test_moe_dense_pair_glu_and_bad_id(L):
+    """Dense routing through the pair and GLU launches (each pair half bit
+    for bit the single call's, the GLU silu(g) * u of them), and an
+    out-of-range id: refused by the strict call, its plane zeroed in both
+    outputs otherwise."""
+    rng = np.random.default_rng(33)
+    E, n, k, batch, topk = 4, 96, 1024, 24, 4
+    wg = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
+    wu = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
+    x = _cuda(rng.standard_normal((batch, 1, k)).astype(np.float32))
+    idn = rng.integers(0, E, (batch, topk)).astype(np.int32)
+    ids = _cuda(idn)
+    qg, qu = L.QTensor.quantize(_cuda(wg), O.Q4K), L.QTensor.quantize(_cuda(wu), O.Q4K)
+    sg = qg.indexed_moe_forward(x, ids).cpu().numpy()
+    su = qu.indexed_moe_forward(x, ids).cpu().numpy()
+    pg, pu = qg.indexed_moe_forward_pair(qu, x, ids)
+    assert np.array_equal(pg.cpu().numpy().view(np.uint32), sg.view(np.uint32))
+    assert np.array_equal(pu.cpu().numpy().view(np.uint32), su.view(np.uint32))
+    glu = qg.indexed_moe_forward_glu_as(qu, x, ids).cpu().numpy()
+    np.testing.assert_allclose(glu, _silu32(sg) * su, rtol=2e-6, atol=1e-7)
+    assert_rows_close(sg, O.matmul_indexed(O.Q4K, qg.data(), E, n, k, x.cpu().numpy(), idn.astype(np.uint32)),
+                      what="moe dense gate")
+    idn[5, 1] = E
+    bad = _cuda(idn)
+    with pytest.raises(L.LloomHipError) as e:
+        qg.indexed_moe_forward_pair(qu, x, bad)
+    assert e.value.name == "EEXPERT"
+    yg, yu = qg.indexed_moe_forward_pair(qu, x, bad, strict=False)
+    assert np.all(yg[5, 1].cpu().numpy() == 0) and np.all(yu[5, 1].cpu().numpy() == 0)
+    assert np.array_equal(yg[4].cpu().numpy().view(np.uint32), sg[4].view(np.uint32))
+    from lloom_amd.quantized import _ctx
+    from lloom_amd.lib import lib
+
+    assert lib().lloom_hip_ctx_sync(_ctx(0)) == 4
+
+
 # ---------------------------------------------------------- embedding (f4) ---
 
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
