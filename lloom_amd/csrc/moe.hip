@@ -622,7 +622,9 @@ __device__ __forceinline__ uint2 moe_b4_h(uint32_t w) {
     return make_uint2(__builtin_bit_cast(uint32_t, e), __builtin_bit_cast(uint32_t, o));
 }
 
-constexpr int MOEM_LDS = 96 * 1024;  // bytes of staged planes a pass
+// bytes of staged planes a pass: 16 planes of k = 2048 (512 tokens top-8 on
+// [128, 768, 2048]: 236 us against 273 with 11 planes a pass)
+constexpr int MOEM_LDS = 140 * 1024;
 constexpr int MOE_MFMA_DENSITY = 8;  // planes per active expert (at least) for the MFMA kernel
 constexpr int MOEM_FUSE_MAX = 1024;  // planes routed inside the kernel (an LDS list per workgroup)
 #ifndef MOEM_WAVES_EU
@@ -898,7 +900,7 @@ static hipError_t moe_mfma_cfg(const void* w, const float* x, float* y, const ui
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)k_moe_mfma<DEPTH, GLU>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, MOEM_LDS + moem_fixed_bytes(4));
         if (e != hipSuccess) return e;
         attr_set = true;
     }
@@ -1031,6 +1033,10 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
         int pgm = MOEM_LDS / moem_plane_bytes((int)k);
         pgm = pgm > 16 ? 16 : pgm < 1 ? 1 : pgm;
         const bool mroute = planes > MOEM_FUSE_MAX;
+        // row groups a wave: 4 when the planes fit one pass (more rows share
+        // a staging; 128 tokens: 73 against 81 us), else 2 (512 tokens: 236
+        // against 256)
+        const int gw = planes <= pgm * max_slots ? 4 : 2;
         if (mroute && !route) {
             hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 2 * E * sizeof(int), s, ids, planes, (int)E, ws,
                                sticky, y, mode == MOE_PAIR ? y2 : nullptr, (int)n);
@@ -1038,9 +1044,9 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
         }
         if (mode == MOE_GLU)
             return moe_mfma_cfg<2, true>(w, x, y, ids, planes, ws, sticky, (int)E, (int)n, (int)k, (int)in_dim1,
-                                         (int)topk, max_slots, pgm, w2, y2, mode, mroute, 2, s);
+                                         (int)topk, max_slots, pgm, w2, y2, mode, mroute, gw, s);
         return moe_mfma_cfg<2, false>(w, x, y, ids, planes, ws, sticky, (int)E, (int)n, (int)k, (int)in_dim1,
-                                      (int)topk, max_slots, pgm, w2, y2, mode, mroute, 2, s);
+                                      (int)topk, max_slots, pgm, w2, y2, mode, mroute, gw, s);
     }
     const MoeOut o{mode, w2, y2, ids, planes, sticky, route};
     const int Ei = (int)E, ni = (int)n, ki = (int)k, d1 = (int)in_dim1, tk = (int)topk;
