@@ -367,6 +367,25 @@ def run_details(L, cu, np, torch, dev, args):
     out["c5_moe_glu_layer"] = {"us": round(t * 1e6, 2), "GB/s": round(byts_glu / t / 1e9, 1),
                                "hbm_frac": round(byts_glu / t / 1e9 / 8000.0, 4),
                                "note": "silu(gate) * up in one routed launch, then down: 2 routed calls"}
+    # the same experts at prefill routing (not a BASELINE config): 512
+    # tokens, top-8 from seeded uniform logits; SwiGLU launch + down
+    Tp = 512
+    lg = L.synth_uniform(5, Tp * E).reshape(Tp, E)
+    idp = cu(np.argsort(-lg, axis=1, kind="stable")[:, :topk].astype(np.int32))
+    xp = cu(L.synth_normal(4002, Tp * hid)).view(Tp, 1, hid)
+    hp = cu(L.synth_normal(4003, Tp * topk * ff)).view(Tp, topk, ff)
+    ygp = torch.empty((Tp, topk, ff), device=dev)
+    ydp = torch.empty((Tp, topk, hid), device=dev)
+
+    def moe_prefill():
+        gate.indexed_moe_forward_glu_into(up, xp, idp, ygp)
+        down.indexed_moe_forward_into(hp, idp, ydp)
+
+    t = time_graph([moe_prefill], 5, 1)
+    flops = 2.0 * Tp * topk * (2 * ff * hid + hid * ff)
+    out["c5_moe_prefill_512"] = {"us": round(t * 1e6, 2), "TFLOP/s": round(flops / t / 1e12, 1),
+                                 "note": "512 tokens top-8, SwiGLU launch + down on the C5 experts "
+                                         "(dense routing: the fp16-MFMA routed-expert kernel)"}
     return out
 
 
