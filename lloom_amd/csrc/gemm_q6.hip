@@ -1,4 +1,4 @@
-// gemm_q6.hip -- Q6_K prefill-shaped matmul (many activation rows) on int8
+// gemm_q6.hip -- Q6_K prefill-shaped matmul (from 48 activation rows) on int8
 // MFMA.
 //
 // y[m, n] = sum_sb d[n,sb] * dy[m,sb] * sum_j sc[n,j] * sum_{k in j} x8[m,k] (q6[n,k] - 32)

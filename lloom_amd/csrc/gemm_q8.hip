@@ -1,5 +1,5 @@
-// gemm_q8.hip -- Q8_0 prefill-shaped matmul (m > 16 activation rows) on
-// int8 MFMA.  Built with the MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
+// gemm_q8.hip -- Q8_0 matmul from five activation rows up (prefill and
+// batched decode) on int8 MFMA.  Built with the MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
 // every result is read by the VALU epilogue right away, and from AGPRs each
 // read would cost one more instruction.
 #include <cstdlib>
