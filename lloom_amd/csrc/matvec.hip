@@ -231,6 +231,19 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         if (kc0) __syncthreads();  // the previous chunk's readers are done with LDS
         float4 xv[XN];
         prefetch_x<Tr::VT, WV, XN>(X, K, kc0, KC, m, mg, xv);
+        // With one or two Q8_K x blocks a wave, every wave's x load goes out ahead of any
+        // wave's weight loads: a barrier between them.  Otherwise the waves'
+        // issue interleaves, and a wave's x load (a cache hit) queues behind
+        // other waves' weight loads (HBM misses) in the CU's memory pipeline,
+        // holding up the quantization every dot waits for (C2 at B = 1:
+        // 4.36 -> 4.07 us, B = 2 5.07 -> 4.52; with four blocks a wave, Q6_K
+        // [2048, 8192], the barrier cost more than it saved: 7.81 -> 8.15,
+        // and for Q8_0's short blocks too: C1 5.62 -> 5.72)
+        if constexpr (TYPE != T_Q8_0 && XN <= 2) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
         // weight loads of the first PF rounds of 64 tasks (tasks past T
         // load task 0, unused; every load is unconditional, so none sits
         // under a branch and the waits stay counted): rows of several rounds
