@@ -231,7 +231,8 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         if (kc0) __syncthreads();  // the previous chunk's readers are done with LDS
         float4 xv[XN];
         prefetch_x<Tr::VT, WV, XN>(X, K, kc0, KC, m, mg, xv);
-        // With one or two Q8_K x blocks a wave, every wave's x load goes out ahead of any
+        // With one or two Q8_K x blocks a wave (Q4_K: up to four, K <= 2048),
+        // every wave's x load goes out ahead of any
         // wave's weight loads: a barrier between them.  Otherwise the waves'
         // issue interleaves, and a wave's x load (a cache hit) queues behind
         // other waves' weight loads (HBM misses) in the CU's memory pipeline,
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
         // 4.36 -> 4.07 us, B = 2 5.07 -> 4.52; with four blocks a wave, Q6_K
         // [2048, 8192], the barrier cost more than it saved: 7.81 -> 8.15,
         // and for Q8_0's short blocks too: C1 5.62 -> 5.72)
-        if constexpr (TYPE != T_Q8_0 && XN <= 2) {
+        if (TYPE != T_Q8_0 && (XN <= 2 || (TYPE == T_Q4K && KC <= 2048))) {  // uniform
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
@@ -584,10 +585,11 @@ __global__ __launch_bounds__(128 * KS) void k_mv_fused(const uint8_t* __restrict
     const int kw = wave % KS, rt = wave / KS;
     const int row = (blockIdx.x * 2 + rt) * 16 + c16;
     const uint8_t* wrow = W + (int64_t)min(row, n - 1) * ((int64_t)KS * BB);
-    MfL<TYPE> wl;
-    mf_load_l<TYPE>(wrow + (int64_t)kw * BB, g, wl);
     // x blocks q = mi * KS + sb, q = wave + WV * t (a block past the end
-    // reloads block 0 and is not stored)
+    // reloads block 0 and is not stored); every wave's x loads go out ahead
+    // of every weight load (a barrier between them), so the quantization
+    // does not wait behind other waves' weight loads in the CU's memory
+    // pipeline
     const int nblk = m * KS;
     float4 xv[XN];
 #pragma unroll
@@ -596,6 +598,11 @@ __global__ __launch_bounds__(128 * KS) void k_mv_fused(const uint8_t* __restrict
         const int qq = q < nblk ? q : 0;
         xv[t] = *(const float4*)(X + (int64_t)(qq / KS) * K + (qq % KS) * 256 + 4 * lane);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    MfL<TYPE> wl;
+    mf_load_l<TYPE>(wrow + (int64_t)kw * BB, g, wl);
     __builtin_amdgcn_sched_barrier(0);
     // element 4*lane.. of a block: sub-block lane / 8, lane group (lane % 8) / 2,
     // byte 4 * (lane % 2) of the group's 8 (k_quantize_split_q8k's layout)
