@@ -17,7 +17,8 @@ B=1), algorithmic bytes per launch over its average launch time.
 
 `details` adds the other BASELINE configs (C1 Q8_0 decode, C3 Q4_K prefill
 TFLOP/s, C4 decoder-layer decode, C5 routed experts) measured the same way,
-plus the prefill of the Q8_0 and Q6_K weights on their own GEMMs, and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
+plus the prefill of the Q8_0 and Q6_K weights on their own GEMMs and the C5
+experts at prefill routing (512 tokens), and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
 (oracle/kq_cpubase.c) on the same weights on a bounded sample.
 """
 import argparse
