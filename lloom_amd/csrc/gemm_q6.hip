@@ -44,10 +44,6 @@ static size_t q6_prep_bytes(int64_t m, int64_t k) {
     return (((size_t)m * k + 255) & ~(size_t)255) + (((size_t)(k / 256) * mp + 128) * sizeof(float) + 255 & ~(size_t)255);
 }
 
-// The prepared activations, then room for up to 8 split-K partial sums.
-size_t q6_gemm_workspace_bytes(int64_t n, int64_t k, int64_t m) {
-    return q6_prep_bytes(m, k) + (size_t)8 * m * n * sizeof(float);
-}
 
 // One wave a (row, superblock).
 __global__ __launch_bounds__(256) void k_gemm_prep_q6(const float* __restrict__ x, int8_t* __restrict__ xq,
@@ -375,6 +371,35 @@ static int q6_tile_env() {
     return v;
 }
 
+// The tile for m rows (LLOOM_HIP_Q6_TILE overrides): to 128 rows 64 x 64,
+// past that 128 x 128 (measurements below, at the launch).
+static int q6_tile_of(int64_t m) {
+    const int t = q6_tile_env();
+    return t >= 0 ? t : m <= 128 ? 2 : 0;
+}
+
+// The K splits a launch of m rows will take (1: no partial sums).
+static int q6_launch_splits(int64_t n, int64_t k, int64_t m) {
+    int64_t tiles;
+    switch (q6_tile_of(m)) {
+        case 1: tiles = q6_tiles<Q6Cfg<2, 2, 2, 2, 2>>(n, m); break;
+        case 2: tiles = q6_tiles<Q6Cfg<2, 2, 1, 1, 3>>(n, m); break;
+        case 3: tiles = q6_tiles<Q6Cfg<2, 4, 1, 1, 3>>(n, m); break;
+        default: tiles = q6_tiles<Q6Cfg<2, 4, 2, 1, 2>>(n, m); break;
+    }
+    const int64_t nsb = k / 256;
+    const int sp = q6_splits(tiles, nsb);
+    const int64_t sps = (nsb + sp - 1) / sp;
+    return (int)((nsb + sps - 1) / sps);
+}
+
+// The prepared activations, then the split-K partial sums when the launch
+// splits K.
+size_t q6_gemm_workspace_bytes(int64_t n, int64_t k, int64_t m) {
+    const int sp = q6_launch_splits(n, k, m);
+    return q6_prep_bytes(m, k) + (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0);
+}
+
 hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
                           int epi, hipStream_t s) {
     const Q6Ptrs p = q6_ptrs(qbuf, m, k);
@@ -384,13 +409,12 @@ hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, in
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     float* psum = (float*)((uint8_t*)qbuf + q6_prep_bytes(m, k));
-    int tile = q6_tile_env();
+    const int tile = q6_tile_of(m);
     // by m (measured with the prep launch, graph replay, [2048, 8192] /
     // [8192, 2048]): to 128 rows 64 x 64 tiles, 3 stages (m = 64 22.3 / 23.2
     // us against 34.8 / 35.5 for 128 x 128, m = 128 34.4 / 30.7); past that
     // 128 x 128 with 8 waves (m = 256 42.4 / 44.8, m = 2048 219.5 / 222.8
     // us against 59.2 / 54.9 and 383 / 405 for 64 x 64).  Few tiles split K.
-    if (tile < 0) tile = m <= 128 ? 2 : 0;
     switch (tile) {
         case 1: return launch_q6_cfg<Q6Cfg<2, 2, 2, 2, 2>>(w, p, y, n, k, m, epi, s, psum);  // 128 x 128, 4 waves
         case 2: return launch_q6_cfg<Q6Cfg<2, 2, 1, 1, 3>>(w, p, y, n, k, m, epi, s, psum);  // 64 x 64, 3 stages
