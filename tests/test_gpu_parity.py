@@ -451,6 +451,32 @@ def _silu32(v):
     return (v / (np.float32(1) + np.exp(-v))).astype(np.float32)
 
 
+@pytest.mark.parametrize("m", [64, 160])
+def test_q6k_split_k_epilogues(L, m):
+    """SiLU and multiply-into stores where the Q6_K GEMM splits K over
+    workgroups (one or two column tiles, 16 superblocks a row): the stores
+    are applied once, by the pass that adds the partial sums in split order,
+    and a second, smaller call reuses the workspace the first one sized."""
+    rng = np.random.default_rng(70 + m)
+    n, k = 64, 4096
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    qt = L.QTensor.quantize(_cuda(w), O.Q6K)
+    mm = L.QMatMul.from_qtensor(qt)
+    xd = _cuda(x)
+    plain = mm.forward(xd).cpu().numpy()
+    want = O.matmul(O.Q6K, x, qt.data(), n)
+    assert_rows_close(plain, want, what=f"q6k split-k m={m}")
+    silu = mm.forward_silu(xd).cpu().numpy()
+    np.testing.assert_allclose(silu, _silu32(plain), rtol=2e-6, atol=1e-7)
+    gate = rng.standard_normal((m, n)).astype(np.float32)
+    g = _cuda(gate)
+    mm.forward_mul_into(xd, g)
+    assert np.array_equal(g.cpu().numpy().view(np.uint32), (gate * plain).astype(np.float32).view(np.uint32))
+    small = mm.forward(_cuda(x[:48])).cpu().numpy()
+    assert_rows_close(small, want[:48], what="q6k split-k after a larger call")
+
+
 @pytest.mark.parametrize("dt", [O.Q8_0, O.Q4K, O.Q6K])
 @pytest.mark.parametrize("m", [1, 2, 5, 16, 40, 64, 200])
 def test_forward_silu_and_mul_into(L, dt, m):
