@@ -134,8 +134,10 @@ int lloom_hip_dequantize(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, i
  * x f32.  Replaces QCudaStorage::fwd (quantized/cuda.rs:862-894).  Each call
  * quantizes x to the VecDotType exactly as the CPU arm does; the dots then
  * run in integer arithmetic with f32 scales, within 1e-3 * max|y row| of the
- * CPU result.  x_dtype / y_dtype: F32 only in this version (F16 is refused
- * by name: LLOOM_HIP_EDTYPE). */
+ * CPU result.  x_dtype / y_dtype: F32 or F16 each.  F16 activations are
+ * the CPU arm's matmul_t_f16 (mod.rs:722,761; k_quants.rs:2802-2835): x
+ * widened to f32 exactly, then the f32 path; an F16 y is each f32 sum
+ * rounded to nearest-even.  The conversions run in the workspace. */
 int lloom_hip_qmatmul(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
                       const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype,
                       void* stream);
@@ -156,6 +158,27 @@ enum { LLOOM_HIP_STORE_PLAIN = 0, LLOOM_HIP_STORE_SILU = 1, LLOOM_HIP_STORE_MUL_
 int lloom_hip_qmatmul_store(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
                             const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, int store,
                             void* stream);
+
+/* Workspace a lloom_hip_qmatmul call of this shape needs on ctx (NULL: a
+ * new context's defaults), so a caller can reserve it before capturing the
+ * call into a graph.  The reference's counterpart is the CUDA arm's
+ * grow-only workspace (quantized/fast_mmvq.rs:49-80), sized on first use. */
+int lloom_hip_qmatmul_workspace_bytes(lloom_hip_ctx* ctx, int ggml_type, int64_t n, int64_t k, int64_t m,
+                                      int x_dtype, int y_dtype, size_t* bytes);
+/* Grow the context workspace to at least `bytes` now.  A call that would
+ * grow it while its stream is being captured fails with LLOOM_HIP_ENOMEM
+ * instead; outgrown workspaces stay allocated until lloom_hip_ctx_destroy
+ * (graphs captured earlier keep using theirs). */
+int lloom_hip_ctx_reserve(lloom_hip_ctx* ctx, size_t bytes);
+/* Bytes the context workspace holds now. */
+int lloom_hip_ctx_workspace_bytes(lloom_hip_ctx* ctx, size_t* bytes);
+
+/* Tensor::to_dtype between F32 and F16 on the device (f32 -> f16 round to
+ * nearest even, as half::f16::from_f32), for the casts the reference makes
+ * around this path: indexed_moe_forward_as casting x to `act`
+ * (mod.rs:1567-1571).  src and dst 16-byte aligned. */
+int lloom_hip_cast(lloom_hip_ctx* ctx, const void* src_dev, int src_dtype, void* dst_dev, int dst_dtype,
+                   int64_t count, void* stream);
 
 /* ------------------------------------------------------- routed experts --
  * QTensor::indexed_moe_forward{,_with,_as} (mod.rs:1560-1645), CPU arm

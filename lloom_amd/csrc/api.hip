@@ -15,27 +15,18 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/lloom_hip.h"
 #include "kernels.hpp"
 #include "kq_common.hpp"
+#include "api_internal.hpp"
 
 using namespace lloom;
 
-struct lloom_hip_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    void* ws = nullptr;  // grow-only workspace
-    size_t ws_bytes = 0;
-    int* flags = nullptr;  // [0] sticky expert-id error
-    int mv_rows_max = 16;
-    int prefill_mma = GEMM_F16;
-    std::mutex mu;
-};
-
 static thread_local std::string g_err;
 
-static int fail(int code, const char* fmt, ...) {
+int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -45,11 +36,6 @@ static int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-#define HIP_OK(expr)                                                                         \
-    do {                                                                                     \
-        hipError_t e_ = (expr);                                                              \
-        if (e_ != hipSuccess) return fail(LLOOM_HIP_EHIP, "%s: %s", #expr, hipGetErrorString(e_)); \
-    } while (0)
 
 // The caller's stream, verbatim: NULL is HIP's null stream (torch's default
 // stream handle is 0), never silently another stream.
@@ -73,19 +59,27 @@ static const char* type_name(int t) {
 }
 
 // Workspace of at least `bytes`, 256-byte aligned; grows, never shrinks
-// (the CUDA arm's per-device workspace, quantized/fast_mmvq.rs:49-80).
-static int ensure_ws(lloom_hip_ctx* ctx, size_t bytes, void** out) {
+// (the CUDA arm's per-device workspace, quantized/fast_mmvq.rs:49-80).  A
+// growth allocates a new buffer of at least twice the old size and retires
+// the old one until the context is destroyed (see lloom_hip_ctx).  Growth is
+// refused while `s` is being captured into a graph: an allocation there
+// would not be part of the graph, so the caller reserves the workspace first
+// (lloom_hip_ctx_reserve).
+static int ensure_ws(lloom_hip_ctx* ctx, size_t bytes, hipStream_t s, void** out) {
     if (bytes > ctx->ws_bytes) {
-        if (ctx->ws) {
-            // earlier calls may still read it on any stream
-            HIP_OK(hipDeviceSynchronize());
-            HIP_OK(hipFree(ctx->ws));
-            ctx->ws = nullptr;
-            ctx->ws_bytes = 0;
-        }
-        size_t want = (bytes + 0xFFFFF) & ~(size_t)0xFFFFF;
-        if (hipMalloc(&ctx->ws, want) != hipSuccess)
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+            return fail(LLOOM_HIP_ENOMEM,
+                        "the call needs a workspace of %zu bytes and the context holds %zu: it cannot grow while "
+                        "the stream is being captured (reserve it first with lloom_hip_ctx_reserve)",
+                        bytes, ctx->ws_bytes);
+        size_t want = bytes > 2 * ctx->ws_bytes ? bytes : 2 * ctx->ws_bytes;
+        want = (want + 0xFFFFF) & ~(size_t)0xFFFFF;
+        void* fresh = nullptr;
+        if (hipMalloc(&fresh, want) != hipSuccess)
             return fail(LLOOM_HIP_ENOMEM, "workspace allocation of %zu bytes failed", want);
+        if (ctx->ws) ctx->retired.push_back(ctx->ws);
+        ctx->ws = fresh;
         ctx->ws_bytes = want;
     }
     *out = ctx->ws;
@@ -130,8 +124,9 @@ int lloom_hip_ctx_create(int device, lloom_hip_ctx** out) {
 int lloom_hip_ctx_destroy(lloom_hip_ctx* ctx) {
     if (!ctx) return LLOOM_HIP_OK;
     (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipDeviceSynchronize();  // calls may have queued work on any stream
     if (ctx->ws) (void)hipFree(ctx->ws);
+    for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->flags) (void)hipFree(ctx->flags);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -254,13 +249,39 @@ int lloom_hip_dequantize(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, i
     return LLOOM_HIP_OK;
 }
 
-static int qmatmul_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
-                        const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, int epi, void* stream) {
+}  // extern "C"
+
+// The route a qmatmul call takes and the workspace it needs.  Activations
+// in F16 (matmul_t_f16, k_quants.rs:2802-2835: the f16 lhs converted to f32,
+// quantized to the VecDotType and dotted exactly as the f32 path; each f32
+// sum rounded to f16) are converted into the workspace first, and F16
+// outputs are formed in f32 in the workspace and rounded at the end.
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+QmmPlan qmm_plan(int mv_rows_max, int prefill_mma, int ggml_type, int64_t n, int64_t k, int64_t m,
+                        int x_dtype, int y_dtype) {
+    QmmPlan p;
+    // Q8_0 from 5 rows takes the GEMM (the decode kernel's time grows with
+    // the rows, 10.6 us at m = 4 and 22.1 at m = 8 on [8192, 2048]; the
+    // split-K GEMM with its activation prep is 11.1 us from m = 3 to 9)
+    p.decode = m <= mv_rows_max && !(ggml_type == T_Q8_0 && m >= Q8_GEMM_MIN_ROWS && q8_gemm_fits(n, k, m));
+    p.path_bytes = p.decode ? matvec_workspace_bytes(ggml_type, n, k, m)
+                            : gemm_workspace_bytes(ggml_type, n, k, m, prefill_mma);
+    p.x32_off = align256(p.path_bytes);
+    p.y32_off = p.x32_off + (x_dtype == T_F16 ? align256((size_t)m * k * sizeof(float)) : 0);
+    p.total = p.y32_off + (y_dtype == T_F16 ? align256((size_t)m * n * sizeof(float)) : 0);
+    return p;
+}
+
+int qmatmul_check(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                         const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, int epi) {
     if (!ctx || !w_dev || !x_dev || !y_dev) return fail(LLOOM_HIP_EINVAL, "qmatmul: null argument");
     if (!is_weight_type(ggml_type))
         return fail(LLOOM_HIP_EDTYPE, "qmatmul: weight dtype %s (%d) is not supported on the HIP quantized path (Q8_0, Q4K, Q6K)", type_name(ggml_type), ggml_type);
-    if (x_dtype != T_F32 || y_dtype != T_F32)
-        return fail(LLOOM_HIP_EDTYPE, "qmatmul: activation dtypes %s -> %s: only F32 -> F32 is supported", type_name(x_dtype), type_name(y_dtype));
+    if ((x_dtype != T_F32 && x_dtype != T_F16) || (y_dtype != T_F32 && y_dtype != T_F16))
+        return fail(LLOOM_HIP_EDTYPE, "qmatmul: activation dtypes %s -> %s: x and y must each be F32 or F16", type_name(x_dtype), type_name(y_dtype));
+    (void)epi;
     int be = block_elems(ggml_type);
     if (n <= 0 || k <= 0 || m <= 0)
         return fail(LLOOM_HIP_EINVAL, "qmatmul: empty shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
@@ -269,29 +290,48 @@ static int qmatmul_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, in
     if ((uintptr_t)w_dev % (ggml_type == T_Q4K ? 16 : 4))
         return fail(LLOOM_HIP_EINVAL, "qmatmul: weight pointer is not %d-byte aligned", ggml_type == T_Q4K ? 16 : 4);
     if ((uintptr_t)x_dev % 16) return fail(LLOOM_HIP_EINVAL, "qmatmul: x must be 16-byte aligned");
-    HIP_OK(hipSetDevice(ctx->device));
-    hipStream_t s = pick_stream(ctx, stream);
-    std::lock_guard<std::mutex> lock(ctx->mu);
-    // Q8_0 from 5 rows takes the GEMM (the decode kernel's time grows with
-    // the rows, 10.6 us at m = 4 and 22.1 at m = 8 on [8192, 2048]; the
-    // split-K GEMM with its activation prep is 11.1 us from m = 3 to 9)
-    const bool decode = m <= ctx->mv_rows_max &&
-                        !(ggml_type == T_Q8_0 && m >= Q8_GEMM_MIN_ROWS && q8_gemm_fits(n, k, m));
-    void* ws = nullptr;
-    size_t need = decode ? matvec_workspace_bytes(ggml_type, n, k, m)
-                         : gemm_workspace_bytes(ggml_type, n, k, m, ctx->prefill_mma);
-    if (need) {
-        int rc = ensure_ws(ctx, need, &ws);
-        if (rc) return rc;
-    }
-    if (decode)
-        HIP_OK(launch_matvec(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, epi, s));
-    else
-        HIP_OK(launch_gemm(ggml_type, w_dev, (const float*)x_dev, (float*)y_dev, n, k, m, ws, ctx->prefill_mma, epi, s));
+    if (y_dtype == T_F16 && (uintptr_t)y_dev % 16) return fail(LLOOM_HIP_EINVAL, "qmatmul: an F16 y must be 16-byte aligned");
     return LLOOM_HIP_OK;
 }
 
-}  // extern "C"
+// The call on a workspace `ws` of `ws_cap` bytes (the plan's total fits).
+int qmatmul_run(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k, const void* x_dev,
+                       int x_dtype, int64_t m, void* y_dev, int y_dtype, int epi, hipStream_t s, const QmmPlan& p,
+                       void* ws, size_t ws_cap) {
+    const float* x = (const float*)x_dev;
+    float* y = (float*)y_dev;
+    if (x_dtype == T_F16) {
+        float* x32 = (float*)((uint8_t*)ws + p.x32_off);
+        HIP_OK(launch_cast(T_F16, x_dev, T_F32, x32, m * k, s));
+        x = x32;
+    }
+    if (y_dtype == T_F16) {
+        y = (float*)((uint8_t*)ws + p.y32_off);
+        // the multiply-into store reads y: its f16 values, widened exactly
+        if (epi == EPI_MUL_INTO) HIP_OK(launch_cast(T_F16, y_dev, T_F32, y, m * n, s));
+    }
+    if (p.decode)
+        HIP_OK(launch_matvec(ggml_type, w_dev, x, y, n, k, m, ws, epi, s));
+    else
+        HIP_OK(launch_gemm(ggml_type, w_dev, x, y, n, k, m, ws, p.total > p.x32_off ? p.x32_off : ws_cap,
+                           ctx->prefill_mma, epi, s));
+    if (y_dtype == T_F16) HIP_OK(launch_cast(T_F32, y, T_F16, y_dev, m * n, s));
+    return LLOOM_HIP_OK;
+}
+
+static int qmatmul_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                        const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, int epi, void* stream) {
+    if (int rc = qmatmul_check(ctx, ggml_type, w_dev, n, k, x_dev, x_dtype, m, y_dev, y_dtype, epi)) return rc;
+    HIP_OK(hipSetDevice(ctx->device));
+    hipStream_t s = pick_stream(ctx, stream);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    const QmmPlan p = qmm_plan(ctx->mv_rows_max, ctx->prefill_mma, ggml_type, n, k, m, x_dtype, y_dtype);
+    void* ws = nullptr;
+    if (p.total) {
+        if (int rc = ensure_ws(ctx, p.total, s, &ws)) return rc;
+    }
+    return qmatmul_run(ctx, ggml_type, w_dev, n, k, x_dev, x_dtype, m, y_dev, y_dtype, epi, s, p, ws, ctx->ws_bytes);
+}
 
 static int moe_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, const void* w2_dev, int64_t n_experts,
                     int64_t n, int64_t k, const float* x_dev, int64_t batch, int64_t in_dim1,
@@ -312,6 +352,50 @@ int lloom_hip_qmatmul_store(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev
         return fail(LLOOM_HIP_EINVAL, "qmatmul_store: store %d is not PLAIN (0), SILU (1) or MUL_INTO (2)", store);
     const int epi = store == LLOOM_HIP_STORE_SILU ? EPI_SILU : store == LLOOM_HIP_STORE_MUL_INTO ? EPI_MUL_INTO : EPI_STORE;
     return qmatmul_impl(ctx, ggml_type, w_dev, n, k, x_dev, x_dtype, m, y_dev, y_dtype, epi, stream);
+}
+
+int lloom_hip_qmatmul_workspace_bytes(lloom_hip_ctx* ctx, int ggml_type, int64_t n, int64_t k, int64_t m, int x_dtype,
+                                      int y_dtype, size_t* bytes) {
+    if (!bytes) return fail(LLOOM_HIP_EINVAL, "qmatmul_workspace_bytes: null output");
+    if (!is_weight_type(ggml_type))
+        return fail(LLOOM_HIP_EDTYPE, "qmatmul_workspace_bytes: weight dtype %s (%d) is not supported", type_name(ggml_type), ggml_type);
+    if ((x_dtype != T_F32 && x_dtype != T_F16) || (y_dtype != T_F32 && y_dtype != T_F16))
+        return fail(LLOOM_HIP_EDTYPE, "qmatmul_workspace_bytes: x and y must each be F32 or F16");
+    if (n <= 0 || k <= 0 || m <= 0 || k % block_elems(ggml_type))
+        return fail(LLOOM_HIP_ESHAPE, "qmatmul_workspace_bytes: bad shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+    const int rows_max = ctx ? ctx->mv_rows_max : 16;
+    int mma = GEMM_F16;
+    if (ctx) mma = ctx->prefill_mma;
+    else if (const char* e = getenv("LLOOM_HIP_PREFILL_MMA")) mma = strcmp(e, "int8") == 0 ? GEMM_INT8 : GEMM_F16;
+    *bytes = qmm_plan(rows_max, mma, ggml_type, n, k, m, x_dtype, y_dtype).total;
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_ctx_reserve(lloom_hip_ctx* ctx, size_t bytes) {
+    if (!ctx) return fail(LLOOM_HIP_EINVAL, "ctx_reserve: null context");
+    HIP_OK(hipSetDevice(ctx->device));
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    void* ws = nullptr;
+    return bytes ? ensure_ws(ctx, bytes, nullptr, &ws) : LLOOM_HIP_OK;
+}
+
+int lloom_hip_ctx_workspace_bytes(lloom_hip_ctx* ctx, size_t* bytes) {
+    if (!ctx || !bytes) return fail(LLOOM_HIP_EINVAL, "ctx_workspace_bytes: null argument");
+    *bytes = ctx->ws_bytes;
+    return LLOOM_HIP_OK;
+}
+
+int lloom_hip_cast(lloom_hip_ctx* ctx, const void* src_dev, int src_dtype, void* dst_dev, int dst_dtype, int64_t count,
+                   void* stream) {
+    if (!ctx || (count && (!src_dev || !dst_dev))) return fail(LLOOM_HIP_EINVAL, "cast: null argument");
+    if (!((src_dtype == T_F32 && dst_dtype == T_F16) || (src_dtype == T_F16 && dst_dtype == T_F32)))
+        return fail(LLOOM_HIP_EDTYPE, "cast: %s -> %s is not F32 <-> F16", type_name(src_dtype), type_name(dst_dtype));
+    if (count < 0) return fail(LLOOM_HIP_EINVAL, "cast: negative count");
+    if ((uintptr_t)src_dev % 16 || (uintptr_t)dst_dev % 16) return fail(LLOOM_HIP_EINVAL, "cast: src and dst must be 16-byte aligned");
+    if (count == 0) return LLOOM_HIP_OK;
+    HIP_OK(hipSetDevice(ctx->device));
+    HIP_OK(launch_cast(src_dtype, src_dev, dst_dtype, dst_dev, count, pick_stream(ctx, stream)));
+    return LLOOM_HIP_OK;
 }
 
 }  // extern "C"
@@ -343,7 +427,7 @@ static int moe_impl(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, const 
     hipStream_t s = pick_stream(ctx, stream);
     std::lock_guard<std::mutex> lock(ctx->mu);
     void* ws = nullptr;
-    int rc = ensure_ws(ctx, moe_workspace_bytes(n_experts, batch * topk, n, k, mode), &ws);
+    int rc = ensure_ws(ctx, moe_workspace_bytes(n_experts, batch * topk, n, k, mode), s, &ws);
     if (rc) return rc;
     HIP_OK(launch_moe(ggml_type, w_dev, n_experts, n, k, x_dev, batch, in_dim1, ids_dev, topk, y_dev, (int*)ws,
                       ctx->flags, mode, w2_dev, y2_dev, s));

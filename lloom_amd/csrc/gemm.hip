@@ -1020,7 +1020,8 @@ static int64_t skinny_max_rows() {
 }
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                       void* qbuf, int mode, int epi, hipStream_t s) {
+                       void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s) {
+    if (gemm_workspace_bytes(type, n, k, m, mode) > ws_cap) return hipErrorInvalidValue;
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
@@ -1050,7 +1051,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
         return hipGetLastError();
     }
     if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m))
-        return launch_q6_gemm(w, x, y, n, k, m, qbuf, epi, s);
+        return launch_q6_gemm(w, x, y, n, k, m, qbuf, ws_cap, epi, s);
     if (use_mq(type, m)) return launch_mq(type, w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);

@@ -334,7 +334,7 @@ static int64_t q6_tiles(int64_t n, int64_t m) {
 
 template <class C>
 static hipError_t launch_q6_cfg(const void* w, const Q6Ptrs& p, float* y, int64_t n, int64_t k, int64_t m, int epi,
-                                hipStream_t s, float* psum) {
+                                hipStream_t s, float* psum, int sp) {
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e =
@@ -343,9 +343,7 @@ static hipError_t launch_q6_cfg(const void* w, const Q6Ptrs& p, float* y, int64_
         attr_set = true;
     }
     const int64_t tiles = q6_tiles<C>(n, m), nsb = k / 256;
-    int sp = q6_splits(tiles, nsb);
     const int sps = (int)((nsb + sp - 1) / sp);
-    sp = (int)((nsb + sps - 1) / sps);  // no split left empty
     hipLaunchKernelGGL(k_gemm_q6k<C>, dim3((unsigned)tiles, sp), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.xq,
                        p.dyt, y, (int)m, (int)n, (int)k, (int)p.mp, epi, sps, sp > 1 ? psum : nullptr);
     hipError_t e = hipGetLastError();
@@ -401,7 +399,11 @@ size_t q6_gemm_workspace_bytes(int64_t n, int64_t k, int64_t m) {
 }
 
 hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
-                          int epi, hipStream_t s) {
+                          size_t ws_cap, int epi, hipStream_t s) {
+    // the split count sizes the partial-sum region: one computation serves
+    // the workspace size and the launch, and the caller's capacity is checked
+    const int sp = q6_launch_splits(n, k, m);
+    if (q6_prep_bytes(m, k) + (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0) > ws_cap) return hipErrorInvalidValue;
     const Q6Ptrs p = q6_ptrs(qbuf, m, k);
     const int64_t nb = m * (k / 256);
     hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.xq, p.dyt, (int)m, (int)k,
@@ -416,10 +418,10 @@ hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, in
     // 128 x 128 with 8 waves (m = 256 42.4 / 44.8, m = 2048 219.5 / 222.8
     // us against 59.2 / 54.9 and 383 / 405 for 64 x 64).  Few tiles split K.
     switch (tile) {
-        case 1: return launch_q6_cfg<Q6Cfg<2, 2, 2, 2, 2>>(w, p, y, n, k, m, epi, s, psum);  // 128 x 128, 4 waves
-        case 2: return launch_q6_cfg<Q6Cfg<2, 2, 1, 1, 3>>(w, p, y, n, k, m, epi, s, psum);  // 64 x 64, 3 stages
-        case 3: return launch_q6_cfg<Q6Cfg<2, 4, 1, 1, 3>>(w, p, y, n, k, m, epi, s, psum);  // 64 x 128, 8 waves
-        default: return launch_q6_cfg<Q6Cfg<2, 4, 2, 1, 2>>(w, p, y, n, k, m, epi, s, psum);  // 128 x 128, 8 waves
+        case 1: return launch_q6_cfg<Q6Cfg<2, 2, 2, 2, 2>>(w, p, y, n, k, m, epi, s, psum, sp);  // 128 x 128, 4 waves
+        case 2: return launch_q6_cfg<Q6Cfg<2, 2, 1, 1, 3>>(w, p, y, n, k, m, epi, s, psum, sp);  // 64 x 64, 3 stages
+        case 3: return launch_q6_cfg<Q6Cfg<2, 4, 1, 1, 3>>(w, p, y, n, k, m, epi, s, psum, sp);  // 64 x 128, 8 waves
+        default: return launch_q6_cfg<Q6Cfg<2, 4, 2, 1, 2>>(w, p, y, n, k, m, epi, s, psum, sp);  // 128 x 128, 8 waves
     }
 }
 

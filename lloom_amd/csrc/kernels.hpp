@@ -11,6 +11,9 @@ namespace lloom {
 hipError_t launch_quantize_act(int vec_dot_type, const float* x, void* out, int64_t elems, hipStream_t s);
 hipError_t launch_quantize_weights(int type, const float* x, void* out, int64_t elems, hipStream_t s);
 hipError_t launch_dequantize(int type, const void* w, void* y, int out_dtype, int64_t elems, hipStream_t s);
+// F32 <-> F16 conversion of count elements (f32 -> f16 round-to-nearest-even);
+// src and dst 16-byte aligned.
+hipError_t launch_cast(int src_t, const void* src, int dst_t, void* dst, int64_t count, hipStream_t s);
 // Rows ids[0 .. n_ids) of an [rows, hidden] weight, dequantized; a bad id
 // gives a zero row and sets flag[0] and flag[1].
 hipError_t launch_embedding(int type, const void* w, int64_t rows, int64_t hidden, const uint32_t* ids, int64_t n_ids,
@@ -41,7 +44,7 @@ hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t 
 // other types through decode tiles; qbuf is workspace for the prepared x.
 constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
-                       void* qbuf, int mode, int epi, hipStream_t s);
+                       void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode);
 // gemm_q6.hip: Q6_K from Q6_GEMM_MIN_ROWS rows (below, k_mv_mfma with 64
 // activation rows a layer: m = 32 22.6 / 17.0 us against 21.7 for the GEMM
@@ -50,7 +53,7 @@ constexpr int Q6_GEMM_MIN_ROWS = 48;
 bool q6_gemm_fits(int64_t n, int64_t k, int64_t m);
 size_t q6_gemm_workspace_bytes(int64_t n, int64_t k, int64_t m);
 hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
-                          int epi, hipStream_t s);
+                          size_t ws_cap, int epi, hipStream_t s);
 // gemm_q8.hip: Q8_0 from Q8_GEMM_MIN_ROWS rows (K in 256-element steps).
 constexpr int Q8_GEMM_MIN_ROWS = 5;
 bool q8_gemm_fits(int64_t n, int64_t k, int64_t m);

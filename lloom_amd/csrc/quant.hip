@@ -615,4 +615,48 @@ hipError_t launch_embedding(int type, const void* w, int64_t rows, int64_t hidde
     return dequant_t<float>(type, w, (float*)y, elems, rm, s);
 }
 
+// ---------------------------------------------------------------- cast --
+// Tensor::to_dtype between F32 and F16 (the cast the CPU arm's callers make
+// around a quantized matmul: matmul_t_f16 converts its f16 lhs to f32 first
+// and its f32 sums to f16 last, k_quants.rs:2802-2835; indexed_moe_forward_as
+// casts x to act first, mod.rs:1567-1571).  f16 -> f32 is exact, f32 -> f16
+// round-to-nearest-even (half::f16::from_f32).  Four elements a lane.
+__global__ __launch_bounds__(256) void k_cast_f32_f16(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                      int64_t count) {
+    const int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (i + 4 <= count) {
+        const float4 v = *(const float4*)(x + i);
+        uint2 o;
+        o.x = (uint32_t)f32_to_f16(v.x) | ((uint32_t)f32_to_f16(v.y) << 16);
+        o.y = (uint32_t)f32_to_f16(v.z) | ((uint32_t)f32_to_f16(v.w) << 16);
+        *(uint2*)(y + i) = o;
+    } else {
+        for (int64_t j = i; j < count; j++) y[j] = f32_to_f16(x[j]);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_cast_f16_f32(const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                      int64_t count) {
+    const int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (i + 4 <= count) {
+        const uint2 v = *(const uint2*)(x + i);
+        *(float4*)(y + i) = make_float4(f16_to_f32(v.x & 0xffffu), f16_to_f32(v.x >> 16), f16_to_f32(v.y & 0xffffu),
+                                        f16_to_f32(v.y >> 16));
+    } else {
+        for (int64_t j = i; j < count; j++) y[j] = f16_to_f32(x[j]);
+    }
+}
+
+hipError_t launch_cast(int src_t, const void* src, int dst_t, void* dst, int64_t count, hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)((count + 1023) / 1024);
+    if (src_t == T_F32 && dst_t == T_F16)
+        hipLaunchKernelGGL(k_cast_f32_f16, dim3(grid), dim3(256), 0, s, (const float*)src, (uint16_t*)dst, count);
+    else if (src_t == T_F16 && dst_t == T_F32)
+        hipLaunchKernelGGL(k_cast_f16_f32, dim3(grid), dim3(256), 0, s, (const uint16_t*)src, (float*)dst, count);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 }  // namespace lloom

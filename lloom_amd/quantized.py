@@ -6,7 +6,7 @@ Names, argument meaning and refusals follow lloom-tensor/src/quantized/mod.rs:
   QTensor.from_data    mod.rs:136-223   (QStorage::from_data: an upload)
   QTensor.dequantize   mod.rs:1065-1086 (and dequantize_f16)
   QTensor.indexed_moe_forward{,_with,_as}  mod.rs:1560-1645
-  QTensor.indexed_moe_forward_pair / _glu_as  mod.rs:1365-1531
+  QTensor.indexed_moe_forward_pair{,_with,_as} / _glu_as  mod.rs:1365-1531
   QTensor.embedding    mod.rs:1101-1137
   QMatMul.from_qtensor / forward          mod.rs:1698-1729, 2022-2025
   QMatMul.forward_silu / forward_mul_into, MvStore  mod.rs:1667-1696, 2102-2156
@@ -90,6 +90,48 @@ def _stream(t):
 
 def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
+
+
+_ACT_IDS = {torch.float32: 0, torch.float16: 1}
+
+
+def _act_id(dtype, what):
+    if dtype not in _ACT_IDS:
+        raise LloomHipError(2, f"{what}: {dtype} is not an activation dtype of the HIP arm (F32 or F16)")
+    return _ACT_IDS[dtype]
+
+
+def _cast(t, dtype):
+    """Tensor::to_dtype between f32 and f16 on the device (RNE), through the
+    C ABI; the same tensor when it already has that dtype."""
+    if t.dtype == dtype:
+        return t
+    src_id, dst_id = _act_id(t.dtype, "cast"), _act_id(dtype, "cast")
+    t = t.contiguous()
+    out = torch.empty(t.shape, dtype=dtype, device=t.device)
+    check(lib().lloom_hip_cast(_ctx(_dev_index(t)), _ptr(t), src_id, _ptr(out), dst_id, t.numel(), _stream(t)))
+    return out
+
+
+def _check_out(y, shape, dtype, device, what):
+    """A caller's output buffer: contiguous, of the call's dtype, shape and device."""
+    if (not isinstance(y, torch.Tensor) or y.dtype != dtype or not y.is_contiguous() or y.device != device
+            or y.numel() != int(np.prod(shape))):
+        raise LloomHipError(3, f"{what}: y {tuple(getattr(y, 'shape', ()))} {getattr(y, 'dtype', None)} does not "
+                               f"fit the contiguous {dtype} output {tuple(shape)} on {device}")
+
+
+def reserve_workspace(nbytes, device=0):
+    """Grow the device context's workspace now (before a graph capture)."""
+    check(lib().lloom_hip_ctx_reserve(_ctx(device), int(nbytes)))
+
+
+def qmatmul_workspace_bytes(dtype, n, k, m, x_dtype=torch.float32, y_dtype=torch.float32, device=0):
+    out = ctypes.c_size_t()
+    check(lib().lloom_hip_qmatmul_workspace_bytes(_ctx(device), int(GgmlDType(dtype)), n, k, m,
+                                                  _act_id(x_dtype, "workspace"), _act_id(y_dtype, "workspace"),
+                                                  ctypes.byref(out)))
+    return out.value
 
 
 def set_mv_rows_max(rows, device=0):
@@ -194,18 +236,35 @@ class QTensor:
     def dequantize_f16(self):
         return self._dequant(1, torch.float16)
 
-    # indexed_moe_forward{,_with,_as} (mod.rs:1560-1645); the arm is ignored
-    def indexed_moe_forward(self, x, ids, arm=None, strict=True):
+    # indexed_moe_forward{,_with,_as} (mod.rs:1370-1645); the arm is ignored
+    def _moe_shapes(self, x, ids, what="indexed_moe_forward"):
         if len(self.shape) != 3:
-            raise LloomHipError(3, f"indexed_moe_forward: weight {self.shape} is not [experts, n, k]")
+            raise LloomHipError(3, f"{what}: weight {self.shape} is not [experts, n, k]")
         n_experts, n, k = self.shape
         if x.dim() != 3 or ids.dim() != 2:
-            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
+            raise LloomHipError(3, f"{what}: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
         batch, in_dim1, k_in = x.shape
         batch_ids, topk = ids.shape
         if k_in != k or batch != batch_ids or (in_dim1 != 1 and in_dim1 != topk):
-            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
-        x = x.to(torch.float32).contiguous()
+            raise LloomHipError(3, f"{what}: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
+        return n_experts, n, k, batch, in_dim1, topk
+
+    @staticmethod
+    def _moe_x(x, act):
+        """x as the CPU arm reads it: cast to `act` first when it differs
+        (mod.rs:1567-1571), then to f32 (mod.rs:1627), contiguous."""
+        act = x.dtype if act is None else act
+        _act_id(act, "indexed_moe_forward_as")
+        _act_id(x.dtype, "indexed_moe_forward_as")
+        return _cast(_cast(x, act), torch.float32).contiguous()
+
+    def indexed_moe_forward_as(self, x, ids, arm=None, act=None, strict=True):
+        """What indexed_moe_forward computes for x cast to `act` (torch.float32
+        or torch.float16; None: x's own dtype), bit for bit (mod.rs:1560-1575):
+        an f32 x with act f16 is rounded to f16 first.  y is f32
+        [batch, topk, n], as the CPU arm returns it."""
+        n_experts, n, k, batch, in_dim1, topk = self._moe_shapes(x, ids)
+        x = self._moe_x(x, act)
         ids = ids.to(torch.int32).contiguous()
         y = torch.empty((batch, topk, n), dtype=torch.float32, device=x.device)
         check(lib().lloom_hip_moe_matmul(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage), n_experts, n,
@@ -213,15 +272,27 @@ class QTensor:
                                          _stream(x)))
         return y
 
+    def indexed_moe_forward(self, x, ids, arm=None, strict=True):
+        return self.indexed_moe_forward_as(x, ids, arm, None, strict)
+
     indexed_moe_forward_with = indexed_moe_forward
+
+    def _moe_into_check(self, x, ids, y, shape_of_y):
+        if x.dtype != torch.float32 or not x.is_contiguous():
+            raise LloomHipError(2, f"indexed_moe_forward_into: x must be contiguous f32, got {x.dtype}")
+        if ids.dtype != torch.int32 or not ids.is_contiguous() or ids.device != x.device:
+            raise LloomHipError(2, "indexed_moe_forward_into: ids must be contiguous int32 on x's device")
+        if x.device != self.storage.device:
+            raise LloomHipError(1, "indexed_moe_forward_into: x is not on the weight's device")
+        _check_out(y, shape_of_y, torch.float32, x.device, "indexed_moe_forward_into")
 
     def indexed_moe_forward_into(self, x, ids, y):
         """indexed_moe_forward into a preallocated contiguous f32 y
-        [batch, topk, n]; non-strict (no stream sync), so it can be captured
+        [batch, topk, n] (x contiguous f32, ids contiguous int32, all on the
+        weight's device); non-strict (no stream sync), so it can be captured
         in a graph; lloom_hip_ctx_sync reports a bad id afterwards."""
-        n_experts, n, k = self.shape
-        batch, in_dim1, _ = x.shape
-        topk = ids.shape[1]
+        n_experts, n, k, batch, in_dim1, topk = self._moe_shapes(x, ids)
+        self._moe_into_check(x, ids, y, (batch, topk, n))
         check(lib().lloom_hip_moe_matmul(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage), n_experts, n,
                                          k, _ptr(x), batch, in_dim1, _ptr(ids), topk, _ptr(y), 0, _stream(x)))
         return y
@@ -232,21 +303,14 @@ class QTensor:
         if up.dtype != self.dtype or up.shape != self.shape:
             raise LloomHipError(3, f"indexed_moe_forward_pair: gate {self.dtype.name}{list(self.shape)} and "
                                    f"up {up.dtype.name}{list(up.shape)} differ")
-        n_experts, n, k = self.shape
-        if x.dim() != 3 or ids.dim() != 2:
-            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
-        batch, in_dim1, k_in = x.shape
-        batch_ids, topk = ids.shape
-        if k_in != k or batch != batch_ids or (in_dim1 != 1 and in_dim1 != topk):
-            raise LloomHipError(3, f"indexed_moe_forward: x {tuple(x.shape)} / ids {tuple(ids.shape)} do not fit weight {self.shape}")
-        return n_experts, n, k, batch, in_dim1, topk
+        return self._moe_shapes(x, ids)
 
-    def indexed_moe_forward_pair(self, up, x, ids, arm=None, strict=True):
+    def indexed_moe_forward_pair_as(self, up, x, ids, arm=None, act=None, strict=True):
         """Gate and up of one routed layer in ONE launch (the reference's
-        Metal kernel_mul_mv_id2, mod.rs:1365-1455): each half is bit for bit
-        what indexed_moe_forward computes for it."""
+        Metal kernel_mul_mv_id2, mod.rs:1365-1455), computed in `act`: each
+        half is bit for bit what indexed_moe_forward_as computes for it."""
         n_experts, n, k, batch, in_dim1, topk = self._moe_check(up, x, ids)
-        x = x.to(torch.float32).contiguous()
+        x = self._moe_x(x, act)
         ids = ids.to(torch.int32).contiguous()
         yg = torch.empty((batch, topk, n), dtype=torch.float32, device=x.device)
         yu = torch.empty_like(yg)
@@ -255,14 +319,19 @@ class QTensor:
                                               topk, _ptr(yg), _ptr(yu), 1 if strict else 0, _stream(x)))
         return yg, yu
 
+    def indexed_moe_forward_pair(self, up, x, ids, arm=None, strict=True):
+        return self.indexed_moe_forward_pair_as(up, x, ids, arm, None, strict)
+
     indexed_moe_forward_pair_with = indexed_moe_forward_pair
 
     def indexed_moe_forward_glu_as(self, up, x, ids, arm=None, act=None, strict=True):
-        """silu(gate) * up of the pair in ONE launch (mod.rs:1457-1531).  The
-        reference returns None off Metal and the caller composes; here the
-        fused launch always serves."""
+        """silu(gate) * up of indexed_moe_forward_pair_as's halves in ONE
+        launch (mod.rs:1457-1531), computed in `act` (x rounded to f16 first
+        when act is f16 and x is not).  The reference returns None off Metal
+        and the caller composes; here the fused launch always serves, with y
+        f32 as the CPU arm's halves are."""
         n_experts, n, k, batch, in_dim1, topk = self._moe_check(up, x, ids)
-        x = x.to(torch.float32).contiguous()
+        x = self._moe_x(x, act)
         ids = ids.to(torch.int32).contiguous()
         y = torch.empty((batch, topk, n), dtype=torch.float32, device=x.device)
         check(lib().lloom_hip_moe_matmul_glu(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage),
@@ -273,9 +342,8 @@ class QTensor:
     def indexed_moe_forward_glu_into(self, up, x, ids, y):
         """indexed_moe_forward_glu_as into a preallocated contiguous f32 y
         [batch, topk, n]; non-strict and allocation-free (graph-capturable)."""
-        n_experts, n, k = self.shape
-        batch, in_dim1, _ = x.shape
-        topk = ids.shape[1]
+        n_experts, n, k, batch, in_dim1, topk = self._moe_check(up, x, ids)
+        self._moe_into_check(x, ids, y, (batch, topk, n))
         check(lib().lloom_hip_moe_matmul_glu(_ctx(_dev_index(x)), int(self.dtype), _ptr(self.storage),
                                              _ptr(up.storage), n_experts, n, k, _ptr(x), batch, in_dim1, _ptr(ids),
                                              topk, _ptr(y), 0, _stream(x)))
@@ -321,58 +389,63 @@ class QMatMul:
     def from_qtensor(qtensor):
         return QMatMul(qtensor)
 
-    def forward(self, xs):
+    def _check_x(self, xs):
         n, k = self.qtensor.shape
         if xs.dim() < 2:
             raise LloomHipError(3, f"input tensor has only one dimension {tuple(xs.shape)}")
         if xs.shape[-1] != k:
             raise LloomHipError(3, f"input tensor {tuple(xs.shape)} incompatible with {self.qtensor.shape}")
-        if xs.dtype != torch.float32:
-            raise LloomHipError(2, f"Expected f32 activations, got {xs.dtype}")
+        if xs.dtype not in _ACT_IDS:
+            raise LloomHipError(2, f"Expected f32/f16 activations, got {xs.dtype}")
         if not xs.is_contiguous():
             raise LloomHipError(1, f"input tensor is not contiguous {tuple(xs.shape)}")
-        m = xs.numel() // k
-        y = torch.empty(tuple(xs.shape[:-1]) + (n,), dtype=torch.float32, device=xs.device)
+        if xs.device != self.qtensor.storage.device:
+            raise LloomHipError(1, f"input tensor is on {xs.device}, the weight on {self.qtensor.storage.device}")
+        return n, k, xs.numel() // k
+
+    def forward(self, xs):
+        """x . W^T; an f16 x gives an f16 y (matmul_t_f16, mod.rs:1983-1994:
+        x widened to f32, the f32 path, each sum rounded to f16)."""
+        n, k, m = self._check_x(xs)
+        y = torch.empty(tuple(xs.shape[:-1]) + (n,), dtype=xs.dtype, device=xs.device)
+        a = _ACT_IDS[xs.dtype]
         check(lib().lloom_hip_qmatmul(_ctx(_dev_index(xs)), int(self.qtensor.dtype), _ptr(self.qtensor.storage), n,
-                                      k, _ptr(xs), 0, m, _ptr(y), 0, _stream(xs)))
+                                      k, _ptr(xs), a, m, _ptr(y), a, _stream(xs)))
         return y
 
     __call__ = forward
 
     def _store(self, xs, y, store):
-        n, k = self.qtensor.shape
-        if xs.dim() < 2 or xs.shape[-1] != k:
-            raise LloomHipError(3, f"input tensor {tuple(xs.shape)} incompatible with {self.qtensor.shape}")
-        if xs.dtype != torch.float32 or not xs.is_contiguous():
-            raise LloomHipError(2, f"Expected contiguous f32 activations, got {xs.dtype}")
-        m = xs.numel() // k
+        n, k, m = self._check_x(xs)
+        _check_out(y, tuple(xs.shape[:-1]) + (n,), xs.dtype, xs.device, "qmatmul store")
+        a = _ACT_IDS[xs.dtype]
         check(lib().lloom_hip_qmatmul_store(_ctx(_dev_index(xs)), int(self.qtensor.dtype), _ptr(self.qtensor.storage),
-                                            n, k, _ptr(xs), 0, m, _ptr(y), 0, int(store), _stream(xs)))
+                                            n, k, _ptr(xs), a, m, _ptr(y), a, int(store), _stream(xs)))
         return y
 
     def forward_silu(self, xs):
         """silu(x . W^T) with the SiLU on the matmul's store, one launch
         (QMatMul::forward_silu, mod.rs:2102-2120; MvStore::Silu)."""
         n, _ = self.qtensor.shape
-        y = torch.empty(tuple(xs.shape[:-1]) + (n,), dtype=torch.float32, device=xs.device)
+        y = torch.empty(tuple(xs.shape[:-1]) + (n,), dtype=xs.dtype, device=xs.device)
         return self._store(xs, y, MvStore.Silu)
 
     def forward_mul_into(self, xs, gate):
         """gate <- gate * (x . W^T) at the store, one launch
         (QMatMul::forward_mul_into, mod.rs:2122-2156; MvStore::MulInto).
-        gate is an f32 contiguous [.., n] and is overwritten."""
-        n, _ = self.qtensor.shape
-        if gate.dtype != torch.float32 or not gate.is_contiguous() or gate.numel() != xs.numel() // xs.shape[-1] * n:
-            raise LloomHipError(3, f"forward_mul_into: gate {tuple(gate.shape)} {gate.dtype} does not fit the output")
+        gate is a contiguous [.., n] of x's dtype and is overwritten."""
         self._store(xs, gate, MvStore.MulInto)
 
     def forward_into(self, xs, y):
-        """forward into a preallocated contiguous f32 y [m, n] (xs [m, k] f32
-        contiguous): no allocation, so it can be captured in a graph."""
-        n, k = self.qtensor.shape
-        m = xs.numel() // k
+        """forward into a preallocated contiguous y [.., n] of x's dtype (xs
+        [.., k] contiguous, on the weight's device): no allocation once the
+        context workspace holds the call's (reserve_workspace), so it can be
+        captured in a graph."""
+        n, k, m = self._check_x(xs)
+        _check_out(y, tuple(xs.shape[:-1]) + (n,), xs.dtype, xs.device, "forward_into")
+        a = _ACT_IDS[xs.dtype]
         check(lib().lloom_hip_qmatmul(_ctx(_dev_index(xs)), int(self.qtensor.dtype), _ptr(self.qtensor.storage), n,
-                                      k, _ptr(xs), 0, m, _ptr(y), 0, _stream(xs)))
+                                      k, _ptr(xs), a, m, _ptr(y), a, _stream(xs)))
         return y
 
 

@@ -667,7 +667,7 @@ def test_refusals_are_named(L):
         L.QMatMul.from_qtensor(qt).forward(_cuda(np.zeros((2, 512), np.float32)))
     assert e.value.name == "ESHAPE"
     with pytest.raises(L.LloomHipError) as e:
-        L.QMatMul.from_qtensor(qt).forward(_cuda(np.zeros((2, 256), np.float16)))
+        L.QMatMul.from_qtensor(qt).forward(torch.zeros((2, 256), dtype=torch.bfloat16, device=DEV))
     assert e.value.name == "EDTYPE"
     from lloom_amd.quantized import _ctx, _ptr, _stream
     from lloom_amd.lib import lib
