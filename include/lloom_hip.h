@@ -180,6 +180,19 @@ int lloom_hip_ctx_workspace_bytes(lloom_hip_ctx* ctx, size_t* bytes);
 int lloom_hip_cast(lloom_hip_ctx* ctx, const void* src_dev, int src_dtype, void* dst_dev, int dst_dtype,
                    int64_t count, void* stream);
 
+/* lloom_hip_qmatmul without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace is a static device array of 32 MiB per GPU, held until the
+ * process ends (its address is looked up on the first call on each device);
+ * a call that needs more fails with LLOOM_HIP_ENOMEM
+ * (lloom_hip_qmatmul_workspace_bytes tells ahead).  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (other streams, other
+ * contexts) race.  Same arguments, results and refusals as
+ * lloom_hip_qmatmul. */
+int lloom_hip_qmatmul_noalloc(lloom_hip_ctx* ctx, int ggml_type, const void* w_dev, int64_t n, int64_t k,
+                              const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype, void* stream);
+
 /* ------------------------------------------------------- routed experts --
  * QTensor::indexed_moe_forward{,_with,_as} (mod.rs:1560-1645), CPU arm
  * matmul_t_indexed (mod.rs:766-810): W [n_experts, n, k] packed, x f32

@@ -62,6 +62,7 @@ def lib():
                 "lloom_hip_ctx_reserve": ([vp, sz], i32),
                 "lloom_hip_ctx_workspace_bytes": ([vp, ctypes.POINTER(sz)], i32),
                 "lloom_hip_cast": ([vp, vp, i32, vp, i32, i64, vp], i32),
+                "lloom_hip_qmatmul_noalloc": ([vp, i32, vp, i64, i64, vp, i32, i64, vp, i32, vp], i32),
                 "lloom_hip_moe_matmul": ([vp, i32, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, i32, vp], i32),
                 "lloom_hip_moe_matmul_pair": ([vp, i32, vp, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, vp, i32,
                                                vp], i32),
