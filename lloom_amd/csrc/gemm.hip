@@ -973,6 +973,7 @@ size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode)
     if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m)) return q6_gemm_workspace_bytes(n, k, m);
     if (use_mq(type, m)) return split_q8k_bytes(k, m);
     if (type == T_Q8_0 && q8_gemm_fits(n, k, m)) return q8_gemm_workspace_bytes(m, k);
+    if (type == T_Q4K && mode == GEMM_INT8 && gemm_i8_fits(n, k, m)) return gemm_i8_workspace_bytes(m, k);
     if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
     return matvec_workspace_bytes(type, n, k, 16);
 }
@@ -1053,6 +1054,8 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
     if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m))
         return launch_q6_gemm(w, x, y, n, k, m, qbuf, ws_cap, epi, s);
     if (use_mq(type, m)) return launch_mq(type, w, x, y, n, k, m, qbuf, epi, s);
+    if (type == T_Q4K && mode == GEMM_INT8 && gemm_i8_fits(n, k, m))
+        return launch_gemm_i8(w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);

@@ -46,6 +46,12 @@ constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode);
+// gemm_i8.hip: Q4_K prefill on int8 MFMA (two scale planes, f16-MFMA min
+// term), 128 x 256 tiles; its activation prep runs in the same call.
+bool gemm_i8_fits(int64_t n, int64_t k, int64_t m);
+size_t gemm_i8_workspace_bytes(int64_t m, int64_t k);
+hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
+                          int epi, hipStream_t s);
 // gemm_q6.hip: Q6_K from Q6_GEMM_MIN_ROWS rows (below, k_mv_mfma with 64
 // activation rows a layer: m = 32 22.6 / 17.0 us against 21.7 for the GEMM
 // on [2048, 8192] / [8192, 2048]; m = 64 31.2 / 23.3 against 22.3 / 23.2).
