@@ -14,8 +14,9 @@
 // (|S_j| <= 4064, exact in fp16) twice, the weight side -dmin * mn_j split
 // into an fp16 pair hi + lo (dmin * mn_j has at most 17 significant bits, so
 // the pair is exact while it stays below 65504; a wave whose columns hold a
-// dmin >= 1024 takes the operand -mn_j and scales by dmin in f32 instead).
-// The epilogue per output and superblock is four VALU instructions:
+// dmin >= 1024 scales every dmin of the superblock by the same power of two
+// 2^-s first, and gives 2^s to dy and 2^-s to d).  The epilogue per output
+// and superblock is four VALU instructions:
 //     v = fma(float(8 hi + lo), d, Dmin);  out = fma(v, dy, out)
 //
 // Operand roles.  The weights are the MFMA's A (rows = weight columns n),
@@ -29,21 +30,20 @@
 // and B agree, which they do lane by lane).
 //
 // Tiling.  512 threads = 8 waves, two a SIMD; the workgroup computes 128
-// activation rows x 256 weight columns, each wave 128 x 32: four m tiles
-// share every unpacked weight operand, so a wave unpacks each weight byte of
-// its columns once.  A superblock of K is one LDS stage (activations 128 x
-// 256 B, swizzled so eight rows reading one 16-byte piece hit eight bank
-// groups; raw Q4_K rows 256 x 144 B; S [128][8] fp16; dy [128] f32), two
+// activation rows x 256 weight columns, each wave 128 x 32: four 32 x 32
+// tiles share every unpacked weight operand, so a wave unpacks each weight
+// byte of its columns once.  A superblock of K is one LDS stage, two
 // stages: the loads of superblock sb + 1 are in flight while sb computes.
-// Every byte arrives by global_load_lds from a scalar base plus per-lane
-// offsets fixed for the whole K loop.
+// Every byte arrives by global_load_lds of 1 KB of contiguous memory (the
+// load issue cost grows with the cache lines an instruction touches) from a
+// scalar base plus a per-lane offset fixed for the whole K loop.  Each
+// activation operand of a tile is refilled with the next tile's as soon as
+// its MFMAs are issued, so only the first tile of a superblock waits on LDS.
 #include "kq_common.hpp"
 #include "kq_quant.hpp"
 #include "kernels.hpp"
 #include "kq_gemm.hpp"
 
-#include <cstdlib>
-#include <type_traits>
 
 namespace lloom {
 
@@ -52,29 +52,28 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 256, WAVES = 8, THREADS = 64 * WAVES, MT16 = BM / 16;
-// LDS, piece-major: a 16-byte piece of every row of a tile side by side, so
-// one global_load_lds (64 lanes x 16 B contiguous) moves one piece of 64
-// rows, eight lanes reading one piece of eight rows touch 32 consecutive
-// dwords (no bank conflict), and every read address is a per-lane base
-// plus a compile-time offset and a stage base.
-//   A  [16 pieces][128 rows][16 B] x8
-//   W  [9 pieces][256 rows][16 B]  pieces 0..7 = the qs bytes 16p .. 16p+15,
-//                                  piece 8 = the 16-byte header (d, dmin, scales)
+constexpr int BM = 128, BN = 256, WAVES = 8, THREADS = 64 * WAVES, MT = BM / 32, STAGES = 2;
+// LDS stage:
+//   A  [16 pieces][128 rows][16 B] x8, piece-major: eight lanes reading one
+//      piece of eight rows touch 32 consecutive dwords (no bank conflict)
+//   W  [256 rows][144 B] the raw Q4_K superblocks (a 36-dword stride: eight
+//      rows reading one piece hit eight bank groups)
 //   S  [128 rows][8] fp16, D [128] f32
+// Every global_load_lds moves 1 KB of contiguous memory (few cache lines:
+// the load issue is the DMA's cost): the activation prep writes x8 in the
+// order the stage holds it, 64 rows at a time, and S and dy superblock-major.
 constexpr int A_BYTES = BM * 256, W_BYTES = BN * 144, S_BYTES = BM * 16, D_BYTES = BM * 4;
-constexpr int A_OFF = 0, W_OFF = 2 * A_BYTES, S_OFF = W_OFF + 2 * W_BYTES, D_OFF = S_OFF + 2 * S_BYTES;
-constexpr int SCR_OFF = D_OFF + 2 * D_BYTES;  // per wave: d of its 32 columns
+constexpr int A_OFF = 0, W_OFF = A_BYTES, S_OFF = W_OFF + W_BYTES, D_OFF = S_OFF + S_BYTES;
+constexpr int STAGE = D_OFF + D_BYTES;
+constexpr int SCR_OFF = STAGES * STAGE;  // per wave: d of its 32 columns
 constexpr int LDS = SCR_OFF + WAVES * 128;
 constexpr int A_PER_WAVE = A_BYTES / 1024 / WAVES;          // 4
 constexpr int W_CHUNKS = W_BYTES / 1024;                    // 36
-constexpr int W_PER_WAVE = (W_CHUNKS + WAVES - 1) / WAVES;  // 5 (waves 4..7: 4)
+constexpr int W_PER_WAVE = (37 + WAVES - 1) / WAVES;  // 5: 37 weight instructions (7 rows each)
 static_assert(A_PER_WAVE == 4 && W_CHUNKS == 36 && LDS <= 160 * 1024, "staging layout");
-static_assert(A_BYTES + 7 * 4096 + 3 * 512 < 65536 && W_BYTES + 6 * 4096 < 65536, "immediate LDS offsets");
+static_assert(4096 * 7 + 512 * 3 < 65536, "immediate LDS offsets past the per-region lane bases");
 
 // Each 16-bit half of q times f (both halves' products below 2^16).
 __device__ __forceinline__ int pk_mul(uint32_t q, uint32_t f2) {
@@ -90,8 +89,9 @@ __device__ __forceinline__ uint32_t byte_pair(uint32_t w, int b) {
 
 // Activation prep: Q8_K of every (row, superblock), bit-exact (the CPU arm's
 // from_float, k_quants.rs:2400-2438), into
-//   xq  int8 [mp][k]       natural order
-//   s16 fp16 [mp][k/32]    S_j = bsums[2j] + bsums[2j + 1]
+//   xq  int8 [mp/64][k/256][16 pieces][64 rows][16 B]  x8, piece p of a
+//       superblock = its elements 16p .. 16p+15
+//   s16 fp16 [k/256][mp][8]  S_j = bsums[2j] + bsums[2j + 1]
 //   dyt f32  [k/256][mp]
 // with rows m .. mp-1 zero (the GEMM reads whole 128-row tiles).
 struct I8Ptrs {
@@ -145,20 +145,22 @@ __global__ __launch_bounds__(256) void k_gemm_prep_i8(const float* __restrict__ 
         int bs = 0;
         if (mi < m) q = q8k_block_wave(v[b], &d, &bs);
         const int sb = sb0 + b;
-        *(uint32_t*)(xq + (int64_t)mi * k + sb * 256 + 4 * lane) = q;
+        // lane l holds elements 4l .. 4l+3: piece l / 4, bytes 4 (l % 4) ..
+        *(uint32_t*)(xq + ((((int64_t)(mi >> 6) * nsb + sb) * 16 + (lane >> 2)) * 64 + (mi & 63)) * 16 +
+                     4 * (lane & 3)) = q;
         const int S = bs + __shfl_xor(bs, 4, 64);  // lanes 8j .. 8j+7: S_j
-        if ((lane & 7) == 0) s16[((int64_t)mi * nsb + sb) * 8 + (lane >> 3)] = (_Float16)(float)S;
+        if ((lane & 7) == 0) s16[((int64_t)sb * mp + mi) * 8 + (lane >> 3)] = (_Float16)(float)S;
         if (lane == 0) dyt[(int64_t)sb * mp + mi] = d;
     }
 }
 
-template <int EXP>
 __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                          const _Float16* __restrict__ s16,
                                                          const float* __restrict__ dyt, float* __restrict__ Y, int m,
                                                          int mp, int n, int k, int epi) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, c32 = lane & 31;
     int bm, bn;
     tile_of(mp / BM, (n + BN - 1) / BN, bm, bn);
     const int m0 = bm * BM, n0 = bn * BN;
@@ -168,257 +170,200 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
     const uint32_t lds0 = lds_addr(smem);
 
     // ---- per-lane DMA offsets, fixed for the K loop ----
-    // activations: instruction q = wave + 8 i moves piece q >> 1 of rows
-    // 64 (q & 1) .. +63; q & 1 = wave & 1 for every i
-    const uint32_t aoff = (uint32_t)(m0 + 64 * (wave & 1) + lane) * (uint32_t)k;
-    // weights: instruction q = wave + 8 i moves LDS piece q >> 2 of rows
-    // 64 (q & 3) .. +63 (q & 3 = wave & 3); rows past n reload row n - 1
-    // (computed, never stored)
-    const uint32_t woff = (uint32_t)min(n0 + 64 * (wave & 3) + lane, n - 1) * rowbytes;
-    // S (waves 4, 5: 64 rows each) and dy (wave 6, lanes 0..31: 4 rows each)
-    const uint32_t sdoff = wave == 6 ? (uint32_t)(m0 + 4 * (lane & 31)) * 4u
-                                     : (uint32_t)(m0 + 64 * (wave & 1) + lane) * (uint32_t)(k / 16);
-
+    // Activations: instruction q = wave + 8 i moves piece q >> 1 of row
+    // group q & 1 (64 rows, 1 KB contiguous in the prep's layout; q & 1 =
+    // wave & 1).  Weights: instruction q moves rows 7q .. 7q+6 of the tile
+    // (lane l: row 7q + l / 9, piece l % 9; lane 63 loads piece 0 of row
+    // 7q + 7, the bytes instruction q + 1 writes there too), so one per-lane
+    // offset serves every instruction; the last moves rows 252..255 (36
+    // lanes).  In the last column tile rows past n reload row n - 1
+    // (computed, never stored).  S (waves 4, 5) and dy (wave 6, lanes 0..31):
+    // 1 KB / 512 B contiguous.
+    const uint32_t lane16 = 16u * (uint32_t)lane;
+    const bool ragged_n = n0 + BN > n;  // uniform
+    const uint32_t wlane = (uint32_t)(lane / 9) * rowbytes + 16u * (uint32_t)(lane % 9);
+    const int8_t* xq_tile = xq + ((size_t)(m0 >> 6) + (size_t)(wv & 1)) * nsb * 16384;
     auto issue = [&](int sb, int stg) {
-        const uint32_t al = lds0 + A_OFF + (uint32_t)stg * A_BYTES;
+        const uint32_t st = lds0 + (uint32_t)stg * STAGE;
+        const int8_t* ab = xq_tile + (size_t)sb * 16384;
 #pragma unroll
         for (int i = 0; i < A_PER_WAVE; i++) {
             const int q = wv + WAVES * i;
-            dma16s(xq + (uint32_t)sb * 256u + 16u * (uint32_t)(q >> 1), aoff, al + 2048u * (uint32_t)(q >> 1) +
-                                                                                  1024u * (uint32_t)(q & 1));
+            dma16s(ab + 1024u * (uint32_t)(q >> 1), lane16,
+                   st + A_OFF + 2048u * (uint32_t)(q >> 1) + 1024u * (uint32_t)(q & 1));
         }
-        const uint32_t wl = lds0 + W_OFF + (uint32_t)stg * W_BYTES;
+        const uint8_t* wb = W + (size_t)n0 * rowbytes + (uint32_t)sb * Q4K_BYTES;
 #pragma unroll
         for (int i = 0; i < W_PER_WAVE; i++) {
-            const int q = wv + WAVES * i, p = q >> 2;
-            if (q < W_CHUNKS)
-                dma16s(W + (uint32_t)sb * Q4K_BYTES + (p < 8 ? 16u + 16u * (uint32_t)p : 0u), woff,
-                       wl + 4096u * (uint32_t)p + 1024u * (uint32_t)(q & 3));
+            const int q = wv + WAVES * i;  // 0 .. 36
+            if (q > 36) continue;
+            if (q < 36 || lane < 36) {
+                if (!ragged_n) {
+                    dma16s(wb + (size_t)7 * q * rowbytes, wlane, st + W_OFF + 1008u * (uint32_t)q);
+                } else {
+                    // rows clamped to n - 1: the offset from the tile's first
+                    // row (never negative, below 256 rows)
+                    const uint32_t off = (uint32_t)(min(n0 + 7 * q + lane / 9, n - 1) - n0) * rowbytes +
+                                         16u * (uint32_t)(lane % 9);
+                    dma16s(wb, off, st + W_OFF + 1008u * (uint32_t)q);
+                }
+            }
         }
         if (wv == 4 || wv == 5)
-            dma16s((const uint8_t*)s16 + (uint32_t)sb * 16u, sdoff,
-                   lds0 + S_OFF + (uint32_t)stg * S_BYTES + 1024u * (uint32_t)(wv - 4));
-        if (wv == 6 && lane < 32)
-            dma16s((const uint8_t*)(dyt + (int64_t)sb * mp), sdoff, lds0 + D_OFF + (uint32_t)stg * D_BYTES);
+            dma16s((const uint8_t*)s16 + ((size_t)sb * mp + m0 + 64 * (wv - 4)) * 16u, lane16,
+                   st + S_OFF + 1024u * (uint32_t)(wv - 4));
+        if (wv == 6 && lane < 32) dma16s((const uint8_t*)(dyt + (int64_t)sb * mp + m0), lane16, st + D_OFF);
+    };
+    auto wait_all = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
     };
 
-    // Per lane: g = lane / 16 picks 16 of an MFMA's 64 k (and 4 of its 16
-    // output rows), r16 = lane % 16 its row (A) or column (B).
-    const int g = lane >> 4, r16 = lane & 15;
-    v4f out[MT16][2];
+    v16f out[MT];
 #pragma unroll
-    for (int t = 0; t < MT16; t++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int u = 0; u < 2; u++) out[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int v = 0; v < 16; v++) out[t][v] = 0.0f;
 
-    // per-lane LDS bases; everything else in a read address is a constant
-    const int wrow = 32 * wave + r16;  // the lane's weight column in n tile 0 (+16 in tile 1)
-    const int abase = A_OFF + 2048 * g + 16 * r16;
-    const int wbase = W_OFF + 4096 * (g & 1) + 16 * wrow, hbase = W_OFF + 8 * 4096 + 16 * wrow;
-    const int sbase = S_OFF + 16 * r16 + 8 * (g & 1), dbase = D_OFF + 4 * r16;
+    // per-lane LDS bases (plus a stage offset); the rest of an address is a constant
+    const int wrow = 32 * wave + c32;  // the lane's weight column in the tile
+    const int la = A_OFF + 2048 * h + 16 * c32;
+    const int lw = W_OFF + 144 * wrow + 16 + 16 * h, lh = W_OFF + 144 * wrow;
+    const int ls = S_OFF + 16 * c32, ld = D_OFF + 4 * c32;
     float* const scr = (float*)(smem + SCR_OFF) + 32 * wave;
-    // the lane's nibble half (k 32..63 of a 64-k step are the high nibbles)
-    // and its scale byte, ((2c + g/2) & 3) for step c, as a v_perm selector
-    const int nsh = 4 * (g >> 1);
-    const uint32_t sel0 = 0x0c000c00u | (uint32_t)(g >> 1) * 0x00010001u, sel2 = sel0 + 0x00020002u;
 
     issue(0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
+    wait_all();
 
-    // One superblock from stage sb & 1, the loads of sb + 1 queued into the other.
     for (int sb = 0; sb < nsb; sb++) {
-        const int stg = sb & 1;
-        const int sa = abase + stg * A_BYTES, sw = wbase + stg * W_BYTES, sh8 = hbase + stg * W_BYTES;
-        const int ss = sbase + stg * S_BYTES, sd = dbase + stg * D_BYTES;
+        const int so = (sb % STAGES) * STAGE;
+        const int sa = la + so, sw = lw + so, sh = lh + so, ss = ls + so, sd = ld + so;
         // 1. this superblock's weight bytes, into registers; the columns' d
         //    to the lanes whose outputs use them (through LDS, within the wave)
-        uint4 hdr[2], raw[2][4];
+        const uint4 hdr = *(const uint4*)(smem + sh);
+        uint4 raw[4];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            hdr[u] = *(const uint4*)(smem + sh8 + 256 * u);
-#pragma unroll
-            for (int c = 0; c < 4; c++) raw[u][c] = *(const uint4*)(smem + sw + (2 * c * 4096 + 256 * u));
-        }
-        float dmin[2];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            scr[16 * u + r16] = f16_to_f32(hdr[u].x & 0xffffu);
-            dmin[u] = f16_to_f32(hdr[u].x >> 16);
-        }
+        for (int c = 0; c < 4; c++) raw[c] = *(const uint4*)(smem + sw + 32 * c);
+        const float dmin = f16_to_f32(hdr.x >> 16);
+        scr[c32] = f16_to_f32(hdr.x & 0xffffu);
         __builtin_amdgcn_wave_barrier();
-        v4f dv[2];
+        v16f dv;
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const float4 q = *(const float4*)(scr + 16 * u + 4 * g);
-            dv[u] = v4f{q.x, q.y, q.z, q.w};
+        for (int g = 0; g < 4; g++) {
+            const float4 q = *(const float4*)(scr + 8 * g + 4 * h);
+            dv[4 * g] = q.x;
+            dv[4 * g + 1] = q.y;
+            dv[4 * g + 2] = q.z;
+            dv[4 * g + 3] = q.w;
         }
-        // 2. queue the next superblock into the other stage
+        // 2. queue superblock sb + 1 into the other stage
         __builtin_amdgcn_sched_barrier(0);
-        if (sb + 1 < nsb && !(EXP & 4)) issue(sb + 1, 1 - stg);
+        if (sb + 1 < nsb) issue(sb + 1, (sb + 1) % STAGES);
         __builtin_amdgcn_sched_barrier(0);
 
-        // 3. the weight operands: planes of the four 64-k steps of both n
-        //    tiles, and the min term's; s = 0 unless a column of the wave
-        //    has dmin >= 1024: then dmin 2^-s < 1024 enters the fp16 pair,
-        //    2^-s goes to d and 2^s to dy (exact powers of two)
-        float dys = 1.0f, sdn = 1.0f;
-        if (__ballot(dmin[0] >= 1024.0f || dmin[1] >= 1024.0f) != 0) {  // wave-uniform, rare
-            const float mx = wave_max(__builtin_fmaxf(dmin[0], dmin[1]));
-            const int e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xffu) - 127 - 9;
-            sdn = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
+        // 3. the weight operands: planes of the eight sub-blocks and the min
+        //    term's.  s = 0 unless a column of the wave has dmin >= 1024: then
+        //    dmin 2^-s < 1024 enters the fp16 pair, 2^-s goes to d and 2^s to
+        //    dy (exact powers of two)
+        float dys = 1.0f;
+        float dmw = dmin;
+        if (__ballot(dmin >= 1024.0f) != 0) {  // wave-uniform, rare
+            const int e = (int)((__builtin_bit_cast(uint32_t, wave_max(dmin)) >> 23) & 0xffu) - 127 - 9;
+            const float sdn = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
             dys = __builtin_bit_cast(float, (uint32_t)(127 + e) << 23);
+            dmw = dmin * sdn;
 #pragma unroll
-            for (int u = 0; u < 2; u++) dv[u] *= sdn;
+            for (int v = 0; v < 16; v++) dv[v] *= sdn;
         }
-        v4i plo[2][4], phi[2][4];
-        v4h amin[2];
+        // scales (get_scale_min_k4, k_quants utils.rs:50-60, four at a time)
+        const uint32_t sc0 = hdr.y & 0x3F3F3F3Fu;
+        const uint32_t sc1 = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+        const uint32_t mn0 = hdr.z & 0x3F3F3F3Fu;
+        const uint32_t mn1 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+        const uint32_t s0a = sc0 & 0x07070707u, s0b = sc1 & 0x07070707u;
+        const uint32_t s1a = (sc0 >> 3) & 0x07070707u, s1b = (sc1 >> 3) & 0x07070707u;
+        v4i plo[8], phi[8];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const uint4 hd = hdr[u];
-            // scales (get_scale_min_k4, k_quants utils.rs:50-60, four at a time)
-            const uint32_t sc0 = hd.y & 0x3F3F3F3Fu;
-            const uint32_t sc1 = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-            const uint32_t mn = (g & 1) ? (((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u))
-                                        : (hd.z & 0x3F3F3F3Fu);
-            const uint32_t s0a = sc0 & 0x07070707u, s0b = sc1 & 0x07070707u;
-            const uint32_t s1a = (sc0 >> 3) & 0x07070707u, s1b = (sc1 >> 3) & 0x07070707u;
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint4 r = raw[u][c];
-                const uint32_t q0 = (r.x >> nsh) & 0x0F0F0F0Fu, q1 = (r.y >> nsh) & 0x0F0F0F0Fu,
-                               q2 = (r.z >> nsh) & 0x0F0F0F0Fu, q3 = (r.w >> nsh) & 0x0F0F0F0Fu;
-                const uint32_t sel = (c & 1) ? sel2 : sel0;
-                const uint32_t f0 = __builtin_amdgcn_perm(0u, c < 2 ? s0a : s0b, sel);
-                const uint32_t f1 = __builtin_amdgcn_perm(0u, c < 2 ? s1a : s1b, sel);
-                if (EXP & 8) {
-                    plo[u][c] = v4i{(int)r.x, (int)r.y, (int)r.z, (int)r.w};
-                    phi[u][c] = v4i{(int)r.y, (int)r.z, (int)r.w, (int)r.x};
-                } else {
-                plo[u][c] = v4i{pk_mul(q0, f0), pk_mul(q1, f0), pk_mul(q2, f0), pk_mul(q3, f0)};
-                phi[u][c] = v4i{pk_mul(q0, f1), pk_mul(q1, f1), pk_mul(q2, f1), pk_mul(q3, f1)};
-                }
-            }
-            // min-term weight operand, k = 4g .. 4g+3: lanes g = 0, 1 the fp16
-            // hi of -dmin' mn_j for j = 4g .. 4g+3, lanes g = 2, 3 the lo
-            const float dm = dmin[u] * sdn;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float v = dm * (float)byte_of(mn, i);  // exact in f32
-                const _Float16 vh = (_Float16)v;
-                const _Float16 vl = (_Float16)(v - (float)vh);
-                amin[u][i] = (g >> 1) ? -vl : -vh;
-            }
+        for (int j = 0; j < 8; j++) {
+            const uint4 r = raw[j >> 1];
+            const int shf = (j & 1) * 4;
+            const uint32_t q0 = (r.x >> shf) & 0x0F0F0F0Fu, q1 = (r.y >> shf) & 0x0F0F0F0Fu,
+                           q2 = (r.z >> shf) & 0x0F0F0F0Fu, q3 = (r.w >> shf) & 0x0F0F0F0Fu;
+            const uint32_t f0 = byte_pair(j < 4 ? s0a : s0b, j & 3), f1 = byte_pair(j < 4 ? s1a : s1b, j & 3);
+            plo[j] = v4i{pk_mul(q0, f0), pk_mul(q1, f0), pk_mul(q2, f0), pk_mul(q3, f0)};
+            phi[j] = v4i{pk_mul(q0, f1), pk_mul(q1, f1), pk_mul(q2, f1), pk_mul(q3, f1)};
         }
-        // 4. the tiles: 16 activation rows x 16 weight columns, eight int8
-        //    MFMAs (four steps, two planes), the min MFMA, the epilogue.
-        //    Software-pipelined: tile i's MFMAs are issued with tile i - 1's
-        //    epilogue between them, and the next m tile's activations are
-        //    read while the current one's MFMAs run.
-        v4i bx[2][4];
-        v4h sv[2];
-        float dy[2];
-        v4i lo[2], hi[2];
-        v4f dmv[2];
-        float dyv[2];
-        auto load_b = [&](int t, int buf) {
+        // min-term weight operand, k = 8h .. 8h+7: half 0 the fp16 hi of
+        // -dmin' mn_j, half 1 the lo
+        v8h amin;
 #pragma unroll
-            for (int c = 0; c < 4; c++) bx[buf][c] = *(const v4i*)(smem + sa + (8192 * c + 256 * t));
-            sv[buf] = *(const v4h*)(smem + ss + 256 * t);
-            dy[buf] = *(const float*)(smem + sd + 64 * t) * dys;
-        };
-        auto mfmas = [&](int buf, int u, int slot) {
-            const v4i z = {0, 0, 0, 0};
-            lo[slot] = __builtin_amdgcn_mfma_i32_16x16x64_i8(plo[u][0], bx[buf][0], z, 0, 0, 0);
-            hi[slot] = __builtin_amdgcn_mfma_i32_16x16x64_i8(phi[u][0], bx[buf][0], z, 0, 0, 0);
-#pragma unroll
-            for (int c = 1; c < 4; c++) {
-                lo[slot] = __builtin_amdgcn_mfma_i32_16x16x64_i8(plo[u][c], bx[buf][c], lo[slot], 0, 0, 0);
-                hi[slot] = __builtin_amdgcn_mfma_i32_16x16x64_i8(phi[u][c], bx[buf][c], hi[slot], 0, 0, 0);
-            }
-            const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
-            dmv[slot] = __builtin_amdgcn_mfma_f32_16x16x16f16(amin[u], sv[buf], zf, 0, 0, 0);
-            dyv[slot] = dy[buf];
-        };
-        auto epi = [&](int t, int u, int buf, int slot) {
-            if (EXP & 64) return;
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float f = (float)(hi[slot][v] * 8 + lo[slot][v]);
-                out[t][u][v] = __builtin_fmaf(__builtin_fmaf(f, dv[u][v], dmv[slot][v]), dyv[slot], out[t][u][v]);
-            }
-        };
-        load_b(0, 0);
-#pragma unroll
-        for (int i = 0; i < 2 * MT16; i++) {
-            const int t = i >> 1, u = i & 1, buf = t & 1, slot = i & 1;
-            if (u == 0 && t + 1 < MT16) load_b(t + 1, buf ^ 1);
-            mfmas(buf, u, slot);
-            if (i > 0) epi((i - 1) >> 1, (i - 1) & 1, ((i - 1) >> 1) & 1, slot ^ 1);
-            // interleave: the reads first, then the MFMAs with the previous
-            // tile's epilogue between them, starting a few MFMAs in (its
-            // inputs have landed by then)
-            if (u == 0 && t + 1 < MT16) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-            if (EXP & 128) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-#pragma unroll
-                for (int k = 0; k < 6; k++) {
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                }
-            } else {
-#pragma unroll
-                for (int k = 0; k < 9; k++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-                }
-            }
+        for (int j = 0; j < 8; j++) {
+            const float v = dmw * (float)byte_of(j < 4 ? mn0 : mn1, j & 3);  // exact in f32
+            const _Float16 vh = (_Float16)v;
+            const _Float16 vl = (_Float16)(v - (float)vh);
+            amin[j] = h ? -vl : -vh;
         }
-        epi(MT16 - 1, 1, (MT16 - 1) & 1, 1);
-        if (EXP & 64)
-            for (int v = 0; v < 4; v++) out[0][0][v] += (float)(lo[0][v] + hi[1][v]) + dmv[0][v] + dmv[1][v];
-        // 5. the next stage has landed (this wave's share) and is visible to all
-        __builtin_amdgcn_sched_barrier(0);
-        if (!(EXP & 2)) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
+
+        // 4. the four 32 x 32 tiles: sixteen int8 MFMAs (eight sub-blocks,
+        //    two planes), each activation operand refilled with the next
+        //    tile's as soon as its MFMAs are issued; then the min MFMA and the
+        //    epilogue (the other wave of the SIMD runs its MFMAs meanwhile)
+        v4i bx[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) bx[j] = *(const v4i*)(smem + sa + 4096 * j);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const v8h sv = *(const v8h*)(smem + ss + 512 * t);
+            const float dy = *(const float*)(smem + sd + 128 * t) * dys;
+            v16i lo, hi;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const v16i z = {};
+                lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(plo[j], bx[j], j ? lo : z, 0, 0, 0);
+                hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(phi[j], bx[j], j ? hi : z, 0, 0, 0);
+                if (t + 1 < MT) bx[j] = *(const v4i*)(smem + sa + (4096 * j + 512 * (t + 1)));
+            }
+            const v16f zf = {};
+            const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(amin, sv, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const float f = (float)(hi[v] * 8 + lo[v]);
+                out[t][v] = __builtin_fmaf(__builtin_fmaf(f, dv[v], dm[v]), dy, out[t][v]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // 5. superblock sb + 1 has landed (this wave's share) and is visible to all
+        wait_all();
     }
 
-    // store: lane row m0 + 16 t + r16, columns n0 + 32 wave + 16 u + 4 g + 0..3
+    // store: lane row m0 + 32 t + c32, columns n0 + 32 wave + 8 g + 4 h + 0..3
 #pragma unroll
-    for (int t = 0; t < MT16; t++) {
-        const int row = m0 + 16 * t + r16;
+    for (int t = 0; t < MT; t++) {
+        const int row = m0 + 32 * t + c32;
         if (row >= m) continue;
         float* yr = Y + (int64_t)row * n;
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int col = n0 + 32 * wave + 16 * u + 4 * g;
+        for (int g = 0; g < 4; g++) {
+            const int col = n0 + 32 * wave + 8 * g + 4 * h;
             if (epi == EPI_STORE && col + 3 < n) {
-                *(float4*)(yr + col) = make_float4(out[t][u][0], out[t][u][1], out[t][u][2], out[t][u][3]);
+                *(float4*)(yr + col) = make_float4(out[t][4 * g], out[t][4 * g + 1], out[t][4 * g + 2], out[t][4 * g + 3]);
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    if (col + r < n) store_epi_slow(yr + col + r, out[t][u][r], epi);
+                    if (col + r < n) store_epi_slow(yr + col + r, out[t][4 * g + r], epi);
             }
         }
     }
 }
 
-
 hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
                           int epi, hipStream_t s) {
-    static int exp_mode = [] { const char* e = getenv("LLOOM_HIP_I8_EXP"); return e ? atoi(e) : 0; }();
     static bool attr_set = false;
     if (!attr_set) {
-        for (const void* f : {(const void*)k_gemm_q4k_i8<0>, (const void*)k_gemm_q4k_i8<2>, (const void*)k_gemm_q4k_i8<4>,
-                              (const void*)k_gemm_q4k_i8<12>, (const void*)k_gemm_q4k_i8<20>,
-                              (const void*)k_gemm_q4k_i8<28>, (const void*)k_gemm_q4k_i8<36>,
-                              (const void*)k_gemm_q4k_i8<44>, (const void*)k_gemm_q4k_i8<68>,
-                              (const void*)k_gemm_q4k_i8<76>, (const void*)k_gemm_q4k_i8<128>,
-                              (const void*)k_gemm_q4k_i8<132>}) {
-            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
-            if (e != hipSuccess) return e;
-        }
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k_i8, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+        if (e != hipSuccess) return e;
         attr_set = true;
     }
     const I8Ptrs p = i8_ptrs(ws, m, k);
@@ -432,23 +377,8 @@ hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, in
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const unsigned grid = (unsigned)((p.mp / BM) * ((n + BN - 1) / BN));
-#define LAUNCH_I8(X) hipLaunchKernelGGL(k_gemm_q4k_i8<X>, dim3(grid), dim3(THREADS), LDS, s, (const uint8_t*)w, p.xq, \
-                                        p.s16, p.dyt, y, (int)m, (int)p.mp, (int)n, (int)k, epi)
-    switch (exp_mode) {
-        case 2: LAUNCH_I8(2); break;
-        case 4: LAUNCH_I8(4); break;
-        case 12: LAUNCH_I8(12); break;
-        case 20: LAUNCH_I8(20); break;
-        case 28: LAUNCH_I8(28); break;
-        case 36: LAUNCH_I8(36); break;
-        case 44: LAUNCH_I8(44); break;
-        case 68: LAUNCH_I8(68); break;
-        case 76: LAUNCH_I8(76); break;
-        case 128: LAUNCH_I8(128); break;
-        case 132: LAUNCH_I8(132); break;
-        default: LAUNCH_I8(0);
-    }
-#undef LAUNCH_I8
+hipLaunchKernelGGL(k_gemm_q4k_i8, dim3(grid), dim3(THREADS), LDS, s, (const uint8_t*)w, p.xq, p.s16, p.dyt, y, (int)m,
+                       (int)p.mp, (int)n, (int)k, epi);
     return hipGetLastError();
 }
 
