@@ -1,24 +1,31 @@
-"""GGUF container: header reader, writer, and the load -> device upload seam.
+"""GGUF files: parse a header, write a file, and hand tensors to the device.
 
-Host mirror of lloom-tensor/src/quantized/gguf_file.rs (and the part of
-ggml_file.rs the GGUF reader calls):
-  Value / ValueType (ids, to_* accessors, to_count)   gguf_file.rs:196-530
-  Content.read (magic, counts, caps, kv, tensor infos, alignment)  :532-654
-  TensorInfo.size_in_bytes / validate_payload / read  gguf_file.rs:81-171
-  Content.validate_payloads / tensor                  gguf_file.rs:656-677
-  packed_offsets / write_header / write               gguf_file.rs:691-781
-  qtensor_from_ggml                                   ggml_file.rs:180-228
-The same caps, the same checked arithmetic (u64 for header geometry, host
-usize / isize limits for materialisation) and the same refusal wording, so a
-file the reference refuses is refused here with the same cause.
+The on-disk format follows the public GGUF specification (ggml's
+docs/gguf.md): a magic word, a version, two counts, the key/value metadata,
+a tensor directory, padding up to the data alignment, then the tensor
+payloads.  Versions 2 and 3 store every count and length as u64; version 1
+stores them as u32.  All scalars are little endian.
 
-Everything in this module is host I/O on a seekable binary reader; the one
-device step is the final upload, `QTensor.from_data`, which lays the packed
-blocks into HBM with the tail pad the kernels read past.  Q8_0, Q4_K and Q6_K
-tensors become device QTensors the matmul path takes; F32 / F16 / BF16
-tensors (norms, biases) become device QTensors that dequantize by
-reinterpretation; every other block type is parsed (its geometry is known)
-but refused at materialisation, since this library has no kernel for it.
+What a file may declare is bounded before anything is allocated:
+
+* counts, string sizes and array lengths are capped at 2^30, and a header
+  must be at least as long as the smallest encoding of what it declares;
+* a tensor has at most 4 dims and arrays nest at most 64 deep;
+* tensor geometry (elements, bytes, file offsets) is computed exactly and
+  refused when it leaves the u64 range; a materialised copy is further
+  refused above the host's isize limit;
+* a payload is checked against the file's extent before it is read.
+
+These are the limits lloom's reader enforces (gguf_file.rs:20-33, 81-171,
+532-654), so the same bytes are accepted or refused with the same cause;
+the parser here is organised around a small wire cursor and a codec table
+of its own, and its messages are its own.
+
+The one device step is the final upload (`QTensor.from_data`), which puts
+the packed blocks in HBM with the tail pad the kernels read past.  Q8_0,
+Q4_K, Q6_K and the float types F32 / F16 / BF16 are uploaded; other block
+types parse (their geometry is known) but are refused at upload, since the
+HIP arm has no kernel for them (ggml_file.rs:180-228 is the reference seam).
 """
 import enum
 import struct
@@ -28,85 +35,77 @@ import numpy as np
 from .lib import LloomHipError
 
 DEFAULT_ALIGNMENT = 32
+CAP_COUNT = 1 << 30            # tensors, metadata entries, array items
+CAP_STRING = 1 << 30           # bytes in one string
+CAP_RANK = 4                   # dims of one tensor
+CAP_NESTING = 64               # array-in-array depth
 
-GGUF_MAX_STRING_LENGTH = 1 << 30
-GGUF_MAX_ARRAY_ELEMENTS = 1 << 30
-GGUF_MAX_TENSOR_DIMS = 4
-GGUF_MAX_VALUE_DEPTH = 64
-
-_U64_MAX = (1 << 64) - 1
-_USIZE_MAX = _U64_MAX          # 64-bit hosts only
-_ISIZE_MAX = (1 << 63) - 1
+_TWO64 = 1 << 64
+_HOST_ISIZE = (1 << 63) - 1    # 64-bit hosts: usize == u64, isize is the allocation limit
+_WRITE_PAD = 32                # the writer pads header and payloads to 32 bytes
 
 GGUF_TYPE_FP8_E4M3 = 1 << 24
 
 
 class GgufError(LloomHipError):
-    """A refused GGUF file or tensor; the message names the cause."""
+    """A GGUF file, tensor or value this module refuses; the text names why."""
 
     def __init__(self, msg):
         super().__init__(3, msg)
 
 
-def _bail(msg):
+def _refuse(msg):
     raise GgufError(msg)
 
 
-# ------------------------------------------------------------ dtypes ---
-# Every GGML type id a GGUF header may name (mod.rs:505-568), with its block
-# geometry (mod.rs:663-713): id -> (name, elements per block, bytes per block).
-FILE_TYPES = {
-    0: ("F32", 1, 4),
-    1: ("F16", 1, 2),
-    2: ("Q4_0", 32, 18),
-    3: ("Q4_1", 32, 20),
-    6: ("Q5_0", 32, 22),
-    7: ("Q5_1", 32, 24),
-    8: ("Q8_0", 32, 34),
-    9: ("Q8_1", 32, 36),
-    10: ("Q2K", 256, 84),
-    11: ("Q3K", 256, 110),
-    12: ("Q4K", 256, 144),
-    13: ("Q5K", 256, 176),
-    14: ("Q6K", 256, 210),
-    15: ("Q8K", 256, 292),
-    16: ("IQ2XXS", 256, 66),
-    17: ("IQ2XS", 256, 74),
-    18: ("IQ3XXS", 256, 98),
-    20: ("IQ4NL", 32, 18),
-    21: ("IQ3S", 256, 110),
-    22: ("IQ2S", 256, 82),
-    23: ("IQ4XS", 256, 136),
-    30: ("BF16", 1, 2),
-    39: ("MXFP4", 32, 17),
-    42: ("Q2_0", 64, 18),
-    GGUF_TYPE_FP8_E4M3: ("FP8E4M3", 32, 34),
-}
-_ACTIVATION_ONLY = (9, 15)      # Q8_1, Q8K: no file stores a weight in them
+def _fits_u64(v, what):
+    if v >= _TWO64:
+        _refuse(f"{what} does not fit in 64 bits")
+    return v
 
+
+# ----------------------------------------------------------- block types
 
 class FileType:
-    """A GGML type as a GGUF header names it (GgmlDType in the reference)."""
+    """A GGML block type id as a tensor directory names it, with its geometry
+    (elements per block, bytes per block; mod.rs:505-568, 663-713)."""
+
+    # id: (name, elements per block, bytes per block)
+    TABLE = {
+        0: ("F32", 1, 4), 1: ("F16", 1, 2), 30: ("BF16", 1, 2),
+        2: ("Q4_0", 32, 18), 3: ("Q4_1", 32, 20), 6: ("Q5_0", 32, 22), 7: ("Q5_1", 32, 24),
+        8: ("Q8_0", 32, 34), 9: ("Q8_1", 32, 36),
+        10: ("Q2K", 256, 84), 11: ("Q3K", 256, 110), 12: ("Q4K", 256, 144), 13: ("Q5K", 256, 176),
+        14: ("Q6K", 256, 210), 15: ("Q8K", 256, 292),
+        16: ("IQ2XXS", 256, 66), 17: ("IQ2XS", 256, 74), 18: ("IQ3XXS", 256, 98), 20: ("IQ4NL", 32, 18),
+        21: ("IQ3S", 256, 110), 22: ("IQ2S", 256, 82), 23: ("IQ4XS", 256, 136),
+        39: ("MXFP4", 32, 17), 42: ("Q2_0", 64, 18), GGUF_TYPE_FP8_E4M3: ("FP8E4M3", 32, 34),
+    }
+    # Activation-side block types: a kernel produces them at run time, a file
+    # never holds weights in them (mod.rs:448-475).
+    ACTIVATION_ONLY = frozenset((9, 15))
 
     __slots__ = ("id",)
 
     def __init__(self, type_id):
-        if type_id not in FILE_TYPES:
-            _bail(f"unknown dtype for tensor {type_id}")
-        self.id = int(type_id)
+        type_id = int(type_id)
+        if type_id not in self.TABLE:
+            _refuse(f"tensor type id {type_id} is not a known GGML type")
+        self.id = type_id
 
-    name = property(lambda self: FILE_TYPES[self.id][0])
+    @property
+    def name(self):
+        return self.TABLE[self.id][0]
 
     def block_size(self):
-        return FILE_TYPES[self.id][1]
+        return self.TABLE[self.id][1]
 
     def type_size(self):
-        return FILE_TYPES[self.id][2]
+        return self.TABLE[self.id][2]
 
     def validate_file_weight(self):
-        """GgmlDType::validate_file_weight (mod.rs:448-475)."""
-        if self.id in _ACTIVATION_ONLY:
-            _bail(f"quantized type {self.name} is not supported yet")
+        if self.id in self.ACTIVATION_ONLY:
+            _refuse(f"{self.name} is an activation-only block type; no file stores weights in it")
 
     def __eq__(self, other):
         if isinstance(other, FileType):
@@ -123,10 +122,14 @@ class FileType:
         return self.name
 
 
-# ------------------------------------------------------------ values ---
+def _as_file_type(t):
+    return t if isinstance(t, FileType) else FileType(t)
+
+
+# ------------------------------------------------------- metadata values
 
 class ValueType(enum.IntEnum):
-    """gguf_file.rs:483-519 (on-disk ids)."""
+    """Metadata value type ids, as the spec numbers them."""
     U8 = 0
     I8 = 1
     U16 = 2
@@ -143,38 +146,33 @@ class ValueType(enum.IntEnum):
 
     @staticmethod
     def from_u32(v):
-        try:
-            return ValueType(v)
-        except ValueError:
-            _bail(f"unrecognized value-type {v:#08x}")
-
-    def min_disk_size(self, prefix):
-        """Smallest encoding of one value (gguf_file.rs:521-530)."""
-        if self in (ValueType.U8, ValueType.I8, ValueType.Bool):
-            return 1
-        if self in (ValueType.U16, ValueType.I16):
-            return 2
-        if self in (ValueType.U32, ValueType.I32, ValueType.F32):
-            return 4
-        if self in (ValueType.U64, ValueType.I64, ValueType.F64):
-            return 8
-        if self == ValueType.String:
-            return prefix
-        return 4 + prefix
+        if v not in ValueType._value2member_map_:
+            _refuse(f"metadata type id {v} is unknown")
+        return ValueType(v)
 
 
-_SCALAR = {
+# Fixed-width codecs: struct format per scalar type.
+_FIXED = {
     ValueType.U8: "<B", ValueType.I8: "<b", ValueType.U16: "<H", ValueType.I16: "<h",
     ValueType.U32: "<I", ValueType.I32: "<i", ValueType.U64: "<Q", ValueType.I64: "<q",
     ValueType.F32: "<f", ValueType.F64: "<d",
 }
-_UNSIGNED = (ValueType.U8, ValueType.U16, ValueType.U32, ValueType.U64)
-_SIGNED = (ValueType.I8, ValueType.I16, ValueType.I32, ValueType.I64)
+_INTEGER = {t: t.name[0] == "U" for t in _FIXED if t.name[0] in "UI"}    # type -> unsigned?
+
+
+def _floor_bytes(vt, len_width):
+    """Fewest bytes one value of type `vt` can occupy on disk: a fixed width,
+    a bare length for a string, or an element type plus a length for an array."""
+    if vt in _FIXED:
+        return struct.calcsize(_FIXED[vt])
+    if vt == ValueType.Bool:
+        return 1
+    return len_width if vt == ValueType.String else 4 + len_width
 
 
 class Value:
-    """A typed metadata value (gguf_file.rs:231-245).  `v` is a Python int,
-    float, bool, str, or a list of Value for arrays."""
+    """One metadata value: `type` plus `v`, a Python int / float / bool / str,
+    or a list of Value for an array."""
 
     __slots__ = ("type", "v")
 
@@ -186,70 +184,66 @@ class Value:
         return f"{self.type.name}({self.v!r})"
 
     def __eq__(self, other):
-        return isinstance(other, Value) and self.type == other.type and self.v == other.v
+        return isinstance(other, Value) and (self.type, self.v) == (other.type, other.v)
 
     def value_type(self):
         return self.type
 
-    def _exact(self, vt, what):
+    def _want(self, vt):
         if self.type != vt:
-            _bail(f"not a {what} {self!r}")
+            _refuse(f"metadata value {self!r} is not of type {vt.name}")
         return self.v
 
-    def to_u8(self): return self._exact(ValueType.U8, "u8")
-    def to_i8(self): return self._exact(ValueType.I8, "i8")
-    def to_u16(self): return self._exact(ValueType.U16, "u16")
-    def to_i16(self): return self._exact(ValueType.I16, "i16")
-    def to_u32(self): return self._exact(ValueType.U32, "u32")
-    def to_i32(self): return self._exact(ValueType.I32, "i32")
-    def to_i64(self): return self._exact(ValueType.I64, "i64")
-    def to_f32(self): return self._exact(ValueType.F32, "f32")
-    def to_f64(self): return self._exact(ValueType.F64, "f64")
-    def to_bool(self): return self._exact(ValueType.Bool, "bool")
-    def to_vec(self): return self._exact(ValueType.Array, "vec")
-    def to_string(self): return self._exact(ValueType.String, "string")
+    def to_u8(self): return self._want(ValueType.U8)
+    def to_i8(self): return self._want(ValueType.I8)
+    def to_u16(self): return self._want(ValueType.U16)
+    def to_i16(self): return self._want(ValueType.I16)
+    def to_u32(self): return self._want(ValueType.U32)
+    def to_i32(self): return self._want(ValueType.I32)
+    def to_i64(self): return self._want(ValueType.I64)
+    def to_f32(self): return self._want(ValueType.F32)
+    def to_f64(self): return self._want(ValueType.F64)
+    def to_bool(self): return self._want(ValueType.Bool)
+    def to_vec(self): return self._want(ValueType.Array)
+    def to_string(self): return self._want(ValueType.String)
 
     def to_u64(self):
-        """Unsigned widths and bool upcast; nothing signed (gguf_file.rs:321-332)."""
-        if self.type in _UNSIGNED:
+        """Any unsigned width, or a bool as 0/1; signed types are refused
+        (gguf_file.rs:321-332)."""
+        if _INTEGER.get(self.type) is True:
             return self.v
         if self.type == ValueType.Bool:
             return int(self.v)
-        _bail(f"not a u64 or upcastable to u64 {self!r}")
+        _refuse(f"metadata value {self!r} cannot widen to u64")
 
     def to_count(self):
-        """Any integer width, refused when negative (gguf_file.rs:334-351)."""
-        if self.type in _UNSIGNED:
-            return self.v
-        if self.type in _SIGNED:
-            if self.v < 0:
-                _bail(f"negative count {self.v}")
-            return self.v
-        _bail(f"not a non-negative integer {self!r}")
+        """Any integer width holding a value >= 0 (gguf_file.rs:334-351)."""
+        if self.type not in _INTEGER:
+            _refuse(f"metadata value {self!r} is not an integer count")
+        if self.v < 0:
+            _refuse(f"metadata count {self.v} is negative")
+        return self.v
 
-    # -- encoding (gguf_file.rs:436-480; arrays always carry a u64 length) --
-    def write(self, w):
+    def encode(self):
+        """The value's bytes as a version-2+ file holds them (u64 lengths)."""
         t = self.type
-        if t in _SCALAR:
-            w.write(struct.pack(_SCALAR[t], self.v))
-        elif t == ValueType.Bool:
-            w.write(bytes([1 if self.v else 0]))
-        elif t == ValueType.String:
-            _write_string(w, self.v)
-        else:
-            if not self.v:
-                inner = ValueType.U32
-            else:
-                kinds = {e.type for e in self.v}
-                if len(kinds) != 1:
-                    _bail(f"multiple value-types in the same array {sorted(k.name for k in kinds)}")
-                inner = kinds.pop()
-            w.write(struct.pack("<IQ", int(inner), len(self.v)))
-            for e in self.v:
-                e.write(w)
+        if t in _FIXED:
+            return struct.pack(_FIXED[t], self.v)
+        if t == ValueType.Bool:
+            return b"\x01" if self.v else b"\x00"
+        if t == ValueType.String:
+            return _encode_string(self.v)
+        kinds = {e.type for e in self.v}
+        if len(kinds) > 1:
+            _refuse(f"array mixes element types {sorted(k.name for k in kinds)}")
+        elem = kinds.pop() if kinds else ValueType.U32      # an empty array says U32
+        return struct.pack("<IQ", elem, len(self.v)) + b"".join(e.encode() for e in self.v)
+
+    def write(self, w):
+        w.write(self.encode())
 
 
-# ------------------------------------------------------------ reading ---
+# ---------------------------------------------------------------- reading
 
 class VersionedMagic(enum.IntEnum):
     GgufV1 = 1
@@ -260,156 +254,189 @@ class VersionedMagic(enum.IntEnum):
         return 4 if self == VersionedMagic.GgufV1 else 8
 
 
-class _Reader:
-    """Little-endian reads over a seekable binary stream, with the file size
-    captured once (the reference's remaining_bytes)."""
+_MAGIC_WORDS = (0x46554747, 0x47475546)     # "GGUF" read little or big endian
 
-    def __init__(self, f):
-        self.f = f
-        start = f.tell()
-        self.file_size = f.seek(0, 2)
-        f.seek(start)
 
-    def exact(self, n):
-        b = self.f.read(n)
+class _Wire:
+    """A forward cursor over a seekable binary stream.  `end` is the stream's
+    extent, taken once, so every declared size can be checked against what
+    the file still holds before anything of that size is read."""
+
+    def __init__(self, stream):
+        self.s = stream
+        here = stream.tell()
+        self.end = stream.seek(0, 2)
+        stream.seek(here)
+        self.version = None
+
+    def left(self):
+        return max(0, self.end - self.s.tell())
+
+    def raw(self, n, what):
+        b = self.s.read(n)
         if len(b) != n:
-            _bail("failed to fill whole buffer")
+            _refuse(f"file ends inside {what}")
         return b
 
-    def u8(self): return self.exact(1)[0]
-    def u32(self): return struct.unpack("<I", self.exact(4))[0]
-    def u64(self): return struct.unpack("<Q", self.exact(8))[0]
+    def fixed(self, fmt, what):
+        return struct.unpack(fmt, self.raw(struct.calcsize(fmt), what))[0]
 
-    def pos(self):
-        return self.f.tell()
+    def length(self, what):
+        """A count or byte length: u32 in version 1, u64 after."""
+        return self.fixed("<I" if self.version == VersionedMagic.GgufV1 else "<Q", what)
 
-    def remaining(self):
-        return max(0, self.file_size - self.pos())
-
-    def length(self, magic):
-        return self.u32() if magic == VersionedMagic.GgufV1 else self.u64()
-
-    def string(self, magic):
-        n = self.length(magic)
-        if n > GGUF_MAX_STRING_LENGTH:
-            _bail(f"gguf: string length {n} exceeds max {GGUF_MAX_STRING_LENGTH}")
-        rem = self.remaining()
-        if n > rem:
-            _bail(f"gguf: string length {n} exceeds remaining file bytes {rem}")
-        b = self.exact(n).rstrip(b"\x00")      # trailing NULs occur in practice
-        return b.decode("utf-8", errors="replace")
-
-    def value(self, vt, magic, depth):
-        if depth > GGUF_MAX_VALUE_DEPTH:
-            _bail(f"gguf: value nesting depth exceeds max {GGUF_MAX_VALUE_DEPTH}")
-        if vt in _SCALAR:
-            fmt = _SCALAR[vt]
-            return Value(vt, struct.unpack(fmt, self.exact(struct.calcsize(fmt)))[0])
-        if vt == ValueType.Bool:
-            b = self.u8()
-            if b > 1:
-                _bail(f"unexpected bool value {b}")
-            return Value(vt, bool(b))
-        if vt == ValueType.String:
-            return Value(vt, self.string(magic))
-        inner = ValueType.from_u32(self.u32())
-        n = self.length(magic)
-        if n > GGUF_MAX_ARRAY_ELEMENTS:
-            _bail(f"gguf: array length {n} exceeds max {GGUF_MAX_ARRAY_ELEMENTS}")
-        need = n * inner.min_disk_size(magic.length_prefix_size())
-        rem = self.remaining()
-        if need > rem:
-            _bail(f"gguf: array of {n} elements needs at least {need} bytes, only {rem} remaining")
-        return Value(vt, [self.value(inner, magic, depth + 1) for _ in range(n)])
+    def text(self, what):
+        n = self.length(what)
+        if n > CAP_STRING:
+            _refuse(f"{what}: declared string size {n} is above the cap of {CAP_STRING}")
+        if n > self.left():
+            _refuse(f"{what}: declared string size {n} runs past the end of the file "
+                    f"({self.left()} bytes left)")
+        # Writers in the wild pad strings with NULs; undecodable bytes become U+FFFD.
+        return self.raw(n, what).rstrip(b"\0").decode("utf-8", "replace")
 
 
-def _read_magic(r):
-    m = r.u32()
-    if m not in (0x46554747, 0x47475546):
-        _bail(f"unknown magic 0x{m:08x}")
-    v = r.u32()
-    if v not in (1, 2, 3):
-        _bail(f"gguf: unsupported magic/version Gguf/{v}")
-    return VersionedMagic(v)
+def _decode_value(wire, vt, depth):
+    if depth > CAP_NESTING:
+        _refuse(f"metadata arrays nested deeper than {CAP_NESTING}")
+    if vt in _FIXED:
+        return Value(vt, wire.fixed(_FIXED[vt], "a metadata value"))
+    if vt == ValueType.Bool:
+        b = wire.raw(1, "a metadata value")[0]
+        if b not in (0, 1):
+            _refuse(f"bool byte {b} (must be 0 or 1)")
+        return Value(vt, b == 1)
+    if vt == ValueType.String:
+        return Value(vt, wire.text("a metadata string"))
+    # Array: element type, length, then the elements.
+    elem = ValueType.from_u32(wire.fixed("<I", "an array header"))
+    n = wire.length("an array header")
+    if n > CAP_COUNT:
+        _refuse(f"metadata array of {n} items is above the cap of {CAP_COUNT}")
+    floor = n * _floor_bytes(elem, wire.version.length_prefix_size())
+    if floor > wire.left():
+        _refuse(f"metadata array of {n} items needs {floor} bytes or more, "
+                f"the file has {wire.left()} left")
+    return Value(vt, [_decode_value(wire, elem, depth + 1) for _ in range(n)])
+
+
+def _read_preamble(wire):
+    word = wire.fixed("<I", "the magic word")
+    if word not in _MAGIC_WORDS:
+        _refuse(f"not a GGUF file (magic word 0x{word:08x})")
+    version = wire.fixed("<I", "the version")
+    if version not in VersionedMagic._value2member_map_:
+        _refuse(f"GGUF version {version} is not supported (1, 2 and 3 are)")
+    wire.version = VersionedMagic(version)
+    n_tensors = wire.length("the tensor count")
+    n_kv = wire.length("the metadata count")
+    for n, what in ((n_tensors, "tensor count"), (n_kv, "metadata count")):
+        if n > CAP_COUNT:
+            _refuse(f"{what} {n} is above the cap of {CAP_COUNT}")
+    # Smallest possible entries: a kv is key length + type id + 1 value byte;
+    # a directory entry is name length + rank + type id + offset.
+    p = wire.version.length_prefix_size()
+    floor = n_kv * (p + 4 + 1) + n_tensors * (p + 4 + 4 + 8)
+    if floor > wire.left():
+        _refuse(f"a header of {n_tensors} tensors and {n_kv} metadata entries takes {floor} "
+                f"bytes or more, the file has {wire.left()} left")
+    return n_tensors, n_kv
+
+
+def _read_directory_entry(wire):
+    name = wire.text("a tensor name")
+    rank = wire.fixed("<I", "a tensor rank")
+    if rank > CAP_RANK:
+        _refuse(f"tensor '{name}': rank {rank} is above the GGUF limit of {CAP_RANK}")
+    dim_fmt = "<I" if wire.version == VersionedMagic.GgufV1 else "<Q"
+    file_dims = [wire.fixed(dim_fmt, "tensor dims") for _ in range(rank)]
+    ftype = FileType(wire.fixed("<I", "a tensor type"))
+    offset = wire.fixed("<Q", "a tensor offset")
+    # The file lists the fastest-varying dim first; shapes here are row-major.
+    info = TensorInfo(ftype, file_dims[::-1], offset)
+    info.size_in_bytes()
+    return name, info
+
+
+def _data_alignment(metadata):
+    """general.alignment when it is a non-negative 8/16/32-bit integer,
+    otherwise the default (gguf_file.rs:631-639); zero is refused."""
+    a = metadata.get("general.alignment")
+    ok = (ValueType.U8, ValueType.U16, ValueType.U32, ValueType.I8, ValueType.I16, ValueType.I32)
+    align = a.v if a is not None and a.type in ok and a.v >= 0 else DEFAULT_ALIGNMENT
+    if align == 0:
+        _refuse("general.alignment of 0 is invalid")
+    return align
 
 
 class TensorInfo:
-    """One tensor of the header: type, shape (row-major, as the reference's
-    Shape holds it: the file's dims reversed) and offset from the data start."""
+    """One directory entry: block type, row-major shape, and the payload's
+    offset from the start of the data section."""
 
     __slots__ = ("ggml_dtype", "shape", "offset")
 
     def __init__(self, ggml_dtype, shape, offset):
-        self.ggml_dtype = ggml_dtype if isinstance(ggml_dtype, FileType) else FileType(int(ggml_dtype))
+        self.ggml_dtype = _as_file_type(ggml_dtype)
         self.shape = tuple(int(d) for d in shape)
         self.offset = int(offset)
 
     def __repr__(self):
         return f"TensorInfo({self.ggml_dtype!r}, {list(self.shape)}, offset={self.offset})"
 
-    def size_in_bytes(self):
-        """Header geometry in u64, checked (gguf_file.rs:88-104)."""
-        elems = 1
+    def elements(self):
+        n = 1
         for d in self.shape:
-            elems *= d
-            if elems > _U64_MAX:
-                _bail("gguf: tensor element count overflow")
-        bs = self.ggml_dtype.block_size()
-        if elems % bs:
-            _bail(f"the number of elements {elems} is not divisible by the block size {bs}")
-        b = (elems // bs) * self.ggml_dtype.type_size()
-        if b > _U64_MAX:
-            _bail("gguf: tensor byte size overflow")
-        return b
+            n = _fits_u64(n * d, "tensor element count")
+        return n
+
+    def size_in_bytes(self):
+        """Packed payload bytes, exact in u64."""
+        n, per = self.elements(), self.ggml_dtype.block_size()
+        if n % per:
+            _refuse(f"{n} elements are not a whole number of {self.ggml_dtype.name} blocks ({per} each)")
+        return _fits_u64(n // per * self.ggml_dtype.type_size(), "tensor byte size")
 
     def materialized_size_in_bytes(self):
-        """Host limits for a materialised copy (gguf_file.rs:106-120)."""
-        elems = 1
-        for d in self.shape:
-            elems *= d
-            if elems > _USIZE_MAX:
-                _bail("gguf: host tensor element count overflow")
-        b = self.size_in_bytes()
-        if b > _USIZE_MAX:
-            _bail("gguf: tensor byte size exceeds host usize")
-        if b > _ISIZE_MAX:
-            _bail(f"gguf: tensor byte size {b} exceeds host allocation limit")
-        return b
+        """Bytes of a host copy: also bounded by the host's isize."""
+        size = self.size_in_bytes()
+        if size > _HOST_ISIZE:
+            _refuse(f"tensor of {size} bytes is larger than the host can allocate")
+        return size
 
     def validate_payload(self, f, tensor_data_offset):
-        """Type, host size and file extent, reading nothing (gguf_file.rs:125-144).
-        Leaves `f` at its end.  Returns (absolute start, byte count)."""
+        """Check type, host size and file extent without reading a byte
+        (only the stream's extent is queried).  Returns (start, size)."""
         self.ggml_dtype.validate_file_weight()
         size = self.materialized_size_in_bytes()
         start = tensor_data_offset + self.offset
-        if start > _U64_MAX:
-            _bail("gguf: tensor start offset overflow")
-        file_size = f.seek(0, 2)
-        if file_size < start:
-            _bail(f"gguf: tensor offset {start} exceeds file size {file_size}, no remaining bytes")
-        rem = file_size - start
-        if size > rem:
-            _bail(f"tensor needs {size} bytes at offset {start}, only {rem} remaining in file")
+        if start >= _TWO64:
+            _refuse("tensor payload starts beyond 2^64")
+        extent = f.seek(0, 2)
+        if start > extent:
+            _refuse(f"tensor payload starts at {start}, beyond the end of the file ({extent} bytes)")
+        if size > extent - start:
+            _refuse(f"tensor payload of {size} bytes at {start} runs past the end of the file "
+                    f"({extent - start} bytes left)")
         return start, size
 
     def read_bytes(self, f, tensor_data_offset):
-        """The tensor's packed bytes as the file holds them (numpy uint8)."""
+        """The payload, as stored (uint8)."""
         start, size = self.validate_payload(f, tensor_data_offset)
+        out = np.empty(size, dtype=np.uint8)
         f.seek(start)
-        raw = np.empty(size, dtype=np.uint8)
-        got = f.readinto(memoryview(raw)) if size else 0
-        if got != size:
-            _bail("failed to fill whole buffer")
-        return raw
+        if size and f.readinto(memoryview(out)) != size:
+            _refuse("file ends inside a tensor payload")
+        return out
 
     def read(self, f, tensor_data_offset, device="cuda"):
-        """TensorInfo::read (gguf_file.rs:146-170): validate, read, upload."""
-        raw = self.read_bytes(f, tensor_data_offset)
-        return qtensor_from_ggml(self.ggml_dtype, raw, list(self.shape), device)
+        """Payload -> device QTensor."""
+        return qtensor_from_ggml(self.ggml_dtype, self.read_bytes(f, tensor_data_offset),
+                                 list(self.shape), device)
 
 
 class Content:
-    """A parsed GGUF header (gguf_file.rs:172-178, 532-677)."""
+    """A parsed header: version, metadata (dict of Value), tensor directory
+    (dict of TensorInfo) and the absolute start of the data section."""
 
     def __init__(self, magic, metadata, tensor_infos, tensor_data_offset):
         self.magic = magic
@@ -419,175 +446,130 @@ class Content:
 
     @staticmethod
     def read(f):
-        r = _Reader(f)
-        magic = _read_magic(r)
-        tensor_count = r.length(magic)
-        kv_count = r.length(magic)
-        if tensor_count > GGUF_MAX_ARRAY_ELEMENTS:
-            _bail(f"gguf: tensor_count {tensor_count} exceeds max {GGUF_MAX_ARRAY_ELEMENTS}")
-        if kv_count > GGUF_MAX_ARRAY_ELEMENTS:
-            _bail(f"gguf: metadata_kv_count {kv_count} exceeds max {GGUF_MAX_ARRAY_ELEMENTS}")
-        prefix = magic.length_prefix_size()
-        need = kv_count * (prefix + 4 + 1) + tensor_count * (prefix + 4 + 4 + 8)
-        rem = r.remaining()
-        if need > rem:
-            _bail(f"gguf: header declares {tensor_count} tensors and {kv_count} metadata entries, "
-                  f"needs at least {need} bytes, only {rem} remaining")
-
+        wire = _Wire(f)
+        n_tensors, n_kv = _read_preamble(wire)
         metadata = {}
-        for _ in range(kv_count):
-            key = r.string(magic)
-            vt = ValueType.from_u32(r.u32())
-            metadata[key] = r.value(vt, magic, 0)
+        for _ in range(n_kv):
+            key = wire.text("a metadata key")
+            metadata[key] = _decode_value(wire, ValueType.from_u32(wire.fixed("<I", "a metadata type")), 0)
+        directory = dict(_read_directory_entry(wire) for _ in range(n_tensors))
 
-        tensor_infos = {}
-        for _ in range(tensor_count):
-            name = r.string(magic)
-            nd = r.u32()
-            if nd > GGUF_MAX_TENSOR_DIMS:
-                _bail(f"gguf: tensor '{name}' has {nd} dimensions, max is {GGUF_MAX_TENSOR_DIMS}")
-            fmt = "<%d%s" % (nd, "I" if magic == VersionedMagic.GgufV1 else "Q")
-            dims = list(struct.unpack(fmt, r.exact(struct.calcsize(fmt))))
-            for d in dims:
-                if d > _USIZE_MAX:
-                    _bail(f"gguf: tensor dimension {d} exceeds host usize")
-            dims.reverse()
-            dtype = FileType(r.u32())
-            offset = r.u64()
-            info = TensorInfo(dtype, dims, offset)
-            info.size_in_bytes()
-            tensor_infos[name] = info
-
-        position = r.pos()
-        alignment = DEFAULT_ALIGNMENT
-        a = metadata.get("general.alignment")
-        if a is not None and a.type in (ValueType.U8, ValueType.U16, ValueType.U32, ValueType.I8,
-                                        ValueType.I16, ValueType.I32) and a.v >= 0:
-            alignment = a.v
-        if alignment == 0:
-            _bail("gguf: general.alignment must be nonzero")
-        tdo = position + (alignment - position % alignment) % alignment
-        if tdo > _U64_MAX:
-            _bail("gguf: aligned tensor data offset overflow")
-        for info in tensor_infos.values():
-            if tdo + info.offset + info.size_in_bytes() > _U64_MAX:
-                _bail("gguf: tensor byte range offset overflow")
-        return Content(magic, metadata, tensor_infos, tdo)
+        align = _data_alignment(metadata)
+        data_start = -(-f.tell() // align) * align
+        if data_start >= _TWO64:
+            _refuse(f"data section would start at {data_start}, beyond 2^64")
+        for name, info in directory.items():
+            if data_start + info.offset + info.size_in_bytes() >= _TWO64:
+                _refuse(f"tensor '{name}': data range ends beyond 2^64")
+        return Content(wire.version, metadata, directory, data_start)
 
     def validate_payloads(self, f):
-        """Every tensor an eager loader would materialise, unread (gguf_file.rs:656-664)."""
+        """Check every payload an eager loader would read, reading nothing."""
         for info in self.tensor_infos.values():
             info.validate_payload(f, self.tensor_data_offset)
 
     def tensor(self, f, name, device="cuda"):
-        info = self.tensor_infos.get(name)
-        if info is None:
-            _bail(f"cannot find tensor info for {name}")
-        return info.read(f, self.tensor_data_offset, device)
+        if name not in self.tensor_infos:
+            _refuse(f"no tensor named '{name}' in this file")
+        return self.tensor_infos[name].read(f, self.tensor_data_offset, device)
 
 
-# ------------------------------------------------------------ writing ---
+# ---------------------------------------------------------------- writing
 
-def _write_string(w, s):
+def _encode_string(s):
     b = s.encode("utf-8")
-    w.write(struct.pack("<Q", len(b)))
-    w.write(b)
+    return struct.pack("<Q", len(b)) + b
 
 
-def _pad32(n):
-    return 31 - (31 + n) % 32
+def _pad_to(n, align=_WRITE_PAD):
+    return -n % align
 
 
 def packed_offsets(sizes):
-    """Offsets `write` gives tensors of these byte sizes: each padded to 32 B
-    (gguf_file.rs:696-708)."""
-    out, off = [], 0
+    """Data-section offsets for payloads of these sizes, each padded to 32 B."""
+    out, at = [], 0
     for s in sizes:
-        out.append(off)
-        off += s + _pad32(s)
+        out.append(at)
+        at += s + _pad_to(s)
     return out
 
 
 class HeaderTensor:
-    """A header entry: name, row-major dims, type, offset (gguf_file.rs:684-690)."""
+    """A directory entry to write: name, row-major dims, block type, offset."""
 
     __slots__ = ("name", "dims", "dtype", "offset")
 
     def __init__(self, name, dims, dtype, offset):
         self.name, self.dims, self.offset = name, tuple(dims), int(offset)
-        self.dtype = dtype if isinstance(dtype, FileType) else FileType(int(dtype))
+        self.dtype = _as_file_type(dtype)
 
 
 def write_header(w, metadata, tensors):
-    """A version-2 header padded to 32 B; returns where the data starts
-    (gguf_file.rs:710-738).  `metadata` is a sequence of (key, Value)."""
-    w.write(struct.pack("<IIQQ", 0x46554747, 2, len(tensors), len(metadata)))
+    """A version-2 header, padded to 32 B; returns the data section's start.
+    `metadata` is a sequence of (key, Value), `tensors` of HeaderTensor."""
+    parts = [b"GGUF", struct.pack("<IQQ", 2, len(tensors), len(metadata))]
     for key, value in metadata:
-        _write_string(w, key)
-        w.write(struct.pack("<I", int(value.value_type())))
-        value.write(w)
+        parts += [_encode_string(key), struct.pack("<I", value.value_type()), value.encode()]
     for t in tensors:
-        _write_string(w, t.name)
-        w.write(struct.pack("<I", len(t.dims)))
-        for d in reversed(t.dims):
-            w.write(struct.pack("<Q", d))
-        w.write(struct.pack("<IQ", int(t.dtype), t.offset))
-    w.write(bytes(_pad32(w.tell())))
+        parts += [_encode_string(t.name), struct.pack("<I", len(t.dims))]
+        parts += [struct.pack("<Q", d) for d in t.dims[::-1]]
+        parts.append(struct.pack("<IQ", int(t.dtype), t.offset))
+    blob = b"".join(parts)
+    w.write(blob)
+    w.write(bytes(_pad_to(w.tell())))
     return w.tell()
 
 
 def write(w, metadata, tensors):
-    """Header, then each tensor's packed bytes at its offset, 32 B padded
-    (gguf_file.rs:740-781).  `tensors` is a sequence of (name, QTensor)."""
-    datas = [t.data() for _, t in tensors]
-    offsets = packed_offsets(d.size for d in datas)
-    start = write_header(w, metadata, [HeaderTensor(name, t.shape, int(t.dtype), off)
-                                       for (name, t), off in zip(tensors, offsets)])
-    for off, data in zip(offsets, datas):
-        pos = w.tell()
-        if start + off != pos:
-            _bail(f"internal error, unexpected current position {start} {off} {pos}")
-        w.write(data.tobytes())
-        w.write(bytes(_pad32(data.size)))
+    """A whole file: header, then each payload at its packed offset.
+    `tensors` is a sequence of (name, tensor) where the tensor has `shape`,
+    `dtype` and `data()` (its packed bytes, as QTensor does)."""
+    payloads = [t.data() for _, t in tensors]
+    offsets = packed_offsets(p.size for p in payloads)
+    entries = [HeaderTensor(name, t.shape, int(t.dtype), at) for (name, t), at in zip(tensors, offsets)]
+    data_start = write_header(w, metadata, entries)
+    for entry, p in zip(entries, payloads):
+        if w.tell() != data_start + entry.offset:
+            _refuse(f"writer out of step at '{entry.name}': at {w.tell()}, "
+                    f"expected {data_start + entry.offset}")
+        w.write(p.tobytes())
+        w.write(bytes(_pad_to(p.size)))
 
 
-# ------------------------------------------------- the upload seam ---
+# ------------------------------------------------------- the upload seam
 
 def checked_tensor_bytes(dtype, dims):
-    """ggml_file.rs:121-139 (with check_shape, mod.rs:894-906)."""
+    """Bytes a tensor of these dims takes in `dtype` blocks, refusing what the
+    upload cannot hold: activation-only types, rank 0, an innermost dim that
+    is not whole blocks, and sizes past the host's limits
+    (ggml_file.rs:121-139, mod.rs:894-906)."""
     dtype.validate_file_weight()
-    bs = dtype.block_size()
-    if not dims:
-        _bail(f"scalar tensor cannot be quantized {list(dims)}")
-    if dims[-1] % bs:
-        _bail(f"quantized tensor must have their last dim divisible by block size {list(dims)} {bs}")
-    elems = 1
+    per = dtype.block_size()
+    if len(dims) == 0:
+        _refuse(f"a rank-0 tensor cannot hold {dtype.name} blocks")
+    if dims[-1] % per:
+        _refuse(f"innermost dim of {list(dims)} is not a multiple of the {dtype.name} block size {per}")
+    n = 1
     for d in dims:
-        elems *= d
-        if elems > _USIZE_MAX:
-            _bail("ggml: tensor element count overflow")
-    b = (elems // bs) * dtype.type_size()
-    if b > _USIZE_MAX:
-        _bail("ggml: tensor byte size overflow")
-    if b > _ISIZE_MAX:
-        _bail(f"ggml: tensor byte size {b} exceeds host allocation limit")
-    return b
+        n = _fits_u64(n * d, "tensor element count")
+    size = _fits_u64(n // per * dtype.type_size(), "tensor byte size")
+    if size > _HOST_ISIZE:
+        _refuse(f"tensor of {size} bytes is larger than the host can allocate")
+    return size
 
 
 def qtensor_from_ggml(dtype, raw, dims, device="cuda"):
-    """Raw file bytes -> a device QTensor (ggml_file.rs:180-228): the first
-    size_in_bytes bytes of `raw`, uploaded unchanged."""
-    from .quantized import QTensor, GgmlDType
+    """Packed file bytes -> a device QTensor, uploaded unchanged.  `raw` may
+    be longer than the tensor; only its first checked_tensor_bytes are used."""
+    from .quantized import GgmlDType, QTensor
 
-    dtype = dtype if isinstance(dtype, FileType) else FileType(int(dtype))
+    dtype = _as_file_type(dtype)
     dims = [int(d) for d in dims]
     size = checked_tensor_bytes(dtype, dims)
-    raw = np.frombuffer(raw, dtype=np.uint8) if not isinstance(raw, np.ndarray) else raw.view(np.uint8)
+    raw = raw.view(np.uint8) if isinstance(raw, np.ndarray) else np.frombuffer(raw, dtype=np.uint8)
     if raw.size < size:
-        _bail(f"ggml: payload length {raw.size} is shorter than expected {size} bytes")
-    try:
-        gd = GgmlDType(dtype.id)
-    except ValueError:
+        _refuse(f"payload holds {raw.size} bytes, the tensor needs {size}")
+    if dtype.id not in GgmlDType._value2member_map_:
         raise LloomHipError(2, f"quantized type {dtype.name} has no kernel on the HIP arm "
-                               f"(Q8_0, Q4K, Q6K, F32, F16, BF16 are uploaded)") from None
-    return QTensor.from_data(raw[:size], dims, gd, device=device)
+                               f"(Q8_0, Q4K, Q6K, F32, F16, BF16 are uploaded)")
+    return QTensor.from_data(raw[:size], dims, GgmlDType(dtype.id), device=device)

@@ -45,31 +45,31 @@ def test_empty_header_loads():
 
 def test_oversized_counts():
     """gguf_tests.rs:46-54"""
-    rejects(header(0, 1 << 31), "metadata_kv_count")
-    rejects(header(1 << 31, 0), "tensor_count")
+    rejects(header(0, 1 << 31), "metadata count")
+    rejects(header(1 << 31, 0), "tensor count")
 
 
 def test_oversized_string_length():
     """gguf_tests.rs:56-62"""
-    rejects(header(1, 0) + struct.pack("<Q", 1 << 31) + bytes(64), "string length")
+    rejects(header(1, 0) + struct.pack("<Q", 1 << 31) + bytes(64), "string size")
 
 
 def test_oversized_array_length():
     """gguf_tests.rs:64-73"""
     buf = header(0, 1) + lp(b"k") + struct.pack("<IIQ", 9, 0, 1 << 31) + bytes(64)
-    rejects(buf, "array length")
+    rejects(buf, "array of")
 
 
 def test_oversized_n_dimensions():
     """gguf_tests.rs:75-82"""
-    rejects(header(1, 0) + lp(b"t") + struct.pack("<I", 0xFFFFFFFF) + bytes(64), "dimensions")
+    rejects(header(1, 0) + lp(b"t") + struct.pack("<I", 0xFFFFFFFF) + bytes(64), "rank")
 
 
 def test_deeply_nested_arrays():
     """gguf_tests.rs:84-99"""
     buf = header(0, 1) + lp(b"k") + struct.pack("<I", 9)
     buf += struct.pack("<IQ", 9, 1) * 256 + struct.pack("<IQ", 0, 0)
-    rejects(buf, "nesting depth")
+    rejects(buf, "nested deeper")
 
 
 def test_empty_v1_header_loads():
@@ -86,8 +86,8 @@ def test_v1_tensor_dims_are_u32():
 
 
 def test_bad_magic_and_version():
-    rejects(b"GGUX" + bytes(20), "unknown magic")
-    rejects(b"GGUF" + struct.pack("<IQQ", 4, 0, 0), "unsupported magic/version")
+    rejects(b"GGUX" + bytes(20), "not a GGUF file")
+    rejects(b"GGUF" + struct.pack("<IQQ", 4, 0, 0), "version 4 is not supported")
 
 
 def test_tensor_size_exceeding_file():
@@ -95,13 +95,13 @@ def test_tensor_size_exceeding_file():
     buf = header(1, 0) + lp(b"t") + struct.pack("<IQIQ", 1, 1 << 30, 0, 0)
     f = io.BytesIO(buf)
     c = Content.read(f)
-    with pytest.raises(GgufError, match="remaining"):
+    with pytest.raises(GgufError, match="end of the file"):
         c.tensor(f, "t", device="cpu")
 
 
 def test_string_length_above_remaining_file():
     """gguf_tests.rs:138-144"""
-    rejects(header(1, 0) + struct.pack("<Q", 1 << 20) + bytes(64), "string length")
+    rejects(header(1, 0) + struct.pack("<Q", 1 << 20) + bytes(64), "string size")
 
 
 def tensor_header(dims, dtype, offset):
@@ -117,7 +117,7 @@ def alignment_header(alignment):
 
 def test_alignment():
     """gguf_tests.rs:230-239: zero refused, any positive alignment kept."""
-    rejects(alignment_header(0), "alignment must be nonzero")
+    rejects(alignment_header(0), "alignment of 0")
     for a in (1, 8, 24, 32):
         buf = alignment_header(a)
         assert Content.read(io.BytesIO(buf)).tensor_data_offset == -(-len(buf) // a) * a
@@ -133,15 +133,15 @@ def test_signed_and_negative_alignment():
 
 def test_tensor_element_and_byte_overflow():
     """gguf_tests.rs:241-258"""
-    rejects(tensor_header([U64_MAX, 2], 0, 0), "element count overflow")
-    rejects(tensor_header([U64_MAX // 4 + 1], 0, 0), "byte size overflow")
+    rejects(tensor_header([U64_MAX, 2], 0, 0), "element count does not fit")
+    rejects(tensor_header([U64_MAX // 4 + 1], 0, 0), "byte size does not fit")
 
 
 def test_large_header_inspectable_materialisation_refused():
     """gguf_tests.rs:260-272"""
     f = io.BytesIO(tensor_header([ISIZE_MAX // 4 + 1], 0, 0))
     c = Content.read(f)
-    with pytest.raises(GgufError, match="host allocation limit"):
+    with pytest.raises(GgufError, match="larger than the host can allocate"):
         c.tensor(f, "t", device="cpu")
 
 
@@ -154,20 +154,20 @@ def test_scalar_zero_axis_shapes_kept():
 
 def test_tensor_start_end_overflow():
     """gguf_tests.rs:288-300: the 57-byte header aligns to 64."""
-    rejects(tensor_header([1], 0, U64_MAX), "byte range offset overflow")
+    rejects(tensor_header([1], 0, U64_MAX), "ends beyond 2^64")
     assert len(tensor_header([1], 0, 0)) == 57
-    rejects(tensor_header([1], 0, U64_MAX - 66), "byte range offset overflow")
+    rejects(tensor_header([1], 0, U64_MAX - 66), "ends beyond 2^64")
     # two bytes lower and the F32 payload ends at u64::MAX exactly
     Content.read(io.BytesIO(tensor_header([1], 0, U64_MAX - 68)))
 
 
 def test_direct_tensor_info_read():
     """gguf_tests.rs:302-323"""
-    for dims, offset, base, want in [([U64_MAX, 2], 0, 0, "element count overflow"),
-                                     ([U64_MAX // 4 + 1], 0, 0, "byte size"),
-                                     ([1], U64_MAX, 1, "start offset overflow"),
-                                     ([0], 1, 0, "exceeds file size"),
-                                     ([1], 0, 0, "remaining")]:
+    for dims, offset, base, want in [([U64_MAX, 2], 0, 0, "element count does not fit"),
+                                     ([U64_MAX // 4 + 1], 0, 0, "byte size does not fit"),
+                                     ([1], U64_MAX, 1, "starts beyond 2^64"),
+                                     ([0], 1, 0, "beyond the end of the file"),
+                                     ([1], 0, 0, "past the end")]:
         info = TensorInfo(FileType(0), dims, offset)
         with pytest.raises(GgufError) as e:
             info.read(io.BytesIO(b""), base, device="cpu")
@@ -197,7 +197,7 @@ class _Positioned(io.RawIOBase):
 
 def test_alignment_roundup_overflow():
     """gguf_tests.rs:325-359"""
-    with pytest.raises(GgufError, match="aligned tensor data offset overflow"):
+    with pytest.raises(GgufError, match="data section would start"):
         Content.read(_Positioned(header(0, 0), U64_MAX - 31))
 
 
@@ -220,25 +220,25 @@ def test_eager_payload_preflight():
     for dt in (9, 15):
         ft = FileType(dt)
         c.tensor_infos["extra"] = TensorInfo(ft, [ft.block_size()], 48)
-        with pytest.raises(GgufError, match="not supported yet"):
+        with pytest.raises(GgufError, match="activation-only"):
             c.validate_payloads(_Extent(U64_MAX))
-        with pytest.raises(GgufError, match="not supported yet"):
+        with pytest.raises(GgufError, match="activation-only"):
             qtensor_from_ggml(dt, b"", [ft.block_size()], device="cpu")
     c.tensor_infos["extra"] = TensorInfo(FileType(0), [4], 48)
-    with pytest.raises(GgufError, match="only 15 remaining"):
+    with pytest.raises(GgufError, match="15 bytes left"):
         c.validate_payloads(_Extent(63))
     c.tensor_infos["extra"] = TensorInfo(FileType(0), [0], 64)
     c.validate_payloads(_Extent(64))
     c.tensor_data_offset = 1
     c.tensor_infos["extra"].offset = U64_MAX
-    with pytest.raises(GgufError, match="offset overflow"):
+    with pytest.raises(GgufError, match="starts beyond 2"):
         c.validate_payloads(_Extent(U64_MAX))
     c.tensor_data_offset = 0
     c.tensor_infos["extra"] = TensorInfo(FileType(2), [31], 0)
-    with pytest.raises(GgufError, match="not divisible"):
+    with pytest.raises(GgufError, match="whole number of"):
         c.validate_payloads(_Extent(64))
     c.tensor_infos["extra"] = TensorInfo(FileType(0), [ISIZE_MAX // 4 + 1], 0)
-    with pytest.raises(GgufError, match="host allocation limit"):
+    with pytest.raises(GgufError, match="larger than the host can allocate"):
         c.validate_payloads(_Extent(U64_MAX))
 
 
@@ -258,9 +258,9 @@ def test_a_count_is_any_non_negative_integer():
 
 
 def test_unknown_tensor_dtype_and_bad_bool():
-    rejects(tensor_header([4], 5, 0), "unknown dtype for tensor 5")
-    rejects(header(0, 1) + lp(b"b") + struct.pack("<IB", 7, 2) + bytes(16), "unexpected bool value 2")
-    rejects(header(0, 1) + lp(b"x") + struct.pack("<I", 13) + bytes(16), "unrecognized value-type")
+    rejects(tensor_header([4], 5, 0), "type id 5 is not")
+    rejects(header(0, 1) + lp(b"b") + struct.pack("<IB", 7, 2) + bytes(16), "bool byte 2")
+    rejects(header(0, 1) + lp(b"x") + struct.pack("<I", 13) + bytes(16), "metadata type id 13")
 
 
 def test_strings_strip_trailing_nuls_and_decode_lossy():
@@ -337,7 +337,7 @@ def test_metadata_values_round_trip():
             assert c.metadata[k] == v
         else:
             assert c.metadata[k] == v, k
-    with pytest.raises(GgufError, match="multiple value-types"):
+    with pytest.raises(GgufError, match="mixes element types"):
         write(io.BytesIO(), [("m", Value(ValueType.Array, [Value(ValueType.U8, 1), Value(ValueType.I8, 1)]))], [])
 
 
@@ -354,13 +354,13 @@ def test_file_type_geometry():
 
 
 def test_upload_refusals_before_any_device_work():
-    with pytest.raises(GgufError, match="shorter than expected"):
+    with pytest.raises(GgufError, match="the tensor needs"):
         qtensor_from_ggml(12, bytes(100), [1, 256], device="cpu")
-    with pytest.raises(GgufError, match="scalar tensor"):
+    with pytest.raises(GgufError, match="rank-0"):
         qtensor_from_ggml(0, bytes(4), [], device="cpu")
-    with pytest.raises(GgufError, match="last dim divisible"):
+    with pytest.raises(GgufError, match="innermost dim"):
         qtensor_from_ggml(8, bytes(68), [2, 34], device="cpu")
     with pytest.raises(LloomHipError, match="no kernel on the HIP arm"):
         qtensor_from_ggml(13, bytes(176), [1, 256], device="cpu")
-    with pytest.raises(GgufError, match="cannot find tensor info for w"):
+    with pytest.raises(GgufError, match="no tensor named 'w'"):
         Content.read(io.BytesIO(header(0, 0))).tensor(io.BytesIO(header(0, 0)), "w", device="cpu")
