@@ -21,10 +21,12 @@ hipError_t launch_embedding(int type, const void* w, int64_t rows, int64_t hidde
 
 // quant.hip: Q8_K activations in the split layout the MFMA kernels read:
 // qs int8 [m][k] then d f32 [k/256][mp] (m padded to mp, a multiple of 16),
-// 256-byte aligned.
+// 256-byte aligned, then (when asked for) the sub-block sums as an MFMA
+// operand, int8 [k/256][mp][16].
 size_t split_q8k_bytes(int64_t k, int64_t m);
-void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d);
-hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s);
+void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d, int8_t** bsp = nullptr);
+hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s,
+                                     int8_t* bsp = nullptr);
 
 // matvec.hip: m <= 16.  Rows up to MV_DOT_MAX_ROWS (Q4_K on a weight of at
 // most 2048^2 elements: up to 4) take the fused dot4 kernel; more rows take

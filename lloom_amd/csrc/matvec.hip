@@ -409,6 +409,44 @@ __device__ __forceinline__ void mf_compute(const MfW<TYPE>& w, const long (&a)[8
     }
 }
 
+// mf_compute's Q4_K arithmetic with the min term on two MFMAs instead of
+// eight: bsum_j = sum of the 32 quantized x of sub-block j = 64 hi_j + lo_j
+// (both int8, from k_quantize_split_q8k's bsp); the activation operand `ab`
+// holds lo_0..7 in lane group 0 and hi_0..7 in group 1 (zero in 2, 3), the
+// weight operand the eight 6-bit mins in group 0 (for the lo sums) or group
+// 1 (for the hi sums), so sum_j m_j bsum_j = D(lo) + 64 D(hi), exact.  The
+// scales and mins are unpacked as whole dwords (scales 0-3 are bytes of
+// hdr.y & 0x3f..., 4-7 are the low nibbles of hdr.w with hdr.y's top bits).
+// Every integer sum equals mf_compute's, so do the outputs.
+__device__ __forceinline__ void mf_compute_q4k_b(const MfW<T_Q4K>& w, const long (&a)[8], long ab, const float4& dy,
+                                                 int g, float (&out)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    const float d = f16_to_f32(w.hdr.x & 0xffffu), dmin = f16_to_f32(w.hdr.x >> 16);
+    const uint32_t sc_lo = w.hdr.y & 0x3F3F3F3Fu, sc_hi = (w.hdr.w & 0x0F0F0F0Fu) | ((w.hdr.y >> 2) & 0x30303030u);
+    const uint32_t mn_lo = w.hdr.z & 0x3F3F3F3Fu,
+                   mn_hi = ((w.hdr.w >> 4) & 0x0F0F0F0Fu) | ((w.hdr.z >> 2) & 0x30303030u);
+    const long mins = (long)(((uint64_t)mn_hi << 32) | mn_lo);
+    v4i accs = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int sc = (int)byte_of(j < 4 ? sc_lo : sc_hi, j & 3);
+        const int c = j >> 1, sh = (j & 1) * 4;
+        const uint32_t lo = (w.q[c].x >> sh) & 0x0F0F0F0Fu, hi = (w.q[c].y >> sh) & 0x0F0F0F0Fu;
+        const long bw = (long)(((uint64_t)hi << 32) | lo);
+        const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; t++) accs[t] += __mul24(sc, dj[t]);
+    }
+    v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ab, g == 1 ? mins : 0l, zero, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 4; t++) mh[t] <<= 6;
+    const v4i accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(ab, g == 0 ? mins : 0l, mh, 0, 0, 0);
+    out[0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
+    out[1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
+    out[2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
+    out[3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
+}
+
 // MA > 1 (prefill): a workgroup layer (grid y) covers MA 16-row activation
 // tiles against the same weight tiles, so each weight superblock is unpacked
 // once for 16 MA activation rows; the activation operands then load at the
@@ -776,6 +814,176 @@ __global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ ps
     store_epi(&Y[i], v, epi);
 }
 
+// ---------------------- 3..16 rows, K <= 2048: the operands through LDS --
+// The same dots as k_mv_mfma (mf_compute on its operand layout) with a
+// load shape fit for a launch this short.  A workgroup of 4 * NT waves owns
+// NT 16-row tiles over all of K.  Its weights (NT x 16 consecutive rows, one
+// contiguous run each) and the quantized x (m rows of K bytes, contiguous)
+// go to LDS as global_load_lds DMAs of 1 KB a wave instruction, so every
+// load instruction covers eight whole cache lines; loading the MFMA operand
+// layout straight from global memory (16 rows x 48 bytes an instruction)
+// multiplies the memory requests and costs ~2 us of a ~6 us call.  After
+// one barrier, wave (tile, q) computes superblocks q, q + 4, ... of its tile
+// out of LDS, and the four K quarters of a tile add up through LDS.
+// Rows past n load the last valid bytes again (their sums are never
+// stored); activation rows past m are zeroed by select.
+constexpr int MV_DMA_KMAX = 2048;
+
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// LDS pitch of a row of `bytes` (a multiple of 16): padded so that its
+// dword count is 4 mod 8 (mod 32 banks: rows r and r + 8 share banks, so a
+// 16-row b128 read takes two passes instead of sixteen).
+constexpr int lds_pitch(int bytes) {
+    int p = (bytes + 15) & ~15;
+    while ((p / 4) % 8 != 4) p += 16;
+    return p;
+}
+
+// DMA of `rows` rows of `bytes` bytes (global row stride `gstride`) into
+// LDS rows of pitch P: the LDS image is cut in 1 KB wave instructions; a
+// lane's 16 bytes are data of one row or pad (pad lanes reload the last
+// data piece).  `lim` clamps every source offset to the valid bytes.
+template <int P, int WV>
+__device__ __forceinline__ void dma_rows(const uint8_t* __restrict__ src, int bytes, int rows, int64_t gstride, int lim,
+                                         uint8_t* lds, int wave, int lane) {
+    const int total = rows * P;
+    for (int i = wave; i * 1024 < total; i += WV) {
+        const int L = i * 1024 + 16 * lane;
+        const int r = L / P, c = L - r * P;
+        const int64_t off = (int64_t)r * gstride + min(c, bytes - 16);
+        dma16(src + min(off, (int64_t)lim), lds + i * 1024);
+    }
+}
+
+template <int TYPE, int NSB, int NT>
+__global__ __launch_bounds__(256 * NT) void k_mv_dma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                     const float* __restrict__ xd, const int8_t* __restrict__ bsp,
+                                                     float* __restrict__ Y, int n, int m, int mp, int epi) {
+    constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int WV = 4 * NT, K = 256 * NSB, RB = NSB * BB;
+    static_assert(RB % 16 == 0, "rows must be whole 16-byte DMA pieces");
+    constexpr int WP = lds_pitch(RB), XP = lds_pitch(K);
+    constexpr int NJ = (NSB + 3) / 4;  // superblocks a wave computes
+    // each DMA instruction writes 1 KB; the slack takes the last one's overhang
+    __shared__ __align__(16) uint8_t wl[NT][16 * WP + 1024];
+    __shared__ __align__(16) uint8_t xl[16 * XP + 1024];
+    __shared__ float4 part[3][NT][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int r0 = (blockIdx.x * NT + t) * 16;
+        const int valid = max(1, min(16, n - r0));
+        // rows past n reload the last valid piece (its overhang is the tail pad)
+        dma_rows<WP, WV>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave, lane);
+    }
+    dma_rows<XP, WV>((const uint8_t*)xq, K, m, K, m * K - 16, xl, wave, lane);
+    const int t = wave >> 2, q = wave & 3;
+    float4 dy[NJ];
+    long ab[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int sb = min(q + 4 * j, NSB - 1);
+        dy[j] = *(const float4*)(xd + (int64_t)sb * mp + 4 * g);
+        if constexpr (TYPE == T_Q4K) {
+            // groups 0 and 1 read the lo and hi sums of row c16; 2 and 3 reread group 1's
+            // (loaded by every lane and masked: a load under the condition
+            // would wait for the DMAs in flight)
+            const long v = *(const long*)(bsp + ((int64_t)sb * mp + c16) * 16 + 8 * min(g, 1));
+            ab[j] = v & -(long)(g < 2 && c16 < m);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const bool arow_ok = c16 < m;
+    const uint8_t* trow = &wl[t][c16 * WP];
+    const uint8_t* xrow = &xl[c16 * XP + 64 * g];
+    float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int sb = q + 4 * j;
+        if (sb < NSB) {  // wave-uniform
+            MfW<TYPE> wu;
+            mf_load<TYPE>(trow + sb * BB, g, wu);
+            long a[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 v = *(const uint4*)(xrow + sb * 256 + 16 * i);
+                a[2 * i] = arow_ok ? (long)(((uint64_t)v.y << 32) | v.x) : 0l;
+                a[2 * i + 1] = arow_ok ? (long)(((uint64_t)v.w << 32) | v.z) : 0l;
+            }
+            if constexpr (TYPE == T_Q4K) mf_compute_q4k_b(wu, a, ab[j], dy[j], g, out);
+            else mf_compute<TYPE>(wu, a, dy[j], g, out);
+        }
+    }
+    if (q) part[q - 1][t][lane] = make_float4(out[0], out[1], out[2], out[3]);
+    __syncthreads();
+    if (q) return;
+#pragma unroll
+    for (int w = 0; w < 3; w++) {
+        const float4 p = part[w][t][lane];
+        out[0] += p.x;
+        out[1] += p.y;
+        out[2] += p.z;
+        out[3] += p.w;
+    }
+    const int row = (blockIdx.x * NT + t) * 16 + c16;
+    if (row < n) {
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            if (4 * g + v < m) store_epi(&Y[(int64_t)(4 * g + v) * n + row], out[v], epi);
+    }
+}
+
+// LLOOM_HIP_MV_DMA: 0 = off (k_mv_mfma), 1 / 2 = tiles a workgroup, unset =
+// two tiles from 384 row tiles up (n >= 6144: 7.6 against 7.9 us at m = 16,
+// with fewer the grid gets too small: 7.1 against 6.7 on n = 2048)
+static int mv_dma_env() {
+    static const int v = [] {
+        const char* e = getenv("LLOOM_HIP_MV_DMA");
+        return e ? atoi(e) : -1;
+    }();
+    return v;
+}
+static bool mv_dma_on() { return mv_dma_env() != 0; }
+static int mv_dma_nt(int64_t tiles) { return mv_dma_env() > 0 ? mv_dma_env() : tiles >= 384 ? 2 : 1; }
+
+template <int TYPE, int NSB>
+static hipError_t launch_mv_dma_k(const void* w, float* y, int64_t n, int64_t m, const int8_t* xq, const float* xd,
+                                  const int8_t* bsp, int epi, hipStream_t s) {
+    const int mp = (int)((m + 15) & ~(int64_t)15);
+    const int64_t tiles = (n + 15) / 16;
+    if (mv_dma_nt(tiles) == 2)
+        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2>), dim3((unsigned)((tiles + 1) / 2)), dim3(512), 0, s,
+                           (const uint8_t*)w, xq, xd, bsp, y, (int)n, (int)m, mp, epi);
+    else
+        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1>), dim3((unsigned)tiles), dim3(256), 0, s, (const uint8_t*)w, xq, xd,
+                           bsp, y, (int)n, (int)m, mp, epi);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+static hipError_t launch_mv_dma(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xq,
+                                const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
+    if constexpr (TYPE == T_Q6K) {
+        return launch_mv_dma_k<TYPE, 8>(w, y, n, m, xq, xd, bsp, epi, s);
+    } else {
+        switch (k / 256) {
+            case 1: return launch_mv_dma_k<TYPE, 1>(w, y, n, m, xq, xd, bsp, epi, s);
+            case 2: return launch_mv_dma_k<TYPE, 2>(w, y, n, m, xq, xd, bsp, epi, s);
+            case 3: return launch_mv_dma_k<TYPE, 3>(w, y, n, m, xq, xd, bsp, epi, s);
+            case 4: return launch_mv_dma_k<TYPE, 4>(w, y, n, m, xq, xd, bsp, epi, s);
+            case 5: return launch_mv_dma_k<TYPE, 5>(w, y, n, m, xq, xd, bsp, epi, s);
+            case 6: return launch_mv_dma_k<TYPE, 6>(w, y, n, m, xq, xd, bsp, epi, s);
+            case 7: return launch_mv_dma_k<TYPE, 7>(w, y, n, m, xq, xd, bsp, epi, s);
+            default: return launch_mv_dma_k<TYPE, 8>(w, y, n, m, xq, xd, bsp, epi, s);
+        }
+    }
+}
+
 template <int TYPE, int MA>
 static hipError_t launch_mv_mfma(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xq,
                                  const float* xd, int epi, hipStream_t s, float* psum = nullptr) {
@@ -841,9 +1049,15 @@ hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int6
     if (type != T_Q8_0 && !mv_dot(type, n, k, m)) {
         int8_t* xq;
         float* xd;
-        split_q8k_ptrs(ws, k, m, &xq, &xd);
-        hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
+        int8_t* bsp;
+        split_q8k_ptrs(ws, k, m, &xq, &xd, &bsp);
+        // Q6_K rows are 16-byte multiples (whole DMA pieces) at k = 2048 only
+        const bool dma = k <= MV_DMA_KMAX && m <= 16 && mv_dma_on() && (type == T_Q4K || k == MV_DMA_KMAX);
+        hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s, dma && type == T_Q4K ? bsp : nullptr);
         if (e != hipSuccess) return e;
+        if (dma)
+            return type == T_Q4K ? launch_mv_dma<T_Q4K>(w, y, n, k, m, xq, xd, bsp, epi, s)
+                                 : launch_mv_dma<T_Q6K>(w, y, n, k, m, xq, xd, bsp, epi, s);
         float* ps = mv_psum(ws, k, m);
         return type == T_Q4K ? launch_mv_mfma<T_Q4K, 1>(w, y, n, k, m, xq, xd, epi, s, ps)
                              : launch_mv_mfma<T_Q6K, 1>(w, y, n, k, m, xq, xd, epi, s, ps);

@@ -38,9 +38,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
 // superblock permuted so that element 32j + 8g + b (sub-block j, lane group
 // g, byte b) sits at 64g + 8j + b: an MFMA lane group's 8 bytes of every
 // sub-block are then one contiguous 64-byte run.  One block per wave; the
-// values are those of k_quantize_q8k.
+// values are those of k_quantize_q8k.  With bsp, also the 32-element sums
+// of every sub-block j as an MFMA operand: bsp [k/256][mp][16] bytes, byte j
+// = sum & 63 and byte 8 + j = sum >> 6 (sum = 64 hi + lo, both int8).
 __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restrict__ x, int8_t* __restrict__ qs,
-                                                            float* __restrict__ dt, int m, int k, int mp) {
+                                                            float* __restrict__ dt, int8_t* __restrict__ bsp, int m,
+                                                            int k, int mp) {
     const int lane = threadIdx.x & 63;
     const int nsb = k >> 8;
     const int sb = blockIdx.y * 4 + (threadIdx.x >> 6), mi = blockIdx.x;
@@ -53,25 +56,37 @@ __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restr
     const int off = 64 * ((lane & 7) >> 1) + 8 * (lane >> 3) + 4 * (lane & 1);
     *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + off) = q;
     if (lane == 0) dt[(int64_t)sb * mp + mi] = d;
+    if (bsp) {
+        // bs is the 16-element sum of the lane's quad; the 8 lanes of
+        // sub-block lane / 8 are two quads
+        const int s32 = bs + dppi<DPP_HALF_MIRROR>(bs);
+        if ((lane & 7) == 0) {
+            int8_t* o = bsp + ((int64_t)sb * mp + mi) * 16 + (lane >> 3);
+            o[0] = (int8_t)(s32 & 63);
+            o[8] = (int8_t)(s32 >> 6);
+        }
+    }
 }
 
 static int64_t pad16(int64_t m) { return (m + 15) & ~(int64_t)15; }
 
 size_t split_q8k_bytes(int64_t k, int64_t m) {
     size_t qb = ((size_t)m * k + 255) & ~(size_t)255;
-    return qb + (size_t)(k / 256) * pad16(m) * sizeof(float);
+    return qb + (size_t)(k / 256) * pad16(m) * (sizeof(float) + 16);
 }
 
-void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d) {
+void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d, int8_t** bsp) {
     size_t qb = ((size_t)m * k + 255) & ~(size_t)255;
     *qs = (int8_t*)base;
     *d = (float*)((uint8_t*)base + qb);
+    if (bsp) *bsp = (int8_t*)((uint8_t*)base + qb + (size_t)(k / 256) * pad16(m) * sizeof(float));
 }
 
-hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s) {
+hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s,
+                                     int8_t* bsp) {
     const int64_t nsb = k / 256;
     hipLaunchKernelGGL(k_quantize_split_q8k, dim3((unsigned)m, (unsigned)((nsb + 3) / 4)), dim3(256), 0, s, x, qs, d,
-                       (int)m, (int)k, (int)pad16(m));
+                       bsp, (int)m, (int)k, (int)pad16(m));
     return hipGetLastError();
 }
 
