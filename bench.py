@@ -12,8 +12,11 @@ timed steps are replayed from one HIP graph (decode launches are a few
 microseconds each; the graph keeps host launch overhead out), bracketed by
 HIP events on the stream they run on.
 
-`roofline` is the dominant kernel's: the single-row decode matvec (C2 at
-B=1), algorithmic bytes per launch over its average launch time.
+`roofline` is the single-row decode matvec's (C2 at B=1), algorithmic bytes
+per launch over its average launch time, with `roofline.also` giving the same
+for the B=8 and B=16 calls (activation quantizer + MFMA decode kernel), which
+take half of a sweep step; `traffic` is the measured HBM bytes of a call
+(profiles/traffic_c2_b*.json).
 
 `details` adds the other BASELINE configs (C1 Q8_0 decode, C3 Q4_K prefill
 TFLOP/s, C4 decoder-layer decode, C5 routed experts) measured the same way,
@@ -48,6 +51,8 @@ def parse():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="launch only the roofline kernel (C2 at B=1, eagerly, on cold weight copies) and a "
                          "64 MiB device copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
+    ap.add_argument("--pmc-probe-b", type=int, default=1, choices=[1, 2, 4, 8, 16],
+                    help="activation rows of the --pmc-probe calls (C2; B >= 5 is two kernels a call)")
     ap.add_argument("--pmc-probe-type", default="q4k", choices=["q4k", "q8_0", "q6k"],
                     help="weight type of --pmc-probe-prefill (q4k: C3's [8192, 2048]; q8_0 [8192, 2048]; "
                          "q6k [2048, 8192])")
@@ -163,10 +168,11 @@ def main():
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
+        pb = args.pmc_probe_b
         for i in range(20):
-            launch(1, rot.tensors[i % len(rot)])()
+            launch(pb, rot.tensors[i % len(rot)])()
         torch.cuda.synchronize()
-        print(json.dumps({"pmc_probe": "c2_b1", "algorithmic_bytes": algo[1], "copy_bytes": 64 << 20}))
+        print(json.dumps({"pmc_probe": "c2_b%d" % pb, "algorithmic_bytes": algo[pb], "copy_bytes": 64 << 20}))
         return
 
     sweep = []
@@ -194,22 +200,39 @@ def main():
         t = time_graph(fns, 3, 1) / len(fns)
         warm[str(b)] = {"us": round(t * 1e6, 3), "GB/s": round(algo[b] / t / 1e9, 1)}
     warm["note"] = "one weight copy replayed: MALL-resident, not an HBM figure"
+    # the floor under every per-launch figure: a one-element fill kernel in
+    # the same graph timing (the dispatch and completion of one kernel)
+    one = torch.empty(1, device=dev)
+    t_floor = time_graph([(lambda: one.fill_(1.0)) for _ in range(len(rot))], 3, 1) / len(rot)
     details = {"c2_q4k_decode_per_batch": per_b, "c2_q4k_decode_warm": warm, "rotation_copies": len(rot),
-               "rotation_bytes": len(rot) * wbytes}
-    # Roofline of the path's dominant kernel: the single-row decode matvec
-    # (C2 at B=1, one kernel per call): algorithmic bytes per launch over the
-    # kernel's average launch time, from the per-B graph above (events on the
-    # replay stream).  traffic: measured HBM bytes per launch, from the
-    # committed rocprofv3 FETCH_SIZE / WRITE_SIZE calibration when present.
-    t_b1 = per_b["1"]["us"] * 1e-6
-    ach = algo[1] / t_b1 / 1e9
-    roofline = {"bound": "hbm", "kernel": "k_matvec<Q4_K, 1 row> (C2, B=1)", "achieved": round(ach, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                "algorithmic_bytes": algo[1], "us_per_launch": per_b["1"]["us"], "traffic": None}
-    tpath = os.path.join(ROOT, "profiles", "traffic_c2_b1.json")
-    if os.path.exists(tpath):
+               "rotation_bytes": len(rot) * wbytes,
+               "graph_launch_floor_us": {"us": round(t_floor * 1e6, 3),
+                                         "note": "a 1-element fill kernel per launch, same graph timing: "
+                                                 "the fixed cost in every per-launch figure"}}
+    # Roofline of the path's kernels: the single-row decode matvec (C2 at
+    # B=1, one kernel a call) and, in `also`, the calls at B=8 and B=16 (the
+    # Q8_K activation quantizer, then the MFMA decode kernel), which take half
+    # of the sweep's time: algorithmic bytes per call over the call's average
+    # time, from the per-B graphs above (events on the replay stream).
+    # traffic: measured HBM bytes per call, from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE calibration when present.
+    def traffic_of(b):
+        tpath = os.path.join(ROOT, "profiles", "traffic_c2_b%d.json" % b)
+        if not os.path.exists(tpath):
+            return None
         with open(tpath) as f:
-            roofline["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+            return json.load(f).get("hbm_bytes_per_launch")
+
+    def roof(b, kernel):
+        t = per_b[str(b)]["us"] * 1e-6
+        ach = algo[b] / t / 1e9
+        return {"bound": "hbm", "kernel": kernel, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "algorithmic_bytes": algo[b],
+                "us_per_launch": per_b[str(b)]["us"], "traffic": traffic_of(b)}
+
+    roofline = roof(1, "k_matvec<Q4_K, 1 row> (C2, B=1)")
+    roofline["also"] = [roof(b, "k_quantize_split_q8k + k_mv_dma<Q4_K, 8 superblocks, 2 tiles> (C2, B=%d)" % b)
+                        for b in (8, 16)]
     del rot
     torch.cuda.empty_cache()
 
@@ -330,6 +353,10 @@ def run_details(L, cu, np, torch, dev, args):
     gate = L.QTensor.quantize(cu(L.synth_normal(40, E * ff * hid, 0.0, 0.02)).view(E, ff, hid), 12)
     up = L.QTensor.quantize(cu(L.synth_normal(41, E * ff * hid, 0.0, 0.02)).view(E, ff, hid), 12)
     down = L.QTensor.quantize(cu(L.synth_normal(42, E * hid * ff, 0.0, 0.02)).view(E, hid, ff), 12)
+    # two copies of the layer's experts (2 x 340 MB), alternated call by
+    # call: no expert a call reads is left in the 256 MB MALL by the call
+    # before it
+    layer_copies = [(gate, up, down), tuple(Rotation(q, 1).tensors[0] for q in (gate, up, down))]
     logits = L.synth_uniform(4, T * E).reshape(T, E)
     p = np.exp(logits - logits.max(1, keepdims=True))
     p /= p.sum(1, keepdims=True)
@@ -341,29 +368,34 @@ def run_details(L, cu, np, torch, dev, args):
     yu = torch.empty((T, topk, ff), device=dev)
     yd = torch.empty((T, topk, hid), device=dev)
 
-    def moe():
-        gate.indexed_moe_forward_into(x, ids_t, yg)
-        up.indexed_moe_forward_into(x, ids_t, yu)
-        down.indexed_moe_forward_into(h, ids_t, yd)
+    def moe_on(g_, u_, d_):
+        def moe():
+            g_.indexed_moe_forward_into(x, ids_t, yg)
+            u_.indexed_moe_forward_into(x, ids_t, yu)
+            d_.indexed_moe_forward_into(h, ids_t, yd)
+        return moe
 
-    # four passes over the layer a graph replay (the replay's own launch
-    # amortized)
-    t = time_graph([moe] * 4, 3, 1) / 4
+    # four passes over the layer a graph replay, on the two copies in turn
+    # (the replay's own launch amortized)
+    t = time_graph([moe_on(*layer_copies[i % 2]) for i in range(4)], 3, 1) / 4
     distinct = len(np.unique(ids))
     byts = distinct * (gate.packed_bytes() + up.packed_bytes() + down.packed_bytes()) // E
     byts += (T * hid + T * topk * ff) * 4 + (2 * T * topk * ff + T * topk * hid) * 4
     out["c5_moe_experts"] = {"us": round(t * 1e6, 2), "distinct_experts": distinct,
                              "unique_expert_bytes": int(byts), "GB/s": round(byts / t / 1e9, 1),
                              "hbm_frac": round(byts / t / 1e9 / 8000.0, 4),
-                             "note": "gate+up+down, 3 routed calls; four passes a graph replay; the 307 MB of touched experts exceed the 256 MB MALL"}
+                             "note": "gate+up+down, 3 routed calls; four passes a graph replay on two "
+                                     "alternating copies of the experts (2 x 340 MB)"}
 
     # the same layer with gate and up as one SwiGLU launch (silu(g) * u
     # stored once) and the down projection over it
-    def moe_glu():
-        gate.indexed_moe_forward_glu_into(up, x, ids_t, yg)
-        down.indexed_moe_forward_into(yg, ids_t, yd)
+    def glu_on(g_, u_, d_):
+        def moe_glu():
+            g_.indexed_moe_forward_glu_into(u_, x, ids_t, yg)
+            d_.indexed_moe_forward_into(yg, ids_t, yd)
+        return moe_glu
 
-    t = time_graph([moe_glu] * 4, 3, 1) / 4
+    t = time_graph([glu_on(*layer_copies[i % 2]) for i in range(4)], 3, 1) / 4
     byts_glu = byts - T * topk * ff * 4  # one [T, topk, ff] store fewer
     out["c5_moe_glu_layer"] = {"us": round(t * 1e6, 2), "GB/s": round(byts_glu / t / 1e9, 1),
                                "hbm_frac": round(byts_glu / t / 1e9 / 8000.0, 4),
