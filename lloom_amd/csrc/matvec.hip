@@ -816,15 +816,15 @@ __global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ ps
 
 // ---------------------- 3..16 rows, K <= 2048: the operands through LDS --
 // The same dots as k_mv_mfma (mf_compute on its operand layout) with a
-// load shape fit for a launch this short.  A workgroup of 4 * NT waves owns
+// load shape fit for a launch this short.  A workgroup of KQ * NT waves owns
 // NT 16-row tiles over all of K.  Its weights (NT x 16 consecutive rows, one
 // contiguous run each) and the quantized x (m rows of K bytes, contiguous)
 // go to LDS as global_load_lds DMAs of 1 KB a wave instruction, so every
 // load instruction covers eight whole cache lines; loading the MFMA operand
 // layout straight from global memory (16 rows x 48 bytes an instruction)
 // multiplies the memory requests and costs ~2 us of a ~6 us call.  After
-// one barrier, wave (tile, q) computes superblocks q, q + 4, ... of its tile
-// out of LDS, and the four K quarters of a tile add up through LDS.
+// one barrier, wave (tile, q) computes superblocks q, q + KQ, ... of its
+// tile out of LDS, and the KQ parts of K of a tile add up through LDS.
 // Rows past n load the last valid bytes again (their sums are never
 // stored); activation rows past m are zeroed by select.
 constexpr int MV_DMA_KMAX = 2048;
@@ -858,19 +858,19 @@ __device__ __forceinline__ void dma_rows(const uint8_t* __restrict__ src, int by
     }
 }
 
-template <int TYPE, int NSB, int NT>
-__global__ __launch_bounds__(256 * NT) void k_mv_dma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+template <int TYPE, int NSB, int NT, int KQ>
+__global__ __launch_bounds__(64 * KQ * NT) void k_mv_dma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                      const float* __restrict__ xd, const int8_t* __restrict__ bsp,
                                                      float* __restrict__ Y, int n, int m, int mp, int epi) {
     constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
-    constexpr int WV = 4 * NT, K = 256 * NSB, RB = NSB * BB;
+    constexpr int WV = KQ * NT, K = 256 * NSB, RB = NSB * BB;
     static_assert(RB % 16 == 0, "rows must be whole 16-byte DMA pieces");
     constexpr int WP = lds_pitch(RB), XP = lds_pitch(K);
-    constexpr int NJ = (NSB + 3) / 4;  // superblocks a wave computes
+    constexpr int NJ = (NSB + KQ - 1) / KQ;  // superblocks a wave computes
     // each DMA instruction writes 1 KB; the slack takes the last one's overhang
     __shared__ __align__(16) uint8_t wl[NT][16 * WP + 1024];
     __shared__ __align__(16) uint8_t xl[16 * XP + 1024];
-    __shared__ float4 part[3][NT][64];
+    __shared__ float4 part[KQ - 1][NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
 #pragma unroll
@@ -881,12 +881,12 @@ __global__ __launch_bounds__(256 * NT) void k_mv_dma(const uint8_t* __restrict__
         dma_rows<WP, WV>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave, lane);
     }
     dma_rows<XP, WV>((const uint8_t*)xq, K, m, K, m * K - 16, xl, wave, lane);
-    const int t = wave >> 2, q = wave & 3;
+    const int t = wave / KQ, q = wave % KQ;
     float4 dy[NJ];
     long ab[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int sb = min(q + 4 * j, NSB - 1);
+        const int sb = min(q + KQ * j, NSB - 1);
         dy[j] = *(const float4*)(xd + (int64_t)sb * mp + 4 * g);
         if constexpr (TYPE == T_Q4K) {
             // groups 0 and 1 read the lo and hi sums of row c16; 2 and 3 reread group 1's
@@ -904,7 +904,7 @@ __global__ __launch_bounds__(256 * NT) void k_mv_dma(const uint8_t* __restrict__
     float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int sb = q + 4 * j;
+        const int sb = q + KQ * j;
         if (sb < NSB) {  // wave-uniform
             MfW<TYPE> wu;
             mf_load<TYPE>(trow + sb * BB, g, wu);
@@ -923,7 +923,7 @@ __global__ __launch_bounds__(256 * NT) void k_mv_dma(const uint8_t* __restrict__
     __syncthreads();
     if (q) return;
 #pragma unroll
-    for (int w = 0; w < 3; w++) {
+    for (int w = 0; w < KQ - 1; w++) {
         const float4 p = part[w][t][lane];
         out[0] += p.x;
         out[1] += p.y;
@@ -949,6 +949,15 @@ static int mv_dma_env() {
     return v;
 }
 static bool mv_dma_on() { return mv_dma_env() != 0; }
+// LLOOM_HIP_MV_DMA_KQ: waves a tile splits K over (4 or 8); unset = 8 with
+// one tile a workgroup (n = 2048, m = 16: 6.13 against 6.32 us), else 4
+static int mv_dma_kq_env() {
+    static const int v = [] {
+        const char* e = getenv("LLOOM_HIP_MV_DMA_KQ");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
 static int mv_dma_nt(int64_t tiles) { return mv_dma_env() > 0 ? mv_dma_env() : tiles >= 384 ? 2 : 1; }
 
 template <int TYPE, int NSB>
@@ -956,11 +965,18 @@ static hipError_t launch_mv_dma_k(const void* w, float* y, int64_t n, int64_t m,
                                   const int8_t* bsp, int epi, hipStream_t s) {
     const int mp = (int)((m + 15) & ~(int64_t)15);
     const int64_t tiles = (n + 15) / 16;
-    if (mv_dma_nt(tiles) == 2)
-        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2>), dim3((unsigned)((tiles + 1) / 2)), dim3(512), 0, s,
+    const int kq = mv_dma_kq_env() ? mv_dma_kq_env() : mv_dma_nt(tiles) == 1 ? 8 : 4;
+    if (kq == 8 && mv_dma_nt(tiles) == 2)
+        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2, 8>), dim3((unsigned)((tiles + 1) / 2)), dim3(1024), 0, s,
+                           (const uint8_t*)w, xq, xd, bsp, y, (int)n, (int)m, mp, epi);
+    else if (kq == 8)
+        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1, 8>), dim3((unsigned)tiles), dim3(512), 0, s, (const uint8_t*)w, xq, xd,
+                           bsp, y, (int)n, (int)m, mp, epi);
+    else if (mv_dma_nt(tiles) == 2)
+        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2, 4>), dim3((unsigned)((tiles + 1) / 2)), dim3(512), 0, s,
                            (const uint8_t*)w, xq, xd, bsp, y, (int)n, (int)m, mp, epi);
     else
-        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1>), dim3((unsigned)tiles), dim3(256), 0, s, (const uint8_t*)w, xq, xd,
+        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1, 4>), dim3((unsigned)tiles), dim3(256), 0, s, (const uint8_t*)w, xq, xd,
                            bsp, y, (int)n, (int)m, mp, epi);
     return hipGetLastError();
 }
