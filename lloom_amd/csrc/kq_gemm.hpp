@@ -29,20 +29,19 @@ __device__ __forceinline__ void tile_of(int nbm, int nbn, int& bm, int& bn) {
 // global_load_lds written as the instruction: the compiler does not see
 // these LDS writes, so it adds no vmcnt(0) in front of later LDS reads it
 // cannot prove disjoint from them; the kernel orders them itself (counted
-// vmcnt waits, then s_barrier).  m0 holds the wave's LDS destination and is
-// set right before each load; nothing else in the kernel uses m0.
+// vmcnt waits, then s_barrier).  The LDS destination goes to m0 through an
+// operand constraint, so the compiler itself writes m0 (and knows it is
+// taken) before each load; the s_nop covers the m0-write-to-LDS-DMA hazard.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
 }
 // From a wave-uniform base (SGPRs) plus a 32-bit per-lane offset, to a
 // wave-uniform LDS destination: the per-step address arithmetic is scalar.
 __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4s(const void* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 }  // namespace lloom
