@@ -123,34 +123,94 @@ bool gemm_i8_fits(int64_t n, int64_t k, int64_t m) {
     return k % 256 == 0 && i8_rows(m) * k < ((int64_t)1 << 31) && n * (k / 256) * Q4K_BYTES < ((int64_t)1 << 31);
 }
 
-// NB consecutive superblocks of one row a wave: their loads go out together.
+// Q8_K of one 256-element block held by 16 lanes (a DPP row), lane j owning
+// elements 16j .. 16j+15 (piece j of the GEMM's operand layout): the same
+// operations as q8k_block_wave (max of |x|, first index on ties, iscale =
+// -127 / max, round-half-away, saturate, d = 1 / iscale, d = 0 for an
+// all-zero block), with the reductions over 16 lanes, so a wave quantizes
+// four blocks at once.  Returns the lane's 16 bytes; *bsum is the sum of its
+// 16 quants.
+__device__ __forceinline__ uint4 q8k_block_row16(const float (&xs)[16], float* d, int* bsum) {
+#pragma clang fp contract(off)
+    float la = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) la = __builtin_fmaxf(la, __builtin_fabsf(xs[i]));
+    la = __builtin_fmaxf(la, dpp<DPP_XOR1>(la));
+    la = __builtin_fmaxf(la, dpp<DPP_XOR2>(la));
+    la = __builtin_fmaxf(la, dpp<DPP_HALF_MIRROR>(la));
+    const float amax = __builtin_fmaxf(la, dpp<DPP_ROW_MIRROR>(la));
+    float mine = 0.0f;
+    bool hit = false;
+#pragma unroll
+    for (int i = 15; i >= 0; i--) {
+        const bool h = __builtin_fabsf(xs[i]) == amax;
+        mine = h ? xs[i] : mine;
+        hit = hit || h;
+    }
+    const int lane = __lane_id(), row = lane & 48;
+    const uint32_t hits = (uint32_t)(__ballot(hit) >> row) & 0xffffu;
+    const int first = hits ? __builtin_ctz(hits) : 0;
+    const float mx = __shfl(mine, row + first, 64);
+    const float iscale = -127.0f / mx;
+    uint32_t w[4];
+    int sum = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int q = clampi(nearest_int(iscale * xs[4 * c + b]), -128, 127);
+            sum += q;
+            packed |= ((uint32_t)q & 0xffu) << (8 * b);
+        }
+        w[c] = packed;
+    }
+    const float dd = 1.0f / iscale;
+    *d = amax == 0.0f ? 0.0f : dd;
+    *bsum = sum;
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Each wave quantizes NB superblocks of 4 rows (a 16-lane row of the wave
+// per activation row; lane j of it holds piece j: 16 elements, 64 contiguous
+// bytes of x, 16 bytes of x8 written where the GEMM's stage wants them).
 template <int NB>
 __global__ __launch_bounds__(256) void k_gemm_prep_i8(const float* __restrict__ x, int8_t* __restrict__ xq,
                                                       _Float16* __restrict__ s16, float* __restrict__ dyt, int m,
                                                       int mp, int k) {
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, j = lane & 15;
     const int nsb = k >> 8, ngr = nsb / NB;
-    const int64_t grp = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (grp >= (int64_t)mp * ngr) return;
-    const int mi = (int)(grp / ngr), sb0 = NB * (int)(grp - (int64_t)mi * ngr);
-    float4 v[NB];
-    if (mi < m) {  // wave-uniform
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (4-row group, superblock group)
+    if (wid >= (int64_t)(mp / 4) * ngr) return;
+    const int mi = (int)(wid / ngr) * 4 + (lane >> 4), sb0 = NB * (int)(wid % ngr);
+    const bool real = mi < m;
+    const float* xr = x + (int64_t)min(mi, m - 1) * k + 16 * j;
+    float xs[NB][16];
 #pragma unroll
-        for (int b = 0; b < NB; b++) v[b] = *(const float4*)(x + (int64_t)mi * k + (sb0 + b) * 256 + 4 * lane);
-    }
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 v = *(const float4*)(xr + (sb0 + b) * 256 + 4 * c);
+            xs[b][4 * c] = v.x;
+            xs[b][4 * c + 1] = v.y;
+            xs[b][4 * c + 2] = v.z;
+            xs[b][4 * c + 3] = v.w;
+        }
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        uint32_t q = 0;
-        float d = 0.0f;
-        int bs = 0;
-        if (mi < m) q = q8k_block_wave(v[b], &d, &bs);
         const int sb = sb0 + b;
-        // lane l holds elements 4l .. 4l+3: piece l / 4, bytes 4 (l % 4) ..
-        *(uint32_t*)(xq + ((((int64_t)(mi >> 6) * nsb + sb) * 16 + (lane >> 2)) * 64 + (mi & 63)) * 16 +
-                     4 * (lane & 3)) = q;
-        const int S = bs + __shfl_xor(bs, 4, 64);  // lanes 8j .. 8j+7: S_j
-        if ((lane & 7) == 0) s16[((int64_t)sb * mp + mi) * 8 + (lane >> 3)] = (_Float16)(float)S;
-        if (lane == 0) dyt[(int64_t)sb * mp + mi] = d;
+        float d;
+        int bs;
+        uint4 q = q8k_block_row16(xs[b], &d, &bs);
+        if (!real) {  // rows past m: zeros
+            q = make_uint4(0, 0, 0, 0);
+            d = 0.0f;
+            bs = 0;
+        }
+        *(uint4*)(xq + ((((int64_t)(mi >> 6) * nsb + sb) * 16 + j) * 64 + (mi & 63)) * 16) = q;
+        const int S = bs + __shfl_xor(bs, 1, 64);  // pieces 2i and 2i + 1: S_i
+        if ((j & 1) == 0) s16[((int64_t)sb * mp + mi) * 8 + (j >> 1)] = (_Float16)(float)S;
+        if (j == 0) dyt[(int64_t)sb * mp + mi] = d;
     }
 }
 
@@ -368,11 +428,12 @@ hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, in
     }
     const I8Ptrs p = i8_ptrs(ws, m, k);
     const int64_t nsb = k / 256;
-    if (nsb % 4 == 0)
-        hipLaunchKernelGGL(k_gemm_prep_i8<4>, dim3((unsigned)((p.mp * (nsb / 4) + 3) / 4)), dim3(256), 0, s, x, p.xq,
-                           p.s16, p.dyt, (int)m, (int)p.mp, (int)k);
+    const int64_t waves2 = p.mp / 4 * (nsb / 2), waves1 = p.mp / 4 * nsb;
+    if (nsb % 2 == 0)
+        hipLaunchKernelGGL(k_gemm_prep_i8<2>, dim3((unsigned)((waves2 + 3) / 4)), dim3(256), 0, s, x, p.xq, p.s16,
+                           p.dyt, (int)m, (int)p.mp, (int)k);
     else
-        hipLaunchKernelGGL(k_gemm_prep_i8<1>, dim3((unsigned)((p.mp * nsb + 3) / 4)), dim3(256), 0, s, x, p.xq, p.s16,
+        hipLaunchKernelGGL(k_gemm_prep_i8<1>, dim3((unsigned)((waves1 + 3) / 4)), dim3(256), 0, s, x, p.xq, p.s16,
                            p.dyt, (int)m, (int)p.mp, (int)k);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
