@@ -453,29 +453,51 @@ static size_t x16_bytes(int64_t m, int64_t k) {
 __global__ __launch_bounds__(256) void k_gemm_prep_x16(const float* __restrict__ x, _Float16* __restrict__ x16,
                                                        _Float16* __restrict__ amin, float* __restrict__ dyt, int m,
                                                        int k) {
-    const int lane = threadIdx.x & 63;
+    // four blocks a wave, one a 16-lane row; lane j of a row holds elements
+    // 16j .. 16j+15 of its block (q8k_block_row16)
+    const int lane = threadIdx.x & 63, j = lane & 15;
     const int nsb = k >> 8;
-    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (blk >= (int64_t)m * nsb) return;
+    const int64_t nblk = (int64_t)m * nsb;
+    const int64_t blk0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const bool real = blk0 < nblk;  // per 16-lane row
+    const int64_t blk = real ? blk0 : 0;
     const int mi = (int)(blk / nsb), sb = (int)(blk - (int64_t)mi * nsb);
-    const float4 v = *(const float4*)(x + (int64_t)mi * k + sb * 256 + 4 * lane);
+    const float* xr = x + (int64_t)mi * k + sb * 256 + 16 * j;
+    float xs[16];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const float4 v = *(const float4*)(xr + 4 * c);
+        xs[4 * c] = v.x;
+        xs[4 * c + 1] = v.y;
+        xs[4 * c + 2] = v.z;
+        xs[4 * c + 3] = v.w;
+    }
     float d;
     int bs;
-    const uint32_t q = q8k_block_wave(v, &d, &bs);
+    const uint4 q = q8k_block_row16(xs, &d, &bs);
+    const int S = bs + __shfl_xor(bs, 1, 64);  // pieces 2i and 2i + 1: S_i
+    if (!real) return;
     // elements 4l .. 4l+3 go to slots 4l, 4l+2, 4l+1, 4l+3 (bits 0, 1 swapped)
-    const _Float16 h0 = (_Float16)(float)(int8_t)(q & 0xff), h1 = (_Float16)(float)(int8_t)((q >> 8) & 0xff);
-    const _Float16 h2v = (_Float16)(float)(int8_t)((q >> 16) & 0xff), h3 = (_Float16)(float)(int8_t)(q >> 24);
-    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-    const v4h o = {h0, h2v, h1, h3};
-    *(v4h*)(x16 + (int64_t)mi * k + sb * 256 + 4 * lane) = o;
-    const int S = bs + __shfl_xor(bs, 4, 64);  // S_j on lanes 8j .. 8j+7
-    if ((lane & 7) == 0) {
-        const int j = lane >> 3;
-        _Float16* a = amin + ((int64_t)mi * nsb + sb) * 16;
-        a[j] = (_Float16)(float)(S >> 6);      // S_hi in [-64, 63]
-        a[8 + j] = (_Float16)(float)(S & 63);  // S_lo in [0, 63]
+    typedef _Float16 v8hh __attribute__((ext_vector_type(8)));
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    v8hh o[2];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t v = w[c];
+        o[c >> 1][4 * (c & 1)] = (_Float16)(float)(int8_t)(v & 0xff);
+        o[c >> 1][4 * (c & 1) + 1] = (_Float16)(float)(int8_t)((v >> 16) & 0xff);
+        o[c >> 1][4 * (c & 1) + 2] = (_Float16)(float)(int8_t)((v >> 8) & 0xff);
+        o[c >> 1][4 * (c & 1) + 3] = (_Float16)(float)(int8_t)(v >> 24);
     }
-    if (lane == 0) dyt[(int64_t)sb * m + mi] = d;
+    _Float16* xo = x16 + (int64_t)mi * k + sb * 256 + 16 * j;
+    *(v8hh*)xo = o[0];
+    *(v8hh*)(xo + 8) = o[1];
+    if ((j & 1) == 0) {
+        _Float16* a = amin + ((int64_t)mi * nsb + sb) * 16;
+        a[j >> 1] = (_Float16)(float)(S >> 6);      // S_hi in [-64, 63]
+        a[8 + (j >> 1)] = (_Float16)(float)(S & 63);  // S_lo in [0, 63]
+    }
+    if (j == 0) dyt[(int64_t)sb * m + mi] = d;
 }
 
 // Four nibbles (one per byte of w, each 0..15) times sc, as fp16 in slot
@@ -1026,7 +1048,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
-        hipLaunchKernelGGL(k_gemm_prep_x16, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.x16, p.amin,
+        hipLaunchKernelGGL(k_gemm_prep_x16, dim3((unsigned)((nb + 15) / 16)), dim3(256), 0, s, x, p.x16, p.amin,
                            p.dyt, (int)m, (int)k);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1059,7 +1081,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
     if (type == T_Q4K && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
-        hipLaunchKernelGGL(k_gemm_prep_x16, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.x16, p.amin,
+        hipLaunchKernelGGL(k_gemm_prep_x16, dim3((unsigned)((nb + 15) / 16)), dim3(256), 0, s, x, p.x16, p.amin,
                            p.dyt, (int)m, (int)k);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -60,6 +60,54 @@ __device__ __forceinline__ uint32_t q8k_block_wave(float4 x, float* d, int* bsum
     return packed;
 }
 
+// Q8_K of one 256-element block held by 16 lanes (a DPP row), lane j owning
+// elements 16j .. 16j+15 (piece j of the GEMM's operand layout): the same
+// operations as q8k_block_wave (max of |x|, first index on ties, iscale =
+// -127 / max, round-half-away, saturate, d = 1 / iscale, d = 0 for an
+// all-zero block), with the reductions over 16 lanes, so a wave quantizes
+// four blocks at once.  Returns the lane's 16 bytes; *bsum is the sum of its
+// 16 quants.
+__device__ __forceinline__ uint4 q8k_block_row16(const float (&xs)[16], float* d, int* bsum) {
+#pragma clang fp contract(off)
+    float la = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) la = __builtin_fmaxf(la, __builtin_fabsf(xs[i]));
+    la = __builtin_fmaxf(la, dpp<DPP_XOR1>(la));
+    la = __builtin_fmaxf(la, dpp<DPP_XOR2>(la));
+    la = __builtin_fmaxf(la, dpp<DPP_HALF_MIRROR>(la));
+    const float amax = __builtin_fmaxf(la, dpp<DPP_ROW_MIRROR>(la));
+    float mine = 0.0f;
+    bool hit = false;
+#pragma unroll
+    for (int i = 15; i >= 0; i--) {
+        const bool h = __builtin_fabsf(xs[i]) == amax;
+        mine = h ? xs[i] : mine;
+        hit = hit || h;
+    }
+    const int lane = __lane_id(), row = lane & 48;
+    const uint32_t hits = (uint32_t)(__ballot(hit) >> row) & 0xffffu;
+    const int first = hits ? __builtin_ctz(hits) : 0;
+    const float mx = __shfl(mine, row + first, 64);
+    const float iscale = -127.0f / mx;
+    uint32_t w[4];
+    int sum = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int q = clampi(nearest_int(iscale * xs[4 * c + b]), -128, 127);
+            sum += q;
+            packed |= ((uint32_t)q & 0xffu) << (8 * b);
+        }
+        w[c] = packed;
+    }
+    const float dd = 1.0f / iscale;
+    *d = amax == 0.0f ? 0.0f : dd;
+    *bsum = sum;
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // Q8_0 of one 32-element block held by 8 consecutive lanes (aligned to 8),
 // sub-lane j owning elements 4j..4j+3.  d = amax / 127 (kept f32 for the
 // rounding), id = 1/d or 0, q = round(x * id) as i8; *d16 is f16(d).
