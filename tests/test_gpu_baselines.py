@@ -90,6 +90,28 @@ def test_c4_q4k_projections(L, b):
 
 # ------------------------------------------------------------------ C5 ---
 
+@pytest.mark.parametrize("dt", [O.Q4K, O.Q6K])
+@pytest.mark.parametrize("k", [1024, 2048, 4096, 8192, 16384])
+def test_decode_rows_long_k(L, dt, k):
+    """3..16 activation rows at short and long K (k_mv_fused, k_mv_dma up to
+    2048, k_mv_mfma with K split over waves and workgroups past it: the C4
+    Q6_K down projection is k = 8192); ragged n; the SiLU store too."""
+    rng = np.random.default_rng(k + dt)
+    n = 40
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    q = L.QTensor.quantize(_cuda(w), dt)
+    qb = q.data()
+    mm = L.QMatMul.from_qtensor(q)
+    for m in (3, 5, 16):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        want = O.matmul(dt, x, qb, n)
+        got = mm.forward(_cuda(x)).cpu().numpy()
+        assert_rows_close(got, want, what=f"dt={dt} k={k} m={m}")
+        silu = mm.forward_silu(_cuda(x)).cpu().numpy()
+        ref = (want / (1.0 + np.exp(-want.astype(np.float64)))).astype(np.float32)
+        assert_rows_close(silu, ref, tol=1.1 * MATMUL_TOL, what=f"silu dt={dt} k={k} m={m}")
+
+
 def _c5_routing(L, T=32, E=128, topk=8, seed=4):
     """top-8 of softmax(U(0,1) logits), descending, ties to the lower index."""
     logits = L.synth_uniform(seed, T * E).reshape(T, E).astype(np.float64)
