@@ -1,5 +1,10 @@
-// gemm.hip -- prefill-shaped quantized matmul (m > 16 activation rows) on
-// int8 MFMA (v_mfma_i32_32x32x32_i8).
+// gemm.hip -- prefill-shaped Q4_K matmul (m > 16 activation rows): the fp16
+// routes (k_gemm_q4k_skinny for up to 128 rows, k_gemm_q4k_x16 past that, the
+// default) further down, the routing (launch_gemm), and first the int8-plane
+// kernel k_gemm_q4k that LLOOM_HIP_MMA_INT8 falls back to when
+// k_gemm_q4k_i8 (gemm_i8.hip) cannot address the shape with 32-bit offsets.
+//
+// k_gemm_q4k, on int8 MFMA (v_mfma_i32_32x32x32_i8):
 //
 // y[m, n] = sum_sb dy[m,sb] * ( d[n,sb] * sum_j sc[n,j] * sum_{k in j} x8[m,k] q[n,k]
 //                              - dmin[n,sb] * sum_j mn[n,j] * sum_{k in j} x8[m,k] )
