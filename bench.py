@@ -56,6 +56,9 @@ def parse():
     ap.add_argument("--pmc-probe-type", default="q4k", choices=["q4k", "q8_0", "q6k"],
                     help="weight type of --pmc-probe-prefill (q4k: C3's [8192, 2048]; q8_0 [8192, 2048]; "
                          "q6k [2048, 8192])")
+    ap.add_argument("--pmc-probe-moe", action="store_true",
+                    help="launch only the C5 gate call (routed Q4_K experts, 32 tokens top-8), six times on two "
+                         "alternating copies of the experts, for rocprofv3 --pmc runs on the routed kernel")
     ap.add_argument("--pmc-probe-prefill", action="store_true",
                     help="launch only the C3 prefill GEMM at m=2048 (5 calls), for rocprofv3 --pmc runs on the "
                          "MFMA kernel")
@@ -81,6 +84,14 @@ class Rotation:
 
     def __len__(self):
         return len(self.tensors)
+
+
+def moe_ids(L, np, T, E, topk):
+    """C5's routing: top-k of a softmax over seeded uniform logits (synth_uniform(4))."""
+    logits = L.synth_uniform(4, T * E).reshape(T, E)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    return np.argsort(-p, axis=1, kind="stable")[:, :topk].astype(np.int32)
 
 
 def copies_for(packed_bytes):
@@ -133,6 +144,22 @@ def main():
 
     def cu(a):
         return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+    if args.pmc_probe_moe:
+        E, ff, hid, T, topk = 128, 768, 2048, 32, 8
+        gate = L.QTensor.quantize(cu(L.synth_normal(40, E * ff * hid, 0.0, 0.02)).view(E, ff, hid), 12)
+        copies = [gate, Rotation(gate, 1).tensors[0]]
+        ids = moe_ids(L, np, T, E, topk)
+        x = cu(L.synth_normal(4000, T * hid)).view(T, 1, hid)
+        yg = torch.empty((T, topk, ff), device=dev)
+        ids_t = cu(ids)
+        for i in range(6):
+            copies[i % 2].indexed_moe_forward_into(x, ids_t, yg)
+        torch.cuda.synchronize()
+        distinct = len(np.unique(ids))
+        print(json.dumps({"pmc_probe": "moe_c5_gate", "distinct_experts": distinct,
+                          "expert_bytes_per_call": distinct * gate.packed_bytes() // E}))
+        return
 
     # ---------------------------------------------------- headline: C2 ---
     n, k = 6144, 2048
@@ -357,10 +384,7 @@ def run_details(L, cu, np, torch, dev, args):
     # call: no expert a call reads is left in the 256 MB MALL by the call
     # before it
     layer_copies = [(gate, up, down), tuple(Rotation(q, 1).tensors[0] for q in (gate, up, down))]
-    logits = L.synth_uniform(4, T * E).reshape(T, E)
-    p = np.exp(logits - logits.max(1, keepdims=True))
-    p /= p.sum(1, keepdims=True)
-    ids = np.argsort(-p, axis=1, kind="stable")[:, :topk].astype(np.int32)
+    ids = moe_ids(L, np, T, E, topk)
     ids_t = cu(ids)
     x = cu(L.synth_normal(4000, T * hid)).view(T, 1, hid)
     h = cu(L.synth_normal(4001, T * topk * ff)).view(T, topk, ff)
