@@ -994,8 +994,21 @@ static int64_t q6_min_rows() {
     return v;
 }
 
+// Q4_K with 17..64 rows and k <= 2048 takes the multi-tile DMA decode
+// kernel (either prefill mode: its dots are int8 MFMAs on the Q8_K
+// activations, as the decode path's); LLOOM_HIP_MV_DMA_MA=0 (read once)
+// turns it off.
+static bool use_dma_ma(int type, int64_t k, int64_t m) {
+    static const bool on = [] {
+        const char* e = getenv("LLOOM_HIP_MV_DMA_MA");
+        return !(e && atoi(e) == 0);
+    }();
+    return on && mv_dma_ma_fits(type, k, m);
+}
+
 static int64_t skinny_max_rows();
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode) {
+    if (use_dma_ma(type, k, m)) return split_q8k_bytes(k, m);
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(0, k, m) && mode != GEMM_INT8) return x16_bytes(m, k);
     if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m)) return q6_gemm_workspace_bytes(n, k, m);
     if (use_mq(type, m)) return split_q8k_bytes(k, m);
@@ -1050,6 +1063,7 @@ static int64_t skinny_max_rows() {
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s) {
     if (gemm_workspace_bytes(type, n, k, m, mode) > ws_cap) return hipErrorInvalidValue;
+    if (use_dma_ma(type, k, m)) return launch_mv_dma_ma(w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);

@@ -26,7 +26,7 @@ hipError_t launch_embedding(int type, const void* w, int64_t rows, int64_t hidde
 size_t split_q8k_bytes(int64_t k, int64_t m);
 void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d, int8_t** bsp = nullptr);
 hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s,
-                                     int8_t* bsp = nullptr);
+                                     int8_t* bsp = nullptr, bool tiled = false);
 
 // matvec.hip: m <= 16.  Rows up to MV_DOT_MAX_ROWS (Q4_K on a weight of at
 // most 2048^2 elements: up to 4) take the fused dot4 kernel; more rows take
@@ -35,6 +35,14 @@ constexpr int MV_DOT_MAX_ROWS = 2;
 size_t matvec_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, int epi, hipStream_t s);
+// matvec.hip: Q4_K with up to MV_DMA_MA_MAX_ROWS rows and k <= 2048 on the
+// DMA kernel with one to four 16-row activation tiles (the decode path from
+// 5 rows, the GEMM path from 17; the workspace is split_q8k_bytes: the split
+// quantizer in its tiled layout, then one launch).
+constexpr int MV_DMA_MA_MAX_ROWS = 64;
+bool mv_dma_ma_fits(int type, int64_t k, int64_t m);
+hipError_t launch_mv_dma_ma(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
+                            int epi, hipStream_t s);
 // matvec.hip: Q4_K / Q6_K with any number of rows on the MFMA decode kernel,
 // 64 activation rows per workgroup layer (the weights are re-read per
 // layer): the workspace quantizer, then one launch.

@@ -900,11 +900,15 @@ __device__ __forceinline__ void dma_rows(const uint8_t* __restrict__ src, int by
     }
 }
 
+// Q6_K, up to 16 activation rows: NT 16-row weight tiles a workgroup, KQ
+// waves a tile splitting K; weights and quantized activations both moved
+// into LDS by 1 KB DMAs (x in the split layout, row-major).
 template <int TYPE, int NSB, int NT, int KQ>
 __global__ __launch_bounds__(64 * KQ * NT) void k_mv_dma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
-                                                     const float* __restrict__ xd, const int8_t* __restrict__ bsp,
-                                                     float* __restrict__ Y, int n, int m, int mp, int epi) {
-    constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES;
+                                                     const float* __restrict__ xd, float* __restrict__ Y, int n, int m,
+                                                     int mp, int epi) {
+    static_assert(TYPE == T_Q6K, "Q4_K takes k_mv_dma_ma");
+    constexpr int BB = Q6K_BYTES;
     constexpr int WV = KQ * NT, K = 256 * NSB, RB = NSB * BB;
     static_assert(RB % 16 == 0, "rows must be whole 16-byte DMA pieces");
     constexpr int WP = lds_pitch(RB), XP = lds_pitch(K);
@@ -925,19 +929,8 @@ __global__ __launch_bounds__(64 * KQ * NT) void k_mv_dma(const uint8_t* __restri
     dma_rows<XP, WV>((const uint8_t*)xq, K, m, K, m * K - 16, xl, wave, lane);
     const int t = wave / KQ, q = wave % KQ;
     float4 dy[NJ];
-    long ab[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int sb = min(q + KQ * j, NSB - 1);
-        dy[j] = *(const float4*)(xd + (int64_t)sb * mp + 4 * g);
-        if constexpr (TYPE == T_Q4K) {
-            // groups 0 and 1 read the lo and hi sums of row c16; 2 and 3 reread group 1's
-            // (loaded by every lane and masked: a load under the condition
-            // would wait for the DMAs in flight)
-            const long v = *(const long*)(bsp + ((int64_t)sb * mp + c16) * 16 + 8 * min(g, 1));
-            ab[j] = v & -(long)(g < 2 && c16 < m);
-        }
-    }
+    for (int j = 0; j < NJ; j++) dy[j] = *(const float4*)(xd + (int64_t)min(q + KQ * j, NSB - 1) * mp + 4 * g);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const bool arow_ok = c16 < m;
@@ -957,8 +950,7 @@ __global__ __launch_bounds__(64 * KQ * NT) void k_mv_dma(const uint8_t* __restri
                 a[2 * i] = arow_ok ? (long)(((uint64_t)v.y << 32) | v.x) : 0l;
                 a[2 * i + 1] = arow_ok ? (long)(((uint64_t)v.w << 32) | v.z) : 0l;
             }
-            if constexpr (TYPE == T_Q4K) mf_compute_q4k_b(wu, a, ab[j], dy[j], g, out);
-            else mf_compute<TYPE>(wu, a, dy[j], g, out);
+            mf_compute<TYPE>(wu, a, dy[j], g, out);
         }
     }
     if (q) part[q - 1][t][lane] = make_float4(out[0], out[1], out[2], out[3]);
@@ -1004,42 +996,167 @@ static int mv_dma_nt(int64_t tiles) { return mv_dma_env() > 0 ? mv_dma_env() : t
 
 template <int TYPE, int NSB>
 static hipError_t launch_mv_dma_k(const void* w, float* y, int64_t n, int64_t m, const int8_t* xq, const float* xd,
-                                  const int8_t* bsp, int epi, hipStream_t s) {
+                                  int epi, hipStream_t s) {
     const int mp = (int)((m + 15) & ~(int64_t)15);
     const int64_t tiles = (n + 15) / 16;
     const int kq = mv_dma_kq_env() ? mv_dma_kq_env() : mv_dma_nt(tiles) == 1 ? 8 : 4;
     if (kq == 8 && mv_dma_nt(tiles) == 2)
         hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2, 8>), dim3((unsigned)((tiles + 1) / 2)), dim3(1024), 0, s,
-                           (const uint8_t*)w, xq, xd, bsp, y, (int)n, (int)m, mp, epi);
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)m, mp, epi);
     else if (kq == 8)
         hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1, 8>), dim3((unsigned)tiles), dim3(512), 0, s, (const uint8_t*)w, xq, xd,
-                           bsp, y, (int)n, (int)m, mp, epi);
+                           y, (int)n, (int)m, mp, epi);
     else if (mv_dma_nt(tiles) == 2)
         hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2, 4>), dim3((unsigned)((tiles + 1) / 2)), dim3(512), 0, s,
-                           (const uint8_t*)w, xq, xd, bsp, y, (int)n, (int)m, mp, epi);
+                           (const uint8_t*)w, xq, xd, y, (int)n, (int)m, mp, epi);
     else
         hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1, 4>), dim3((unsigned)tiles), dim3(256), 0, s, (const uint8_t*)w, xq, xd,
-                           bsp, y, (int)n, (int)m, mp, epi);
+                           y, (int)n, (int)m, mp, epi);
     return hipGetLastError();
 }
 
-template <int TYPE>
-static hipError_t launch_mv_dma(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xq,
-                                const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
-    if constexpr (TYPE == T_Q6K) {
-        return launch_mv_dma_k<TYPE, 8>(w, y, n, m, xq, xd, bsp, epi, s);
-    } else {
-        switch (k / 256) {
-            case 1: return launch_mv_dma_k<TYPE, 1>(w, y, n, m, xq, xd, bsp, epi, s);
-            case 2: return launch_mv_dma_k<TYPE, 2>(w, y, n, m, xq, xd, bsp, epi, s);
-            case 3: return launch_mv_dma_k<TYPE, 3>(w, y, n, m, xq, xd, bsp, epi, s);
-            case 4: return launch_mv_dma_k<TYPE, 4>(w, y, n, m, xq, xd, bsp, epi, s);
-            case 5: return launch_mv_dma_k<TYPE, 5>(w, y, n, m, xq, xd, bsp, epi, s);
-            case 6: return launch_mv_dma_k<TYPE, 6>(w, y, n, m, xq, xd, bsp, epi, s);
-            case 7: return launch_mv_dma_k<TYPE, 7>(w, y, n, m, xq, xd, bsp, epi, s);
-            default: return launch_mv_dma_k<TYPE, 8>(w, y, n, m, xq, xd, bsp, epi, s);
+// Q6_K, k = 2048, up to 16 rows
+static hipError_t launch_mv_dma(const void* w, float* y, int64_t n, int64_t m, const int8_t* xq, const float* xd,
+                                int epi, hipStream_t s) {
+    return launch_mv_dma_k<T_Q6K, 8>(w, y, n, m, xq, xd, epi, s);
+}
+
+// Q4_K with 5 .. 64 activation rows and k <= 2048 (decode from B = 5 and
+// short prefill): MA 16-row activation tiles (16 MA >= m) against NT 16-row
+// weight tiles, one superblock a wave
+// (NSB waves), so every unpacked weight superblock serves the MA activation
+// tiles and every activation operand the NT weight tiles.  The weights move
+// as in k_mv_dma (1 KB DMAs of whole rows into LDS); the activations, MA
+// times the bytes of a decode call, skip LDS: each wave loads its
+// superblock's operands from the tiled layout of k_quantize_split_q8k
+// straight into registers, 1 KB of contiguous bytes an instruction, issued
+// with the DMAs.  The NSB partial sums of each (weight tile, activation
+// tile) meet in LDS and are added in superblock order, one pair a wave.
+// Rows past m in the last tile read the tile's padding and are never stored
+// (an activation row of the MFMA reaches only its own outputs).
+template <int NSB, int NT, int MA>
+__global__ __launch_bounds__(64 * NSB) void k_mv_dma_ma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xt,
+                                                      const float* __restrict__ xd, const int8_t* __restrict__ bsp,
+                                                      float* __restrict__ Y, int n, int m, int mp, int epi) {
+    constexpr int BB = Q4K_BYTES, RB = NSB * BB;
+    static_assert(RB % 16 == 0, "rows must be whole 16-byte DMA pieces");
+    constexpr int WP = lds_pitch(RB);
+    __shared__ __align__(16) uint8_t wl[NT][16 * WP + 1024];
+    __shared__ float4 part[NSB][NT * MA][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int r0 = (blockIdx.x * NT + t) * 16;
+        const int valid = max(1, min(16, n - r0));
+        dma_rows<WP, NSB>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave,
+                          lane);
+    }
+    const int sb = wave;
+    const int tiles = mp >> 4;  // activation tiles present (the rest load the last)
+    uint4 xv[MA][4];
+    float4 dy[MA];
+    long ab[MA];
+#pragma unroll
+    for (int a = 0; a < MA; a++) {
+        const int at = min(a, tiles - 1);
+        const int8_t* src = xt + ((int64_t)(at * NSB + sb) * 4) * 1024 + 16 * lane;
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[a][i] = *(const uint4*)(src + 1024 * i);
+        dy[a] = *(const float4*)(xd + (int64_t)sb * mp + 16 * at + 4 * g);
+        // groups 0 and 1 read the lo and hi sums of row c16 (masked past m;
+        // loaded by every lane: a load under the condition would wait for
+        // the DMAs in flight)
+        const long v = *(const long*)(bsp + ((int64_t)sb * mp + 16 * at + c16) * 16 + 8 * min(g, 1));
+        ab[a] = v & -(long)(g < 2 && 16 * a + c16 < m);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        MfW<T_Q4K> wu;
+        mf_load<T_Q4K>(&wl[t][c16 * WP] + sb * BB, g, wu);
+#pragma unroll
+        for (int a = 0; a < MA; a++) {
+            long av[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 v = xv[a][i];
+                av[2 * i] = (long)(((uint64_t)v.y << 32) | v.x);
+                av[2 * i + 1] = (long)(((uint64_t)v.w << 32) | v.z);
+            }
+            float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            mf_compute_q4k_b(wu, av, ab[a], dy[a], g, out);
+            part[sb][t * MA + a][lane] = make_float4(out[0], out[1], out[2], out[3]);
         }
     }
+    __syncthreads();
+    for (int pr = wave; pr < NT * MA; pr += NSB) {  // uniform
+        const int t = pr / MA, a = pr - t * MA;
+        float4 acc = part[0][pr][lane];
+#pragma unroll
+        for (int w = 1; w < NSB; w++) {
+            const float4 p = part[w][pr][lane];
+            acc.x += p.x;
+            acc.y += p.y;
+            acc.z += p.z;
+            acc.w += p.w;
+        }
+        const int row = (blockIdx.x * NT + t) * 16 + c16;
+        const float o[4] = {acc.x, acc.y, acc.z, acc.w};
+        if (row < n) {
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                if (16 * a + 4 * g + v < m) store_epi(&Y[(int64_t)(16 * a + 4 * g + v) * n + row], o[v], epi);
+        }
+    }
+}
+
+template <int NSB, int MA>
+static hipError_t launch_mv_dma_ma_k(const void* w, float* y, int64_t n, int64_t m, const int8_t* xt,
+                                     const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
+    const int mp = (int)((m + 15) & ~(int64_t)15);
+    const int64_t tiles = (n + 15) / 16;
+    if (mv_dma_nt(tiles) == 2)
+        hipLaunchKernelGGL((k_mv_dma_ma<NSB, 2, MA>), dim3((unsigned)((tiles + 1) / 2)), dim3(64 * NSB), 0, s,
+                           (const uint8_t*)w, xt, xd, bsp, y, (int)n, (int)m, mp, epi);
+    else
+        hipLaunchKernelGGL((k_mv_dma_ma<NSB, 1, MA>), dim3((unsigned)tiles), dim3(64 * NSB), 0, s, (const uint8_t*)w,
+                           xt, xd, bsp, y, (int)n, (int)m, mp, epi);
+    return hipGetLastError();
+}
+
+template <int MA>
+static hipError_t launch_mv_dma_ma_m(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xt,
+                                     const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
+    switch (k / 256) {
+        case 1: return launch_mv_dma_ma_k<1, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 2: return launch_mv_dma_ma_k<2, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 3: return launch_mv_dma_ma_k<3, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 4: return launch_mv_dma_ma_k<4, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 5: return launch_mv_dma_ma_k<5, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 6: return launch_mv_dma_ma_k<6, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 7: return launch_mv_dma_ma_k<7, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        default: return launch_mv_dma_ma_k<8, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+    }
+}
+
+bool mv_dma_ma_fits(int type, int64_t k, int64_t m) {
+    return type == T_Q4K && m <= MV_DMA_MA_MAX_ROWS && k <= MV_DMA_KMAX && k % 256 == 0 && mv_dma_on();
+}
+
+hipError_t launch_mv_dma_ma(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
+                            int epi, hipStream_t s) {
+    int8_t* xt;
+    float* xd;
+    int8_t* bsp;
+    split_q8k_ptrs(ws, k, m, &xt, &xd, &bsp);
+    hipError_t e = launch_quantize_split_q8k(x, m, k, xt, xd, s, bsp, true);
+    if (e != hipSuccess) return e;
+    if (m <= 16) return launch_mv_dma_ma_m<1>(w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 32) return launch_mv_dma_ma_m<2>(w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 48) return launch_mv_dma_ma_m<3>(w, y, n, k, m, xt, xd, bsp, epi, s);
+    return launch_mv_dma_ma_m<4>(w, y, n, k, m, xt, xd, bsp, epi, s);
 }
 
 template <int TYPE, int MA>
@@ -1104,18 +1221,20 @@ hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int6
     if (type != T_Q8_0 && !mv_dot(type, n, k, m) && m <= FUSED_MAX_ROWS && (k == 2048 || k == 1024))
         return type == T_Q4K ? launch_fused<T_Q4K>(w, x, y, n, k, m, epi, s)
                              : launch_fused<T_Q6K>(w, x, y, n, k, m, epi, s);
+    // Q4_K from 5 rows (k <= 2048): the split quantizer in its tiled layout,
+    // then k_mv_dma_ma with one activation tile (C2, B = 8 / 16: 7.28 /
+    // 7.37 us against 7.41 / 7.62 for k_mv_dma with x staged in LDS)
+    if (type == T_Q4K && !mv_dot(type, n, k, m) && mv_dma_ma_fits(type, k, m))
+        return launch_mv_dma_ma(w, x, y, n, k, m, ws, epi, s);
     if (type != T_Q8_0 && !mv_dot(type, n, k, m)) {
         int8_t* xq;
         float* xd;
-        int8_t* bsp;
-        split_q8k_ptrs(ws, k, m, &xq, &xd, &bsp);
+        split_q8k_ptrs(ws, k, m, &xq, &xd);
         // Q6_K rows are 16-byte multiples (whole DMA pieces) at k = 2048 only
-        const bool dma = k <= MV_DMA_KMAX && m <= 16 && mv_dma_on() && (type == T_Q4K || k == MV_DMA_KMAX);
-        hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s, dma && type == T_Q4K ? bsp : nullptr);
+        const bool dma = type == T_Q6K && k == MV_DMA_KMAX && m <= 16 && mv_dma_on();
+        hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
         if (e != hipSuccess) return e;
-        if (dma)
-            return type == T_Q4K ? launch_mv_dma<T_Q4K>(w, y, n, k, m, xq, xd, bsp, epi, s)
-                                 : launch_mv_dma<T_Q6K>(w, y, n, k, m, xq, xd, bsp, epi, s);
+        if (dma) return launch_mv_dma(w, y, n, m, xq, xd, epi, s);
         float* ps = mv_psum(ws, k, m);
         return type == T_Q4K ? launch_mv_mfma<T_Q4K, 1>(w, y, n, k, m, xq, xd, epi, s, ps)
                              : launch_mv_mfma<T_Q6K, 1>(w, y, n, k, m, xq, xd, epi, s, ps);

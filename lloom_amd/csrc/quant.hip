@@ -41,9 +41,14 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
 // values are those of k_quantize_q8k.  With bsp, also the 32-element sums
 // of every sub-block j as an MFMA operand: bsp [k/256][mp][16] bytes, byte j
 // = sum & 63 and byte 8 + j = sum >> 6 (sum = 64 hi + lo, both int8).
+// With `tiled`, qs is instead [mp/16][k/256][4][64][16] bytes: 16-row
+// groups, and in each superblock the 64-byte run of lane group g of row r
+// (the permuted offsets 64g .. 64g+63) split into four 16-byte pieces i,
+// piece i at [i][16g + r % 16]: the MFMA lane 16g + r % 16 then loads its
+// operand piece i of a row group's superblock from 1 KB of contiguous bytes.
 __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restrict__ x, int8_t* __restrict__ qs,
                                                             float* __restrict__ dt, int8_t* __restrict__ bsp, int m,
-                                                            int k, int mp) {
+                                                            int k, int mp, int tiled) {
     const int lane = threadIdx.x & 63;
     const int nsb = k >> 8;
     const int sb = blockIdx.y * 4 + (threadIdx.x >> 6), mi = blockIdx.x;
@@ -54,7 +59,12 @@ __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restr
     const uint32_t q = q8k_block_wave(v, &d, &bs);
     // lane owns elements 4*lane..: sub-block lane/8, group (lane%8)/2, byte 4*(lane%2)
     const int off = 64 * ((lane & 7) >> 1) + 8 * (lane >> 3) + 4 * (lane & 1);
-    *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + off) = q;
+    if (tiled) {  // uniform
+        const int64_t piece = (((int64_t)(mi >> 4) * nsb + sb) * 4 + ((off >> 4) & 3)) * 64 + 16 * (off >> 6) + (mi & 15);
+        *(uint32_t*)(qs + piece * 16 + (off & 15)) = q;
+    } else {
+        *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + off) = q;
+    }
     if (lane == 0) dt[(int64_t)sb * mp + mi] = d;
     if (bsp) {
         // bs is the 16-element sum of the lane's quad; the 8 lanes of
@@ -71,22 +81,22 @@ __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restr
 static int64_t pad16(int64_t m) { return (m + 15) & ~(int64_t)15; }
 
 size_t split_q8k_bytes(int64_t k, int64_t m) {
-    size_t qb = ((size_t)m * k + 255) & ~(size_t)255;
+    size_t qb = ((size_t)pad16(m) * k + 255) & ~(size_t)255;  // the tiled layout's padded rows
     return qb + (size_t)(k / 256) * pad16(m) * (sizeof(float) + 16);
 }
 
 void split_q8k_ptrs(void* base, int64_t k, int64_t m, int8_t** qs, float** d, int8_t** bsp) {
-    size_t qb = ((size_t)m * k + 255) & ~(size_t)255;
+    size_t qb = ((size_t)pad16(m) * k + 255) & ~(size_t)255;
     *qs = (int8_t*)base;
     *d = (float*)((uint8_t*)base + qb);
     if (bsp) *bsp = (int8_t*)((uint8_t*)base + qb + (size_t)(k / 256) * pad16(m) * sizeof(float));
 }
 
 hipError_t launch_quantize_split_q8k(const float* x, int64_t m, int64_t k, int8_t* qs, float* d, hipStream_t s,
-                                     int8_t* bsp) {
+                                     int8_t* bsp, bool tiled) {
     const int64_t nsb = k / 256;
     hipLaunchKernelGGL(k_quantize_split_q8k, dim3((unsigned)m, (unsigned)((nsb + 3) / 4)), dim3(256), 0, s, x, qs, d,
-                       bsp, (int)m, (int)k, (int)pad16(m));
+                       bsp, (int)m, (int)k, (int)pad16(m), tiled ? 1 : 0);
     return hipGetLastError();
 }
 
