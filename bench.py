@@ -258,7 +258,8 @@ def main():
                 "us_per_launch": per_b[str(b)]["us"], "traffic": traffic_of(b)}
 
     roofline = roof(1, "k_matvec<Q4_K, 1 row> (C2, B=1)")
-    roofline["also"] = [roof(b, "k_quantize_split_q8k + k_mv_dma<Q4_K, 8 superblocks, 2 tiles> (C2, B=%d)" % b)
+    roofline["also"] = [roof(b, "k_quantize_split_q8k + k_mv_dma_ma<8 superblocks, 2 weight tiles, 1 activation "
+                                "tile> (C2, B=%d)" % b)
                         for b in (8, 16)]
     del rot
     torch.cuda.empty_cache()
