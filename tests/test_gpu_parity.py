@@ -176,6 +176,26 @@ def test_prefill_q4k_few_rows(L, m, n, k):
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"few rows m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("m", [17, 40, 64])
+@pytest.mark.parametrize("mma", ["f16", "int8"])
+def test_prefill_q4k_few_rows_long_k(L, m, mma):
+    """Q4_K with 17..64 rows past k = 2048 keeps the earlier routes: the
+    skinny fp16 kernel, or with int8 planes selected the MFMA decode kernel
+    with four activation tiles."""
+    from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
+
+    n, k = 72, 4608
+    rng = np.random.default_rng(m + 7 * k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    set_prefill_mma(MMA_INT8 if mma == "int8" else MMA_F16)
+    try:
+        y, q = _qmm(L, O.Q4K, w, x)
+    finally:
+        set_prefill_mma(MMA_F16)
+    assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"few rows long k {mma} m={m}")
+
+
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 96), (300, 70, 160)])
 def test_prefill_gemm_q8_0_shapes(L, m, n, k):
     """The Q8_0 prefill GEMM (K in whole 256-element steps) on ragged tiles,
