@@ -994,7 +994,7 @@ static int64_t q6_min_rows() {
     return v;
 }
 
-// Q4_K with 17..64 rows and k <= 2048 takes the multi-tile DMA decode
+// Q4_K with 17..128 rows and k <= 2048 takes the multi-tile DMA decode
 // kernel (either prefill mode: its dots are int8 MFMAs on the Q8_K
 // activations, as the decode path's); LLOOM_HIP_MV_DMA_MA=0 (read once)
 // turns it off.

@@ -36,10 +36,10 @@ size_t matvec_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, int epi, hipStream_t s);
 // matvec.hip: Q4_K with up to MV_DMA_MA_MAX_ROWS rows and k <= 2048 on the
-// DMA kernel with one to four 16-row activation tiles (the decode path from
+// DMA kernel with one to eight 16-row activation tiles (the decode path from
 // 5 rows, the GEMM path from 17; the workspace is split_q8k_bytes: the split
 // quantizer in its tiled layout, then one launch).
-constexpr int MV_DMA_MA_MAX_ROWS = 64;
+constexpr int MV_DMA_MA_MAX_ROWS = 128;
 bool mv_dma_ma_fits(int type, int64_t k, int64_t m);
 hipError_t launch_mv_dma_ma(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
                             int epi, hipStream_t s);

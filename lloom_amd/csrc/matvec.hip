@@ -1021,7 +1021,7 @@ static hipError_t launch_mv_dma(const void* w, float* y, int64_t n, int64_t m, c
     return launch_mv_dma_k<T_Q6K, 8>(w, y, n, m, xq, xd, epi, s);
 }
 
-// Q4_K with 5 .. 64 activation rows and k <= 2048 (decode from B = 5 and
+// Q4_K with 5 .. 128 activation rows and k <= 2048 (decode from B = 5 and
 // short prefill): MA 16-row activation tiles (16 MA >= m) against NT 16-row
 // weight tiles, one superblock a wave
 // (NSB waves), so every unpacked weight superblock serves the MA activation
@@ -1117,8 +1117,10 @@ static hipError_t launch_mv_dma_ma_k(const void* w, float* y, int64_t n, int64_t
                                      const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
     const int mp = (int)((m + 15) & ~(int64_t)15);
     const int64_t tiles = (n + 15) / 16;
-    if (mv_dma_nt(tiles) == 2)
-        hipLaunchKernelGGL((k_mv_dma_ma<NSB, 2, MA>), dim3((unsigned)((tiles + 1) / 2)), dim3(64 * NSB), 0, s,
+    // two weight tiles a workgroup (as k_mv_dma) up to four activation
+    // tiles; past that one, so the partial sums fit LDS
+    if (MA <= 4 && mv_dma_nt(tiles) == 2)
+        hipLaunchKernelGGL((k_mv_dma_ma<NSB, MA <= 4 ? 2 : 1, MA>), dim3((unsigned)((tiles + 1) / 2)), dim3(64 * NSB), 0, s,
                            (const uint8_t*)w, xt, xd, bsp, y, (int)n, (int)m, mp, epi);
     else
         hipLaunchKernelGGL((k_mv_dma_ma<NSB, 1, MA>), dim3((unsigned)tiles), dim3(64 * NSB), 0, s, (const uint8_t*)w,
@@ -1156,7 +1158,9 @@ hipError_t launch_mv_dma_ma(const void* w, const float* x, float* y, int64_t n, 
     if (m <= 16) return launch_mv_dma_ma_m<1>(w, y, n, k, m, xt, xd, bsp, epi, s);
     if (m <= 32) return launch_mv_dma_ma_m<2>(w, y, n, k, m, xt, xd, bsp, epi, s);
     if (m <= 48) return launch_mv_dma_ma_m<3>(w, y, n, k, m, xt, xd, bsp, epi, s);
-    return launch_mv_dma_ma_m<4>(w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 64) return launch_mv_dma_ma_m<4>(w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 96) return launch_mv_dma_ma_m<6>(w, y, n, k, m, xt, xd, bsp, epi, s);
+    return launch_mv_dma_ma_m<8>(w, y, n, k, m, xt, xd, bsp, epi, s);
 }
 
 template <int TYPE, int MA>

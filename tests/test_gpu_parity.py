@@ -161,11 +161,11 @@ def test_prefill_gemm_q4k_shapes(L, m, n, k, mma):
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"gemm {mma} m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("m", [17, 24, 32, 33, 48, 49, 64])
+@pytest.mark.parametrize("m", [17, 24, 32, 33, 48, 49, 64, 65, 96, 100, 128])
 @pytest.mark.parametrize("n,k", [(6152, 2048), (1000, 1280), (40, 256)])
 def test_prefill_q4k_few_rows(L, m, n, k):
-    """Q4_K with 17..64 activation rows and k <= 2048 (the DMA kernel with
-    two to four 16-row activation tiles): two- and one-tile workgroups,
+    """Q4_K with 17..128 activation rows and k <= 2048 (the DMA kernel with
+    two to eight 16-row activation tiles): two- and one-tile workgroups,
     ragged n and m, 8, 5 and 1 superblocks, an all-zero activation block."""
     rng = np.random.default_rng(m * 31 + n + k)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
