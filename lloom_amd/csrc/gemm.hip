@@ -1063,7 +1063,7 @@ static int64_t skinny_max_rows() {
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s) {
     if (gemm_workspace_bytes(type, n, k, m, mode) > ws_cap) return hipErrorInvalidValue;
-    if (use_dma_ma(type, k, m)) return launch_mv_dma_ma(w, x, y, n, k, m, qbuf, epi, s);
+    if (use_dma_ma(type, k, m)) return launch_mv_dma_ma(type, w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(n, k, m) && mode != GEMM_INT8) {
         X16Ptrs p = x16_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);

@@ -41,8 +41,8 @@ hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int6
 // quantizer in its tiled layout, then one launch).
 constexpr int MV_DMA_MA_MAX_ROWS = 128;
 bool mv_dma_ma_fits(int type, int64_t k, int64_t m);
-hipError_t launch_mv_dma_ma(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
-                            int epi, hipStream_t s);
+hipError_t launch_mv_dma_ma(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
+                            void* ws, int epi, hipStream_t s);
 // matvec.hip: Q4_K / Q6_K with any number of rows on the MFMA decode kernel,
 // 64 activation rows per workgroup layer (the weights are re-read per
 // layer): the workspace quantizer, then one launch.

@@ -856,19 +856,12 @@ __global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ ps
     store_epi(&Y[i], v, epi);
 }
 
-// ---------------------- 3..16 rows, K <= 2048: the operands through LDS --
-// The same dots as k_mv_mfma (mf_compute on its operand layout) with a
-// load shape fit for a launch this short.  A workgroup of KQ * NT waves owns
-// NT 16-row tiles over all of K.  Its weights (NT x 16 consecutive rows, one
-// contiguous run each) and the quantized x (m rows of K bytes, contiguous)
-// go to LDS as global_load_lds DMAs of 1 KB a wave instruction, so every
-// load instruction covers eight whole cache lines; loading the MFMA operand
-// layout straight from global memory (16 rows x 48 bytes an instruction)
-// multiplies the memory requests and costs ~2 us of a ~6 us call.  After
-// one barrier, wave (tile, q) computes superblocks q, q + KQ, ... of its
-// tile out of LDS, and the KQ parts of K of a tile add up through LDS.
-// Rows past n load the last valid bytes again (their sums are never
-// stored); activation rows past m are zeroed by select.
+// ------------------- 3..128 rows, K <= 2048: weight DMAs, tiled activations --
+// Every weight byte goes to LDS as global_load_lds DMAs of 1 KB a wave
+// instruction, so every load instruction covers eight whole cache lines;
+// loading the MFMA operand layout straight from global memory (16 rows x 48
+// bytes an instruction) multiplies the memory requests and cost ~2 us of a
+// ~6 us call in the kernel before this one.
 constexpr int MV_DMA_KMAX = 2048;
 
 __device__ __forceinline__ void dma16(const void* src, void* lds) {
@@ -900,81 +893,9 @@ __device__ __forceinline__ void dma_rows(const uint8_t* __restrict__ src, int by
     }
 }
 
-// Q6_K, up to 16 activation rows: NT 16-row weight tiles a workgroup, KQ
-// waves a tile splitting K; weights and quantized activations both moved
-// into LDS by 1 KB DMAs (x in the split layout, row-major).
-template <int TYPE, int NSB, int NT, int KQ>
-__global__ __launch_bounds__(64 * KQ * NT) void k_mv_dma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
-                                                     const float* __restrict__ xd, float* __restrict__ Y, int n, int m,
-                                                     int mp, int epi) {
-    static_assert(TYPE == T_Q6K, "Q4_K takes k_mv_dma_ma");
-    constexpr int BB = Q6K_BYTES;
-    constexpr int WV = KQ * NT, K = 256 * NSB, RB = NSB * BB;
-    static_assert(RB % 16 == 0, "rows must be whole 16-byte DMA pieces");
-    constexpr int WP = lds_pitch(RB), XP = lds_pitch(K);
-    constexpr int NJ = (NSB + KQ - 1) / KQ;  // superblocks a wave computes
-    // each DMA instruction writes 1 KB; the slack takes the last one's overhang
-    __shared__ __align__(16) uint8_t wl[NT][16 * WP + 1024];
-    __shared__ __align__(16) uint8_t xl[16 * XP + 1024];
-    __shared__ float4 part[KQ - 1][NT][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane >> 4, c16 = lane & 15;
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int r0 = (blockIdx.x * NT + t) * 16;
-        const int valid = max(1, min(16, n - r0));
-        // rows past n reload the last valid piece (its overhang is the tail pad)
-        dma_rows<WP, WV>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave, lane);
-    }
-    dma_rows<XP, WV>((const uint8_t*)xq, K, m, K, m * K - 16, xl, wave, lane);
-    const int t = wave / KQ, q = wave % KQ;
-    float4 dy[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) dy[j] = *(const float4*)(xd + (int64_t)min(q + KQ * j, NSB - 1) * mp + 4 * g);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    const bool arow_ok = c16 < m;
-    const uint8_t* trow = &wl[t][c16 * WP];
-    const uint8_t* xrow = &xl[c16 * XP + 64 * g];
-    float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int sb = q + KQ * j;
-        if (sb < NSB) {  // wave-uniform
-            MfW<TYPE> wu;
-            mf_load<TYPE>(trow + sb * BB, g, wu);
-            long a[8];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint4 v = *(const uint4*)(xrow + sb * 256 + 16 * i);
-                a[2 * i] = arow_ok ? (long)(((uint64_t)v.y << 32) | v.x) : 0l;
-                a[2 * i + 1] = arow_ok ? (long)(((uint64_t)v.w << 32) | v.z) : 0l;
-            }
-            mf_compute<TYPE>(wu, a, dy[j], g, out);
-        }
-    }
-    if (q) part[q - 1][t][lane] = make_float4(out[0], out[1], out[2], out[3]);
-    __syncthreads();
-    if (q) return;
-#pragma unroll
-    for (int w = 0; w < KQ - 1; w++) {
-        const float4 p = part[w][t][lane];
-        out[0] += p.x;
-        out[1] += p.y;
-        out[2] += p.z;
-        out[3] += p.w;
-    }
-    const int row = (blockIdx.x * NT + t) * 16 + c16;
-    if (row < n) {
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-            if (4 * g + v < m) store_epi(&Y[(int64_t)(4 * g + v) * n + row], out[v], epi);
-    }
-}
-
-// LLOOM_HIP_MV_DMA: 0 = off (k_mv_mfma), 1 / 2 = tiles a workgroup, unset =
-// two tiles from 384 row tiles up (n >= 6144: 7.6 against 7.9 us at m = 16,
-// with fewer the grid gets too small: 7.1 against 6.7 on n = 2048)
+// LLOOM_HIP_MV_DMA: 0 = off (k_mv_mfma), 1 / 2 = weight tiles a workgroup,
+// unset = two from 384 weight tiles up (n >= 6144), one below (fewer
+// workgroups than CUs: n = 2048, m = 16 6.97 against 6.17 us with one)
 static int mv_dma_env() {
     static const int v = [] {
         const char* e = getenv("LLOOM_HIP_MV_DMA");
@@ -983,119 +904,109 @@ static int mv_dma_env() {
     return v;
 }
 static bool mv_dma_on() { return mv_dma_env() != 0; }
-// LLOOM_HIP_MV_DMA_KQ: waves a tile splits K over (4 or 8); unset = 8 with
-// one tile a workgroup (n = 2048, m = 16: 6.13 against 6.32 us), else 4
-static int mv_dma_kq_env() {
-    static const int v = [] {
-        const char* e = getenv("LLOOM_HIP_MV_DMA_KQ");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
 static int mv_dma_nt(int64_t tiles) { return mv_dma_env() > 0 ? mv_dma_env() : tiles >= 384 ? 2 : 1; }
 
-template <int TYPE, int NSB>
-static hipError_t launch_mv_dma_k(const void* w, float* y, int64_t n, int64_t m, const int8_t* xq, const float* xd,
-                                  int epi, hipStream_t s) {
-    const int mp = (int)((m + 15) & ~(int64_t)15);
-    const int64_t tiles = (n + 15) / 16;
-    const int kq = mv_dma_kq_env() ? mv_dma_kq_env() : mv_dma_nt(tiles) == 1 ? 8 : 4;
-    if (kq == 8 && mv_dma_nt(tiles) == 2)
-        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2, 8>), dim3((unsigned)((tiles + 1) / 2)), dim3(1024), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)m, mp, epi);
-    else if (kq == 8)
-        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1, 8>), dim3((unsigned)tiles), dim3(512), 0, s, (const uint8_t*)w, xq, xd,
-                           y, (int)n, (int)m, mp, epi);
-    else if (mv_dma_nt(tiles) == 2)
-        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 2, 4>), dim3((unsigned)((tiles + 1) / 2)), dim3(512), 0, s,
-                           (const uint8_t*)w, xq, xd, y, (int)n, (int)m, mp, epi);
-    else
-        hipLaunchKernelGGL((k_mv_dma<TYPE, NSB, 1, 4>), dim3((unsigned)tiles), dim3(256), 0, s, (const uint8_t*)w, xq, xd,
-                           y, (int)n, (int)m, mp, epi);
-    return hipGetLastError();
-}
-
-// Q6_K, k = 2048, up to 16 rows
-static hipError_t launch_mv_dma(const void* w, float* y, int64_t n, int64_t m, const int8_t* xq, const float* xd,
-                                int epi, hipStream_t s) {
-    return launch_mv_dma_k<T_Q6K, 8>(w, y, n, m, xq, xd, epi, s);
-}
-
-// Q4_K with 5 .. 128 activation rows and k <= 2048 (decode from B = 5 and
-// short prefill): MA 16-row activation tiles (16 MA >= m) against NT 16-row
-// weight tiles, one superblock a wave
-// (NSB waves), so every unpacked weight superblock serves the MA activation
+// Q4_K / Q6_K with k <= 2048 on 16-row activation tiles, from 3 rows
+// (decode) to 128 (short prefill; Q6_K to 16): MA 16-row activation tiles
+// (16 MA >= m) against NT 16-row weight tiles, one superblock a wave (NSB
+// waves), so every unpacked weight superblock serves the MA activation
 // tiles and every activation operand the NT weight tiles.  The weights move
-// as in k_mv_dma (1 KB DMAs of whole rows into LDS); the activations, MA
-// times the bytes of a decode call, skip LDS: each wave loads its
-// superblock's operands from the tiled layout of k_quantize_split_q8k
-// straight into registers, 1 KB of contiguous bytes an instruction, issued
-// with the DMAs.  The NSB partial sums of each (weight tile, activation
-// tile) meet in LDS and are added in superblock order, one pair a wave.
-// Rows past m in the last tile read the tile's padding and are never stored
-// (an activation row of the MFMA reaches only its own outputs).
-template <int NSB, int NT, int MA>
+// as 1 KB DMAs of whole rows into padded LDS rows; the activations, MA times
+// the bytes of a decode call, skip LDS: each wave loads its superblock's
+// operands from the tiled layout of k_quantize_split_q8k straight into
+// registers, 1 KB of contiguous bytes an instruction, issued with the DMAs.
+// The NSB partial sums of each (weight tile, activation tile) meet in LDS
+// and are added in superblock order, one pair a wave.  Rows past m in the
+// last tile read the tile's padding and are never stored (an activation row
+// of the MFMA reaches only its own outputs).
+template <int TYPE, int NSB, int NT, int MA>
 __global__ __launch_bounds__(64 * NSB) void k_mv_dma_ma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xt,
                                                       const float* __restrict__ xd, const int8_t* __restrict__ bsp,
                                                       float* __restrict__ Y, int n, int m, int mp, int epi) {
-    constexpr int BB = Q4K_BYTES, RB = NSB * BB;
+    constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES, RB = NSB * BB;
+    constexpr int WV = NSB, NJ = 1;
+    static_assert(NSB <= 8, "one superblock a wave, at most 8 waves");
     static_assert(RB % 16 == 0, "rows must be whole 16-byte DMA pieces");
     constexpr int WP = lds_pitch(RB);
     __shared__ __align__(16) uint8_t wl[NT][16 * WP + 1024];
-    __shared__ float4 part[NSB][NT * MA][64];
+    __shared__ float4 part[WV][NT * MA][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int r0 = (blockIdx.x * NT + t) * 16;
         const int valid = max(1, min(16, n - r0));
-        dma_rows<WP, NSB>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave,
-                          lane);
+        dma_rows<WP, WV>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave, lane);
     }
-    const int sb = wave;
     const int tiles = mp >> 4;  // activation tiles present (the rest load the last)
-    uint4 xv[MA][4];
-    float4 dy[MA];
-    long ab[MA];
+    // (NJ = 1: the per-superblock arrays keep the loops' shape)
+    uint4 xv[NJ][MA][4];
+    float4 dy[NJ][MA];
+    long ab[NJ][MA];
 #pragma unroll
-    for (int a = 0; a < MA; a++) {
-        const int at = min(a, tiles - 1);
-        const int8_t* src = xt + ((int64_t)(at * NSB + sb) * 4) * 1024 + 16 * lane;
+    for (int j = 0; j < NJ; j++) {
+        const int sb = wave * NJ + j;
 #pragma unroll
-        for (int i = 0; i < 4; i++) xv[a][i] = *(const uint4*)(src + 1024 * i);
-        dy[a] = *(const float4*)(xd + (int64_t)sb * mp + 16 * at + 4 * g);
-        // groups 0 and 1 read the lo and hi sums of row c16 (masked past m;
-        // loaded by every lane: a load under the condition would wait for
-        // the DMAs in flight)
-        const long v = *(const long*)(bsp + ((int64_t)sb * mp + 16 * at + c16) * 16 + 8 * min(g, 1));
-        ab[a] = v & -(long)(g < 2 && 16 * a + c16 < m);
+        for (int a = 0; a < MA; a++) {
+            const int at = min(a, tiles - 1);
+            const int8_t* src = xt + ((int64_t)(at * NSB + sb) * 4) * 1024 + 16 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[j][a][i] = *(const uint4*)(src + 1024 * i);
+            dy[j][a] = *(const float4*)(xd + (int64_t)sb * mp + 16 * at + 4 * g);
+            if constexpr (TYPE == T_Q4K) {
+                // groups 0 and 1 read the lo and hi sums of row c16 (masked
+                // past m; loaded by every lane: a load under the condition
+                // would wait for the DMAs in flight)
+                const long v = *(const long*)(bsp + ((int64_t)sb * mp + 16 * at + c16) * 16 + 8 * min(g, 1));
+                ab[j][a] = v & -(long)(g < 2 && 16 * a + c16 < m);
+            } else {
+                ab[j][a] = 0;
+            }
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    float out[NT][MA][4];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        MfW<T_Q4K> wu;
-        mf_load<T_Q4K>(&wl[t][c16 * WP] + sb * BB, g, wu);
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int a = 0; a < MA; a++) {
-            long av[8];
+        for (int a = 0; a < MA; a++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint4 v = xv[a][i];
-                av[2 * i] = (long)(((uint64_t)v.y << 32) | v.x);
-                av[2 * i + 1] = (long)(((uint64_t)v.w << 32) | v.z);
+            for (int v = 0; v < 4; v++) out[t][a][v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int sb = wave * NJ + j;
+        {
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                MfW<TYPE> wu;
+                mf_load<TYPE>(&wl[t][c16 * WP] + sb * BB, g, wu);
+#pragma unroll
+                for (int a = 0; a < MA; a++) {
+                    long av[8];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint4 v = xv[j][a][i];
+                        av[2 * i] = (long)(((uint64_t)v.y << 32) | v.x);
+                        av[2 * i + 1] = (long)(((uint64_t)v.w << 32) | v.z);
+                    }
+                    if constexpr (TYPE == T_Q4K) mf_compute_q4k_b(wu, av, ab[j][a], dy[j][a], g, out[t][a]);
+                    else mf_compute<TYPE>(wu, av, dy[j][a], g, out[t][a]);
+                }
             }
-            float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            mf_compute_q4k_b(wu, av, ab[a], dy[a], g, out);
-            part[sb][t * MA + a][lane] = make_float4(out[0], out[1], out[2], out[3]);
         }
     }
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int a = 0; a < MA; a++)
+            part[wave][t * MA + a][lane] = make_float4(out[t][a][0], out[t][a][1], out[t][a][2], out[t][a][3]);
     __syncthreads();
-    for (int pr = wave; pr < NT * MA; pr += NSB) {  // uniform
+    for (int pr = wave; pr < NT * MA; pr += WV) {  // uniform
         const int t = pr / MA, a = pr - t * MA;
         float4 acc = part[0][pr][lane];
 #pragma unroll
-        for (int w = 1; w < NSB; w++) {
+        for (int w = 1; w < WV; w++) {
             const float4 p = part[w][pr][lane];
             acc.x += p.x;
             acc.y += p.y;
@@ -1112,55 +1023,69 @@ __global__ __launch_bounds__(64 * NSB) void k_mv_dma_ma(const uint8_t* __restric
     }
 }
 
-template <int NSB, int MA>
+template <int TYPE, int NSB, int MA>
 static hipError_t launch_mv_dma_ma_k(const void* w, float* y, int64_t n, int64_t m, const int8_t* xt,
                                      const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
+    constexpr int WV = NSB;
     const int mp = (int)((m + 15) & ~(int64_t)15);
     const int64_t tiles = (n + 15) / 16;
-    // two weight tiles a workgroup (as k_mv_dma) up to four activation
-    // tiles; past that one, so the partial sums fit LDS
-    if (MA <= 4 && mv_dma_nt(tiles) == 2)
-        hipLaunchKernelGGL((k_mv_dma_ma<NSB, MA <= 4 ? 2 : 1, MA>), dim3((unsigned)((tiles + 1) / 2)), dim3(64 * NSB), 0, s,
-                           (const uint8_t*)w, xt, xd, bsp, y, (int)n, (int)m, mp, epi);
+    // two weight tiles a workgroup from 384 weight tiles up to four
+    // activation tiles; past that one, so the partial sums fit LDS
+    constexpr bool two = MA <= 4;
+    if (two && mv_dma_nt(tiles) == 2)
+        hipLaunchKernelGGL((k_mv_dma_ma<TYPE, NSB, two ? 2 : 1, MA>), dim3((unsigned)((tiles + 1) / 2)), dim3(64 * WV),
+                           0, s, (const uint8_t*)w, xt, xd, bsp, y, (int)n, (int)m, mp, epi);
     else
-        hipLaunchKernelGGL((k_mv_dma_ma<NSB, 1, MA>), dim3((unsigned)tiles), dim3(64 * NSB), 0, s, (const uint8_t*)w,
-                           xt, xd, bsp, y, (int)n, (int)m, mp, epi);
+        hipLaunchKernelGGL((k_mv_dma_ma<TYPE, NSB, 1, MA>), dim3((unsigned)tiles), dim3(64 * WV), 0, s,
+                           (const uint8_t*)w, xt, xd, bsp, y, (int)n, (int)m, mp, epi);
     return hipGetLastError();
 }
 
 template <int MA>
-static hipError_t launch_mv_dma_ma_m(const void* w, float* y, int64_t n, int64_t k, int64_t m, const int8_t* xt,
-                                     const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
+static hipError_t launch_mv_dma_ma_m(int type, const void* w, float* y, int64_t n, int64_t k, int64_t m,
+                                     const int8_t* xt, const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
+    if (type == T_Q6K) {
+        if constexpr (MA == 1) return launch_mv_dma_ma_k<T_Q6K, 8, 1>(w, y, n, m, xt, xd, bsp, epi, s);
+        return hipErrorInvalidValue;
+    }
     switch (k / 256) {
-        case 1: return launch_mv_dma_ma_k<1, MA>(w, y, n, m, xt, xd, bsp, epi, s);
-        case 2: return launch_mv_dma_ma_k<2, MA>(w, y, n, m, xt, xd, bsp, epi, s);
-        case 3: return launch_mv_dma_ma_k<3, MA>(w, y, n, m, xt, xd, bsp, epi, s);
-        case 4: return launch_mv_dma_ma_k<4, MA>(w, y, n, m, xt, xd, bsp, epi, s);
-        case 5: return launch_mv_dma_ma_k<5, MA>(w, y, n, m, xt, xd, bsp, epi, s);
-        case 6: return launch_mv_dma_ma_k<6, MA>(w, y, n, m, xt, xd, bsp, epi, s);
-        case 7: return launch_mv_dma_ma_k<7, MA>(w, y, n, m, xt, xd, bsp, epi, s);
-        default: return launch_mv_dma_ma_k<8, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 1: return launch_mv_dma_ma_k<T_Q4K, 1, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 2: return launch_mv_dma_ma_k<T_Q4K, 2, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 3: return launch_mv_dma_ma_k<T_Q4K, 3, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 4: return launch_mv_dma_ma_k<T_Q4K, 4, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 5: return launch_mv_dma_ma_k<T_Q4K, 5, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 6: return launch_mv_dma_ma_k<T_Q4K, 6, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        case 7: return launch_mv_dma_ma_k<T_Q4K, 7, MA>(w, y, n, m, xt, xd, bsp, epi, s);
+        default: return launch_mv_dma_ma_k<T_Q4K, 8, MA>(w, y, n, m, xt, xd, bsp, epi, s);
     }
 }
 
+// Shapes k_mv_dma_ma takes: Q4_K with k <= 2048 in whole superblocks, to
+// 128 rows; Q6_K at k = 2048 (its rows are whole 16-byte DMA pieces at 8
+// superblocks), to 16 rows.  Longer k stays on the split-K MFMA kernel: a
+// single-tile workgroup streaming a whole long row block measured slower
+// (Q6_K [2048, 8192] at m = 16: 16.7 against 13.4 us).
 bool mv_dma_ma_fits(int type, int64_t k, int64_t m) {
-    return type == T_Q4K && m <= MV_DMA_MA_MAX_ROWS && k <= MV_DMA_KMAX && k % 256 == 0 && mv_dma_on();
+    if (k % 256 || !mv_dma_on() || m > MV_DMA_MA_MAX_ROWS) return false;
+    if (type == T_Q4K) return k <= MV_DMA_KMAX;
+    if (type == T_Q6K) return k == MV_DMA_KMAX && m <= 16;
+    return false;
 }
 
-hipError_t launch_mv_dma_ma(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
-                            int epi, hipStream_t s) {
+hipError_t launch_mv_dma_ma(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
+                            void* ws, int epi, hipStream_t s) {
     int8_t* xt;
     float* xd;
     int8_t* bsp;
     split_q8k_ptrs(ws, k, m, &xt, &xd, &bsp);
-    hipError_t e = launch_quantize_split_q8k(x, m, k, xt, xd, s, bsp, true);
+    hipError_t e = launch_quantize_split_q8k(x, m, k, xt, xd, s, type == T_Q4K ? bsp : nullptr, true);
     if (e != hipSuccess) return e;
-    if (m <= 16) return launch_mv_dma_ma_m<1>(w, y, n, k, m, xt, xd, bsp, epi, s);
-    if (m <= 32) return launch_mv_dma_ma_m<2>(w, y, n, k, m, xt, xd, bsp, epi, s);
-    if (m <= 48) return launch_mv_dma_ma_m<3>(w, y, n, k, m, xt, xd, bsp, epi, s);
-    if (m <= 64) return launch_mv_dma_ma_m<4>(w, y, n, k, m, xt, xd, bsp, epi, s);
-    if (m <= 96) return launch_mv_dma_ma_m<6>(w, y, n, k, m, xt, xd, bsp, epi, s);
-    return launch_mv_dma_ma_m<8>(w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 16) return launch_mv_dma_ma_m<1>(type, w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 32) return launch_mv_dma_ma_m<2>(type, w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 48) return launch_mv_dma_ma_m<3>(type, w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 64) return launch_mv_dma_ma_m<4>(type, w, y, n, k, m, xt, xd, bsp, epi, s);
+    if (m <= 96) return launch_mv_dma_ma_m<6>(type, w, y, n, k, m, xt, xd, bsp, epi, s);
+    return launch_mv_dma_ma_m<8>(type, w, y, n, k, m, xt, xd, bsp, epi, s);
 }
 
 template <int TYPE, int MA>
@@ -1225,20 +1150,19 @@ hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int6
     if (type != T_Q8_0 && !mv_dot(type, n, k, m) && m <= FUSED_MAX_ROWS && (k == 2048 || k == 1024))
         return type == T_Q4K ? launch_fused<T_Q4K>(w, x, y, n, k, m, epi, s)
                              : launch_fused<T_Q6K>(w, x, y, n, k, m, epi, s);
-    // Q4_K from 5 rows (k <= 2048): the split quantizer in its tiled layout,
-    // then k_mv_dma_ma with one activation tile (C2, B = 8 / 16: 7.28 /
-    // 7.37 us against 7.41 / 7.62 for k_mv_dma with x staged in LDS)
-    if (type == T_Q4K && !mv_dot(type, n, k, m) && mv_dma_ma_fits(type, k, m))
-        return launch_mv_dma_ma(w, x, y, n, k, m, ws, epi, s);
+    // Past the dot4 and fused kernels, up to 2048 elements of k: the split
+    // quantizer in its tiled layout, then k_mv_dma_ma with one activation
+    // tile (C2, B = 8 / 16: 7.28 / 7.37 us against 7.41 / 7.62 for the
+    // earlier kernel with x staged in LDS; Q6_K [8192, 2048] 11.35 / 11.34
+    // against 11.87 / 12.19)
+    if (type != T_Q8_0 && !mv_dot(type, n, k, m) && mv_dma_ma_fits(type, k, m))
+        return launch_mv_dma_ma(type, w, x, y, n, k, m, ws, epi, s);
     if (type != T_Q8_0 && !mv_dot(type, n, k, m)) {
         int8_t* xq;
         float* xd;
         split_q8k_ptrs(ws, k, m, &xq, &xd);
-        // Q6_K rows are 16-byte multiples (whole DMA pieces) at k = 2048 only
-        const bool dma = type == T_Q6K && k == MV_DMA_KMAX && m <= 16 && mv_dma_on();
         hipError_t e = launch_quantize_split_q8k(x, m, k, xq, xd, s);
         if (e != hipSuccess) return e;
-        if (dma) return launch_mv_dma(w, y, n, m, xq, xd, epi, s);
         float* ps = mv_psum(ws, k, m);
         return type == T_Q4K ? launch_mv_mfma<T_Q4K, 1>(w, y, n, k, m, xq, xd, epi, s, ps)
                              : launch_mv_mfma<T_Q6K, 1>(w, y, n, k, m, xq, xd, epi, s, ps);
