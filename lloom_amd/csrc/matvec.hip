@@ -924,89 +924,69 @@ __global__ __launch_bounds__(64 * NSB) void k_mv_dma_ma(const uint8_t* __restric
                                                       const float* __restrict__ xd, const int8_t* __restrict__ bsp,
                                                       float* __restrict__ Y, int n, int m, int mp, int epi) {
     constexpr int BB = TYPE == T_Q4K ? Q4K_BYTES : Q6K_BYTES, RB = NSB * BB;
-    constexpr int WV = NSB, NJ = 1;
     static_assert(NSB <= 8, "one superblock a wave, at most 8 waves");
     static_assert(RB % 16 == 0, "rows must be whole 16-byte DMA pieces");
     constexpr int WP = lds_pitch(RB);
     __shared__ __align__(16) uint8_t wl[NT][16 * WP + 1024];
-    __shared__ float4 part[WV][NT * MA][64];
+    __shared__ float4 part[NSB][NT * MA][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
+    const int sb = wave;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int r0 = (blockIdx.x * NT + t) * 16;
         const int valid = max(1, min(16, n - r0));
-        dma_rows<WP, WV>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave, lane);
+        dma_rows<WP, NSB>(W + (int64_t)min(r0, n - 1) * RB, RB, 16, RB, (valid * RB - 1) & ~15, &wl[t][0], wave,
+                          lane);
     }
     const int tiles = mp >> 4;  // activation tiles present (the rest load the last)
-    // (NJ = 1: the per-superblock arrays keep the loops' shape)
-    uint4 xv[NJ][MA][4];
-    float4 dy[NJ][MA];
-    long ab[NJ][MA];
+    uint4 xv[MA][4];
+    float4 dy[MA];
+    long ab[MA];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int sb = wave * NJ + j;
+    for (int a = 0; a < MA; a++) {
+        const int at = min(a, tiles - 1);
+        const int8_t* src = xt + ((int64_t)(at * NSB + sb) * 4) * 1024 + 16 * lane;
 #pragma unroll
-        for (int a = 0; a < MA; a++) {
-            const int at = min(a, tiles - 1);
-            const int8_t* src = xt + ((int64_t)(at * NSB + sb) * 4) * 1024 + 16 * lane;
-#pragma unroll
-            for (int i = 0; i < 4; i++) xv[j][a][i] = *(const uint4*)(src + 1024 * i);
-            dy[j][a] = *(const float4*)(xd + (int64_t)sb * mp + 16 * at + 4 * g);
-            if constexpr (TYPE == T_Q4K) {
-                // groups 0 and 1 read the lo and hi sums of row c16 (masked
-                // past m; loaded by every lane: a load under the condition
-                // would wait for the DMAs in flight)
-                const long v = *(const long*)(bsp + ((int64_t)sb * mp + 16 * at + c16) * 16 + 8 * min(g, 1));
-                ab[j][a] = v & -(long)(g < 2 && 16 * a + c16 < m);
-            } else {
-                ab[j][a] = 0;
-            }
+        for (int i = 0; i < 4; i++) xv[a][i] = *(const uint4*)(src + 1024 * i);
+        dy[a] = *(const float4*)(xd + (int64_t)sb * mp + 16 * at + 4 * g);
+        if constexpr (TYPE == T_Q4K) {
+            // groups 0 and 1 read the lo and hi sums of row c16 (masked past
+            // m; loaded by every lane: a load under the condition would wait
+            // for the DMAs in flight)
+            const long v = *(const long*)(bsp + ((int64_t)sb * mp + 16 * at + c16) * 16 + 8 * min(g, 1));
+            ab[a] = v & -(long)(g < 2 && 16 * a + c16 < m);
+        } else {
+            ab[a] = 0;
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    float out[NT][MA][4];
 #pragma unroll
-    for (int t = 0; t < NT; t++)
+    for (int t = 0; t < NT; t++) {
+        MfW<TYPE> wu;
+        mf_load<TYPE>(&wl[t][c16 * WP] + sb * BB, g, wu);
 #pragma unroll
-        for (int a = 0; a < MA; a++)
+        for (int a = 0; a < MA; a++) {
+            long av[8];
 #pragma unroll
-            for (int v = 0; v < 4; v++) out[t][a][v] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int sb = wave * NJ + j;
-        {
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                MfW<TYPE> wu;
-                mf_load<TYPE>(&wl[t][c16 * WP] + sb * BB, g, wu);
-#pragma unroll
-                for (int a = 0; a < MA; a++) {
-                    long av[8];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint4 v = xv[j][a][i];
-                        av[2 * i] = (long)(((uint64_t)v.y << 32) | v.x);
-                        av[2 * i + 1] = (long)(((uint64_t)v.w << 32) | v.z);
-                    }
-                    if constexpr (TYPE == T_Q4K) mf_compute_q4k_b(wu, av, ab[j][a], dy[j][a], g, out[t][a]);
-                    else mf_compute<TYPE>(wu, av, dy[j][a], g, out[t][a]);
-                }
+            for (int i = 0; i < 4; i++) {
+                const uint4 v = xv[a][i];
+                av[2 * i] = (long)(((uint64_t)v.y << 32) | v.x);
+                av[2 * i + 1] = (long)(((uint64_t)v.w << 32) | v.z);
             }
+            float out[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (TYPE == T_Q4K) mf_compute_q4k_b(wu, av, ab[a], dy[a], g, out);
+            else mf_compute<TYPE>(wu, av, dy[a], g, out);
+            part[sb][t * MA + a][lane] = make_float4(out[0], out[1], out[2], out[3]);
         }
     }
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int a = 0; a < MA; a++)
-            part[wave][t * MA + a][lane] = make_float4(out[t][a][0], out[t][a][1], out[t][a][2], out[t][a][3]);
     __syncthreads();
-    for (int pr = wave; pr < NT * MA; pr += WV) {  // uniform
+    for (int pr = wave; pr < NT * MA; pr += NSB) {  // uniform
         const int t = pr / MA, a = pr - t * MA;
         float4 acc = part[0][pr][lane];
 #pragma unroll
-        for (int w = 1; w < WV; w++) {
+        for (int w = 1; w < NSB; w++) {
             const float4 p = part[w][pr][lane];
             acc.x += p.x;
             acc.y += p.y;
@@ -1026,17 +1006,16 @@ __global__ __launch_bounds__(64 * NSB) void k_mv_dma_ma(const uint8_t* __restric
 template <int TYPE, int NSB, int MA>
 static hipError_t launch_mv_dma_ma_k(const void* w, float* y, int64_t n, int64_t m, const int8_t* xt,
                                      const float* xd, const int8_t* bsp, int epi, hipStream_t s) {
-    constexpr int WV = NSB;
     const int mp = (int)((m + 15) & ~(int64_t)15);
     const int64_t tiles = (n + 15) / 16;
     // two weight tiles a workgroup from 384 weight tiles up to four
     // activation tiles; past that one, so the partial sums fit LDS
     constexpr bool two = MA <= 4;
     if (two && mv_dma_nt(tiles) == 2)
-        hipLaunchKernelGGL((k_mv_dma_ma<TYPE, NSB, two ? 2 : 1, MA>), dim3((unsigned)((tiles + 1) / 2)), dim3(64 * WV),
+        hipLaunchKernelGGL((k_mv_dma_ma<TYPE, NSB, two ? 2 : 1, MA>), dim3((unsigned)((tiles + 1) / 2)), dim3(64 * NSB),
                            0, s, (const uint8_t*)w, xt, xd, bsp, y, (int)n, (int)m, mp, epi);
     else
-        hipLaunchKernelGGL((k_mv_dma_ma<TYPE, NSB, 1, MA>), dim3((unsigned)tiles), dim3(64 * WV), 0, s,
+        hipLaunchKernelGGL((k_mv_dma_ma<TYPE, NSB, 1, MA>), dim3((unsigned)tiles), dim3(64 * NSB), 0, s,
                            (const uint8_t*)w, xt, xd, bsp, y, (int)n, (int)m, mp, epi);
     return hipGetLastError();
 }
