@@ -196,6 +196,36 @@ def test_prefill_q4k_few_rows_long_k(L, m, mma):
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"few rows long k {mma} m={m}")
 
 
+def _random_shapes(count, seed=20261202):
+    """(dt, m, n, k) drawn across every routing band: m from each of
+    1-2, 3-4, 5-16, 17-64, 65-128 and 129-600 rows; k in whole blocks up to
+    4608 (Q4_K / Q6_K in superblocks, Q8_0 in 32-element blocks); n ragged;
+    m * n * k kept below 2.5e8 so the oracle stays fast."""
+    rng = np.random.default_rng(seed)
+    bands = [(1, 2), (3, 4), (5, 16), (17, 64), (65, 128), (129, 600)]
+    out = []
+    while len(out) < count:
+        dt = [O.Q8_0, O.Q4K, O.Q6K][len(out) % 3]
+        lo, hi = bands[(len(out) // 3) % len(bands)]
+        m = int(rng.integers(lo, hi + 1))
+        be = 32 if dt == O.Q8_0 else 256
+        k = be * int(rng.integers(1, 4608 // be + 1))
+        n = int(rng.integers(1, 3000))
+        if m * n * k <= 2.5e8:
+            out.append((dt, m, n, k))
+    return out
+
+
+@pytest.mark.parametrize("dt,m,n,k", _random_shapes(54))
+def test_random_shapes_all_routes(L, dt, m, n, k):
+    """Seeded random shapes through every route against the oracle."""
+    rng = np.random.default_rng(m * 131 + n * 7 + k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y, q = _qmm(L, dt, w, x)
+    assert_rows_close(y, O.matmul(dt, x, q, n), what=f"random dt={dt} m={m} n={n} k={k}")
+
+
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 96), (300, 70, 160)])
 def test_prefill_gemm_q8_0_shapes(L, m, n, k):
     """The Q8_0 prefill GEMM (K in whole 256-element steps) on ragged tiles,
