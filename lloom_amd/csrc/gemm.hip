@@ -1037,8 +1037,8 @@ static hipError_t launch_x16(const void* w, const X16Ptrs& p, float* y, int64_t 
 
 // LLOOM_HIP_X16_TILE (read once) picks the tile for tuning: 0 = 256 x 128,
 // 1 = 128 x 256, 2 = 128 x 128 (4 waves, 128 x 64 or 64 x 64 each), 3 =
-// 128 x 256 with 8 waves of 64 x 64 (two per SIMD); -1 (default) chooses
-// by m.
+// 128 x 256 with 8 waves of 64 x 64 (two per SIMD), 4 = 64 x 128 (4 waves
+// of 32 x 64); -1 (default) chooses by m.
 static int x16_tile_env() {
     static const int v = [] {
         const char* e = getenv("LLOOM_HIP_X16_TILE");
@@ -1107,13 +1107,16 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
         // 128 x 256 tiles (8 waves) past 512 rows: there the 128 x 128
         // tiles start a second, mostly empty round of workgroups (measured
         // on [8192, 2048]: m = 640 53.7 against 70.1 us, m = 512 52.2
-        // against 42.0)
+        // against 42.0); 64 x 128 tiles to 256 rows, twice the workgroups
+        // of 128 x 128 (m = 160 26.6 against 32.5 us, m = 256 27.6 / 32.7;
+        // m = 320 35.4 / 33.9)
         int tile = x16_tile_env();
-        if (tile < 0) tile = m > 512 ? 3 : 2;
+        if (tile < 0) tile = m > 512 ? 3 : m > 256 ? 2 : 4;
         switch (tile) {
             case 0: return launch_x16<4, 2, 4>(w, p, y, n, k, m, epi, s);
             case 1: return launch_x16<4, 4, 4>(w, p, y, n, k, m, epi, s);
             case 3: return launch_x16<2, 4, 8>(w, p, y, n, k, m, epi, s);
+            case 4: return launch_x16<1, 2, 4>(w, p, y, n, k, m, epi, s);
             default: return launch_x16<2, 2, 4>(w, p, y, n, k, m, epi, s);
         }
     }

@@ -140,7 +140,7 @@ def test_qmatmul_matches_oracle(L, dt, m):
 
 GEMM_SHAPES = [(17, 1, 256), (64, 128, 2048), (100, 7, 768), (128, 300, 512), (96, 200, 2048), (129, 40, 2048),
                (64, 8200, 512), (128, 8200, 256), (200, 129, 1024), (1030, 130, 512), (257, 64, 256),
-               (512, 256, 2048)]
+               (512, 256, 2048), (129, 520, 768), (256, 1000, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k,mma", [s + (mma,) for s in GEMM_SHAPES for mma in ("f16", "int8")])
