@@ -310,7 +310,7 @@ def run_details(L, cu, np, torch, dev, args):
     # C3 Q4_K prefill
     n, k = 8192, 2048
     qt = L.QTensor.quantize(cu(L.synth_normal(2, n * k, 0.0, 0.02)).view(n, k), L.GgmlDType.Q4K)
-    from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
+    from lloom_amd.quantized import MMA_AUTO, MMA_F16, MMA_INT8, set_prefill_mma
 
     # rotating weight copies (>= 512 MB together, past the 256 MB MALL), one
     # call a copy, all of them in one graph: the per-call figure carries
@@ -329,7 +329,7 @@ def run_details(L, cu, np, torch, dev, args):
             c3[str(m)] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 2),
                           "i8_peak_frac": round(ops / t / 1e12 / I8_PEAK_TOPS, 4)}
         out["c3_q4k_prefill_" + mode_name] = c3
-    set_prefill_mma(MMA_F16)
+    set_prefill_mma(MMA_AUTO)
     del rot3
     torch.cuda.empty_cache()
     # prefill of the other weight types on their GEMMs (not a BASELINE

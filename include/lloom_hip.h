@@ -76,14 +76,16 @@ int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows);
 /* Matrix-core family of the Q4_K prefill GEMM (m > mv_rows_max).  Both
  * compute the CPU arm's integer sums exactly (Q8_K activations, per-sub-block
  * integer scales) and combine them in f32 once per superblock:
- * LLOOM_HIP_MMA_F16 (default): the integer operands x8 and sc * q, both
- *   exact in fp16, on v_mfma_f32_32x32x16_f16 (f32 accumulation of exact
- *   products), the min term as one more MFMA;
+ * LLOOM_HIP_MMA_F16: the integer operands x8 and sc * q, both exact in
+ *   fp16, on v_mfma_f32_32x32x16_f16 (f32 accumulation of exact products),
+ *   the min term as one more MFMA;
  * LLOOM_HIP_MMA_INT8: v_mfma_i32_32x32x32_i8 with the weights split into
- *   two int8 planes (sc = 8 sc_hi + sc_lo).
- * LLOOM_HIP_PREFILL_MMA=int8 sets the default of new contexts.  No
- * counterpart in the reference (its CUDA arm has one MMQ kernel). */
-enum { LLOOM_HIP_MMA_F16 = 0, LLOOM_HIP_MMA_INT8 = 1 };
+ *   two int8 planes (sc = 8 sc_hi + sc_lo);
+ * LLOOM_HIP_MMA_AUTO (default): F16 up to 512 rows, INT8 past (each the
+ *   faster there).
+ * LLOOM_HIP_PREFILL_MMA=f16|int8|auto sets the default of new contexts.
+ * No counterpart in the reference (its CUDA arm has one MMQ kernel). */
+enum { LLOOM_HIP_MMA_F16 = 0, LLOOM_HIP_MMA_INT8 = 1, LLOOM_HIP_MMA_AUTO = 2 };
 int lloom_hip_ctx_set_prefill_mma(lloom_hip_ctx* ctx, int mode);
 
 /* Wait for the device; report a device-side error (an out-of-range expert

@@ -105,7 +105,7 @@ int lloom_hip_ctx_create(int device, lloom_hip_ctx** out) {
     HIP_OK(hipSetDevice(device));
     lloom_hip_ctx* c = new lloom_hip_ctx();
     c->device = device;
-    if (const char* e = getenv("LLOOM_HIP_PREFILL_MMA")) c->prefill_mma = strcmp(e, "int8") == 0 ? GEMM_INT8 : GEMM_F16;
+    c->prefill_mma = gemm_mode_env(getenv("LLOOM_HIP_PREFILL_MMA"));
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return fail(LLOOM_HIP_EHIP, "ctx_create: stream creation failed");
@@ -144,9 +144,9 @@ int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows) {
 
 int lloom_hip_ctx_set_prefill_mma(lloom_hip_ctx* ctx, int mode) {
     if (!ctx) return fail(LLOOM_HIP_EINVAL, "set_prefill_mma: null context");
-    if (mode != LLOOM_HIP_MMA_F16 && mode != LLOOM_HIP_MMA_INT8)
-        return fail(LLOOM_HIP_EINVAL, "set_prefill_mma: mode %d is neither F16 (0) nor INT8 (1)", mode);
-    ctx->prefill_mma = mode == LLOOM_HIP_MMA_INT8 ? GEMM_INT8 : GEMM_F16;
+    if (mode != LLOOM_HIP_MMA_F16 && mode != LLOOM_HIP_MMA_INT8 && mode != LLOOM_HIP_MMA_AUTO)
+        return fail(LLOOM_HIP_EINVAL, "set_prefill_mma: mode %d is none of F16 (0), INT8 (1), AUTO (2)", mode);
+    ctx->prefill_mma = mode == LLOOM_HIP_MMA_INT8 ? GEMM_INT8 : mode == LLOOM_HIP_MMA_F16 ? GEMM_F16 : GEMM_AUTO;
     return LLOOM_HIP_OK;
 }
 
@@ -364,9 +364,7 @@ int lloom_hip_qmatmul_workspace_bytes(lloom_hip_ctx* ctx, int ggml_type, int64_t
     if (n <= 0 || k <= 0 || m <= 0 || k % block_elems(ggml_type))
         return fail(LLOOM_HIP_ESHAPE, "qmatmul_workspace_bytes: bad shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
     const int rows_max = ctx ? ctx->mv_rows_max : 16;
-    int mma = GEMM_F16;
-    if (ctx) mma = ctx->prefill_mma;
-    else if (const char* e = getenv("LLOOM_HIP_PREFILL_MMA")) mma = strcmp(e, "int8") == 0 ? GEMM_INT8 : GEMM_F16;
+    const int mma = ctx ? ctx->prefill_mma : gemm_mode_env(getenv("LLOOM_HIP_PREFILL_MMA"));
     *bytes = qmm_plan(rows_max, mma, ggml_type, n, k, m, x_dtype, y_dtype).total;
     return LLOOM_HIP_OK;
 }

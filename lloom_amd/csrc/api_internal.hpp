@@ -22,7 +22,7 @@ struct lloom_hip_ctx {
     std::vector<void*> retired;
     int* flags = nullptr;  // [0] sticky expert-id error
     int mv_rows_max = 16;
-    int prefill_mma = lloom::GEMM_F16;
+    int prefill_mma = lloom::GEMM_AUTO;
     std::mutex mu;
 };
 

@@ -1008,6 +1008,7 @@ static bool use_dma_ma(int type, int64_t k, int64_t m) {
 
 static int64_t skinny_max_rows();
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode) {
+    mode = gemm_mode(mode, m);
     if (use_dma_ma(type, k, m)) return split_q8k_bytes(k, m);
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(0, k, m) && mode != GEMM_INT8) return x16_bytes(m, k);
     if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m)) return q6_gemm_workspace_bytes(n, k, m);
@@ -1062,6 +1063,7 @@ static int64_t skinny_max_rows() {
 
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s) {
+    mode = gemm_mode(mode, m);
     if (gemm_workspace_bytes(type, n, k, m, mode) > ws_cap) return hipErrorInvalidValue;
     if (use_dma_ma(type, k, m)) return launch_mv_dma_ma(type, w, x, y, n, k, m, qbuf, epi, s);
     if (type == T_Q4K && m <= skinny_max_rows() && fits_32bit(n, k, m) && mode != GEMM_INT8) {

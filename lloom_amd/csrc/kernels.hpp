@@ -52,7 +52,21 @@ hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t 
 // gemm.hip: m > 16 rows.  Q4_K on MFMA (mode: GEMM_F16, exact integer
 // operands on fp16 MFMA, or GEMM_INT8, two int8 scale planes), the
 // other types through decode tiles; qbuf is workspace for the prepared x.
-constexpr int GEMM_F16 = 0, GEMM_INT8 = 1;
+constexpr int GEMM_F16 = 0, GEMM_INT8 = 1, GEMM_AUTO = 2;
+// GEMM_AUTO's choice: the fp16 route to 512 rows (m = 512 on [8192, 2048]:
+// 40.2 against 47.3 us), the int8 planes past (m = 768 49.5 / 51.8, 1024
+// 53.7 / 57.2, 2048 101.5 / 104.0)
+constexpr int64_t GEMM_AUTO_INT8_ROWS = 512;
+inline int gemm_mode(int mode, int64_t m) {
+    return mode == GEMM_AUTO ? (m > GEMM_AUTO_INT8_ROWS ? GEMM_INT8 : GEMM_F16) : mode;
+}
+// LLOOM_HIP_PREFILL_MMA: "int8", "f16", anything else or unset: auto
+inline int gemm_mode_env(const char* e) {
+    if (!e) return GEMM_AUTO;
+    if (e[0] == 'i' && e[1] == 'n' && e[2] == 't' && e[3] == '8' && !e[4]) return GEMM_INT8;
+    if (e[0] == 'f' && e[1] == '1' && e[2] == '6' && !e[3]) return GEMM_F16;
+    return GEMM_AUTO;
+}
 hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                        void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode);

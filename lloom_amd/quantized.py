@@ -138,13 +138,14 @@ def set_mv_rows_max(rows, device=0):
     check(lib().lloom_hip_ctx_set_mv_rows_max(_ctx(device), rows))
 
 
-MMA_F16, MMA_INT8 = 0, 1
+MMA_F16, MMA_INT8, MMA_AUTO = 0, 1, 2
 
 
 def set_prefill_mma(mode, device=0):
-    """Matrix-core family of the Q4_K prefill GEMM: MMA_F16 (default: the
-    exact integer operands on fp16 MFMA) or MMA_INT8 (two int8 scale planes).
-    Both compute the CPU arm's integer sums exactly."""
+    """Matrix-core family of the Q4_K prefill GEMM: MMA_F16 (the exact
+    integer operands on fp16 MFMA), MMA_INT8 (two int8 scale planes) or
+    MMA_AUTO (the default: F16 up to 512 rows, INT8 past).  All compute the
+    CPU arm's integer sums exactly."""
     check(lib().lloom_hip_ctx_set_prefill_mma(_ctx(device), mode))
 
 

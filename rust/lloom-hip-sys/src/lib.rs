@@ -44,6 +44,7 @@ pub const LLOOM_HIP_Q8K: c_int = 15;
 // Prefill operand mode (lloom_hip_ctx_set_prefill_mma).
 pub const LLOOM_HIP_MMA_F16: c_int = 0;
 pub const LLOOM_HIP_MMA_INT8: c_int = 1;
+pub const LLOOM_HIP_MMA_AUTO: c_int = 2;
 
 // Fused stores (MvStore: none / Silu / MulInto).
 pub const LLOOM_HIP_STORE_PLAIN: c_int = 0;

@@ -54,7 +54,7 @@ def test_c3_q4k_prefill_m2048(L, mma):
     """C3 at M = 2048 on W [8192, 2048] (the largest prefill tile, every
     activation row), checked on a column subset that covers every column
     tile and both halves of each."""
-    from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
+    from lloom_amd.quantized import MMA_AUTO, MMA_F16, MMA_INT8, set_prefill_mma
 
     n, k, m = 8192, 2048, 2048
     w = L.synth_normal(2, n * k, 0.0, 0.02).reshape(n, k)
@@ -64,7 +64,7 @@ def test_c3_q4k_prefill_m2048(L, mma):
     try:
         y = L.QMatMul.from_qtensor(qt).forward(_cuda(x)).cpu().numpy()
     finally:
-        set_prefill_mma(MMA_F16)
+        set_prefill_mma(MMA_AUTO)
     cols = np.unique(np.concatenate([np.arange(0, n, 53), np.arange(127, n, 128)]))
     want = O.matmul(O.Q4K, x, _rows_of(qt.data(), O.Q4K, k, cols), len(cols))
     assert_rows_close(y[:, cols], want, what=f"C3 m=2048 {mma}")

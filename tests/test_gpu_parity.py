@@ -147,7 +147,7 @@ GEMM_SHAPES = [(17, 1, 256), (64, 128, 2048), (100, 7, 768), (128, 300, 512), (9
 def test_prefill_gemm_q4k_shapes(L, m, n, k, mma):
     """Both prefill GEMMs (exact fp16 operands, the default, and int8 scale
     planes) on ragged tiles (m, n not multiples of the tile)."""
-    from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
+    from lloom_amd.quantized import MMA_AUTO, MMA_F16, MMA_INT8, set_prefill_mma
 
     rng = np.random.default_rng(m * 7 + n)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -157,7 +157,7 @@ def test_prefill_gemm_q4k_shapes(L, m, n, k, mma):
     try:
         y, q = _qmm(L, O.Q4K, w, x)
     finally:
-        set_prefill_mma(MMA_F16)
+        set_prefill_mma(MMA_AUTO)
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"gemm {mma} m={m} n={n} k={k}")
 
 
@@ -182,7 +182,7 @@ def test_prefill_q4k_few_rows_long_k(L, m, mma):
     """Q4_K with 17..64 rows past k = 2048 keeps the earlier routes: the
     skinny fp16 kernel, or with int8 planes selected the MFMA decode kernel
     with four activation tiles."""
-    from lloom_amd.quantized import MMA_F16, MMA_INT8, set_prefill_mma
+    from lloom_amd.quantized import MMA_AUTO, MMA_F16, MMA_INT8, set_prefill_mma
 
     n, k = 72, 4608
     rng = np.random.default_rng(m + 7 * k)
@@ -192,7 +192,7 @@ def test_prefill_q4k_few_rows_long_k(L, m, mma):
     try:
         y, q = _qmm(L, O.Q4K, w, x)
     finally:
-        set_prefill_mma(MMA_F16)
+        set_prefill_mma(MMA_AUTO)
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"few rows long k {mma} m={m}")
 
 
@@ -741,6 +741,11 @@ def test_refusals_are_named(L):
     y = torch.empty((1, 4), device=DEV)
     rc = lib().lloom_hip_qmatmul(_ctx(0), 15, _ptr(qt.storage), 4, 256, _ptr(x), 0, 1, _ptr(y), 0, _stream(x))
     assert rc == 2 and b"Q8K" in lib().lloom_hip_last_error()
+    # prefill matrix-core modes: F16 (0), INT8 (1), AUTO (2, the default); others refused
+    assert lib().lloom_hip_ctx_set_prefill_mma(_ctx(0), 3) == 1
+    assert b"AUTO (2)" in lib().lloom_hip_last_error()
+    for mode in (0, 1, 2):
+        assert lib().lloom_hip_ctx_set_prefill_mma(_ctx(0), mode) == 0
 
 
 @pytest.mark.parametrize("dt,m,n,k", [(O.Q8_0, 9, 300, 2048), (O.Q8_0, 100, 300, 2048), (O.Q8_0, 600, 300, 1024),
