@@ -5,6 +5,8 @@ Bars: quantizers and dequantizers bit-exact; matmul max|d| <= 1e-3 * max|y row|
 relative error < 1e-4 against a dense f32 reference
 (lloom-tensor/tests/moe_routed_metal.rs:148-154, 244-327).
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -216,7 +218,11 @@ def _random_shapes(count, seed=20261202):
     return out
 
 
-@pytest.mark.parametrize("dt,m,n,k", _random_shapes(54))
+# LLOOM_HIP_PARITY_SEEDS=s draws 54 shapes from each of s seeds (default 1)
+_SEEDS = int(os.environ.get("LLOOM_HIP_PARITY_SEEDS", "1"))
+
+
+@pytest.mark.parametrize("dt,m,n,k", [c for i in range(_SEEDS) for c in _random_shapes(54, seed=20261202 + i)])
 def test_random_shapes_all_routes(L, dt, m, n, k):
     """Seeded random shapes through every route against the oracle."""
     rng = np.random.default_rng(m * 131 + n * 7 + k)
@@ -224,6 +230,20 @@ def test_random_shapes_all_routes(L, dt, m, n, k):
     x = rng.standard_normal((m, k)).astype(np.float32)
     y, q = _qmm(L, dt, w, x)
     assert_rows_close(y, O.matmul(dt, x, q, n), what=f"random dt={dt} m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("dt,m", [(O.Q4K, 3), (O.Q4K, 16), (O.Q4K, 17), (O.Q4K, 100), (O.Q6K, 5), (O.Q6K, 16)])
+@pytest.mark.parametrize("n", [15, 16, 17, 6136, 6144, 6152])
+def test_dma_kernel_tile_thresholds(L, dt, m, n):
+    """The DMA kernel at k = 2048 around its tile edges: a partial first
+    tile, exactly one, one row past; and around 384 weight tiles, where a
+    workgroup takes two (6136 = 383.5 tiles, 6144, 6152)."""
+    k = 2048
+    rng = np.random.default_rng(n * 17 + m)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y, q = _qmm(L, dt, w, x)
+    assert_rows_close(y, O.matmul(dt, x, q, n), what=f"tile edges dt={dt} m={m} n={n}")
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 96), (300, 70, 160)])
