@@ -379,6 +379,7 @@ int lloom_hip_ctx_reserve(lloom_hip_ctx* ctx, size_t bytes) {
 
 int lloom_hip_ctx_workspace_bytes(lloom_hip_ctx* ctx, size_t* bytes) {
     if (!ctx || !bytes) return fail(LLOOM_HIP_EINVAL, "ctx_workspace_bytes: null argument");
+    std::lock_guard<std::mutex> lock(ctx->mu);
     *bytes = ctx->ws_bytes;
     return LLOOM_HIP_OK;
 }

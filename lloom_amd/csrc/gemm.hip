@@ -1023,13 +1023,7 @@ template <int MT, int WNW, int WV>
 static hipError_t launch_x16(const void* w, const X16Ptrs& p, float* y, int64_t n, int64_t k, int64_t m,
                              int epi, hipStream_t s) {
     using C = XCfg<MT, WNW, WV>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k_x16<MT, WNW, WV>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (hipError_t e = set_lds_limit((const void*)k_gemm_q4k_x16<MT, WNW, WV>, C::LDS)) return e;
     const unsigned grid = (unsigned)(((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN));
     hipLaunchKernelGGL((k_gemm_q4k_x16<MT, WNW, WV>), dim3(grid), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w,
                        p.x16, p.amin, p.dyt, y, (int)m, (int)n, (int)k, epi);
@@ -1123,13 +1117,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
         }
     }
     if (type == T_Q4K && fits_32bit(n, k, m)) {
-        static bool attr_set = false;
-        if (!attr_set) {
-            hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               G_LDS);
-            if (e != hipSuccess) return e;
-            attr_set = true;
-        }
+        if (hipError_t e = set_lds_limit((const void*)k_gemm_q4k, G_LDS)) return e;
         PrepPtrs p = prep_ptrs(qbuf, m, k);
         const int64_t nb = m * (k / 256);
         hipLaunchKernelGGL(k_gemm_prep_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.xq, p.sp, p.dyt,

@@ -9,9 +9,12 @@
 // as two int8 planes, sc = 8 * s1 + s0 with s0, s1 <= 7: each plane byte is
 // at most 105, and one v_pk_mul_lo_u16 scales four packed nibble bytes with
 // no carry between them.  Two MFMA chains (lo, hi) sum a superblock, I1 =
-// 8 * hi + lo.  The min term is one v_mfma_f32_32x32x16_f16 a tile and
-// superblock: the activation side holds the eight 32-element sums S_j
-// (|S_j| <= 4064, exact in fp16) twice, the weight side -dmin * mn_j split
+// 8 * hi + lo.  The min term is two v_mfma_f32_32x32x16_f16 a tile and
+// superblock: the eight 32-element sums S_j reach |S_j| <= 4064, past the
+// integers fp16 holds exactly (2048), so the activation side holds them as
+// S_j = 64 S_hi + S_lo (S_hi = S >> 6 in [-64, 63], S_lo = S & 63), one
+// MFMA on the eight 64 S_hi twice and one on the eight S_lo twice (both
+// exact in fp16), the weight side -dmin * mn_j split
 // into an fp16 pair hi + lo (dmin * mn_j has at most 17 significant bits, so
 // the pair is exact while it stays below 65504; a wave whose columns hold a
 // dmin >= 1024 scales every dmin of the superblock by the same power of two
@@ -60,11 +63,11 @@ constexpr int BM = 128, BN = 256, WAVES = 8, THREADS = 64 * WAVES, MT = BM / 32,
 //      piece of eight rows touch 32 consecutive dwords (no bank conflict)
 //   W  [256 rows][144 B] the raw Q4_K superblocks (a 36-dword stride: eight
 //      rows reading one piece hit eight bank groups)
-//   S  [128 rows][8] fp16, D [128] f32
+//   S  [128 rows][16] fp16 (64 S_hi[8], S_lo[8]), D [128] f32
 // Every global_load_lds moves 1 KB of contiguous memory (few cache lines:
 // the load issue is the DMA's cost): the activation prep writes x8 in the
 // order the stage holds it, 64 rows at a time, and S and dy superblock-major.
-constexpr int A_BYTES = BM * 256, W_BYTES = BN * 144, S_BYTES = BM * 16, D_BYTES = BM * 4;
+constexpr int A_BYTES = BM * 256, W_BYTES = BN * 144, S_BYTES = BM * 32, D_BYTES = BM * 4;
 constexpr int A_OFF = 0, W_OFF = A_BYTES, S_OFF = W_OFF + W_BYTES, D_OFF = S_OFF + S_BYTES;
 constexpr int STAGE = D_OFF + D_BYTES;
 constexpr int SCR_OFF = STAGES * STAGE;  // per wave: d of its 32 columns
@@ -91,7 +94,8 @@ __device__ __forceinline__ uint32_t byte_pair(uint32_t w, int b) {
 // from_float, k_quants.rs:2400-2438), into
 //   xq  int8 [mp/64][k/256][16 pieces][64 rows][16 B]  x8, piece p of a
 //       superblock = its elements 16p .. 16p+15
-//   s16 fp16 [k/256][mp][8]  S_j = bsums[2j] + bsums[2j + 1]
+//   s16 fp16 [k/256][mp][16]  64 S_hi_j then S_lo_j for S_j = bsums[2j] +
+//       bsums[2j + 1] = 64 S_hi_j + S_lo_j, S_lo_j in [0, 63]
 //   dyt f32  [k/256][mp]
 // with rows m .. mp-1 zero (the GEMM reads whole 128-row tiles).
 struct I8Ptrs {
@@ -104,7 +108,7 @@ static int64_t i8_rows(int64_t m) { return (m + BM - 1) / BM * BM; }
 static I8Ptrs i8_ptrs(void* base, int64_t m, int64_t k) {
     const int64_t mp = i8_rows(m);
     const size_t a = ((size_t)mp * k + 255) & ~(size_t)255;
-    const size_t b = ((size_t)mp * (k / 32) * 2 + 255) & ~(size_t)255;
+    const size_t b = ((size_t)mp * (k / 32) * 4 + 255) & ~(size_t)255;
     I8Ptrs p;
     p.xq = (int8_t*)base;
     p.s16 = (_Float16*)((uint8_t*)base + a);
@@ -115,7 +119,7 @@ static I8Ptrs i8_ptrs(void* base, int64_t m, int64_t k) {
 size_t gemm_i8_workspace_bytes(int64_t m, int64_t k) {
     const int64_t mp = i8_rows(m);
     const size_t a = ((size_t)mp * k + 255) & ~(size_t)255;
-    const size_t b = ((size_t)mp * (k / 32) * 2 + 255) & ~(size_t)255;
+    const size_t b = ((size_t)mp * (k / 32) * 4 + 255) & ~(size_t)255;
     return a + b + (size_t)(k / 256) * mp * sizeof(float) + 256;
 }
 bool gemm_i8_fits(int64_t n, int64_t k, int64_t m) {
@@ -161,7 +165,11 @@ __global__ __launch_bounds__(256) void k_gemm_prep_i8(const float* __restrict__ 
         }
         *(uint4*)(xq + ((((int64_t)(mi >> 6) * nsb + sb) * 16 + j) * 64 + (mi & 63)) * 16) = q;
         const int S = bs + __shfl_xor(bs, 1, 64);  // pieces 2i and 2i + 1: S_i
-        if ((j & 1) == 0) s16[((int64_t)sb * mp + mi) * 8 + (j >> 1)] = (_Float16)(float)S;
+        if ((j & 1) == 0) {
+            _Float16* sr = s16 + ((int64_t)sb * mp + mi) * 16 + (j >> 1);
+            sr[0] = (_Float16)(float)(64 * (S >> 6));  // a multiple of 64 below 2^12 in size: exact
+            sr[8] = (_Float16)(float)(S & 63);
+        }
         if (j == 0) dyt[(int64_t)sb * mp + mi] = d;
     }
 }
@@ -189,8 +197,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
     // 7q + 7, the bytes instruction q + 1 writes there too), so one per-lane
     // offset serves every instruction; the last moves rows 252..255 (36
     // lanes).  In the last column tile rows past n reload row n - 1
-    // (computed, never stored).  S (waves 4, 5) and dy (wave 6, lanes 0..31):
-    // 1 KB / 512 B contiguous.
+    // (computed, never stored).  S (waves 4..7, 1 KB each) and dy (wave 6,
+    // lanes 0..31, 512 B), contiguous.
     const uint32_t lane16 = 16u * (uint32_t)lane;
     const bool ragged_n = n0 + BN > n;  // uniform
     const uint32_t wlane = (uint32_t)(lane / 9) * rowbytes + 16u * (uint32_t)(lane % 9);
@@ -221,8 +229,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
                 }
             }
         }
-        if (wv == 4 || wv == 5)
-            dma16s((const uint8_t*)s16 + ((size_t)sb * mp + m0 + 64 * (wv - 4)) * 16u, lane16,
+        if (wv >= 4)
+            dma16s((const uint8_t*)s16 + ((size_t)sb * mp + m0 + 32 * (wv - 4)) * 32u, lane16,
                    st + S_OFF + 1024u * (uint32_t)(wv - 4));
         if (wv == 6 && lane < 32) dma16s((const uint8_t*)(dyt + (int64_t)sb * mp + m0), lane16, st + D_OFF);
     };
@@ -242,7 +250,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
     const int wrow = 32 * wave + c32;  // the lane's weight column in the tile
     const int la = A_OFF + 2048 * h + 16 * c32;
     const int lw = W_OFF + 144 * wrow + 16 + 16 * h, lh = W_OFF + 144 * wrow;
-    const int ls = S_OFF + 16 * c32, ld = D_OFF + 4 * c32;
+    const int ls = S_OFF + 32 * c32, ld = D_OFF + 4 * c32;
     float* const scr = (float*)(smem + SCR_OFF) + 32 * wave;
 
     issue(0, 0);
@@ -326,7 +334,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
         for (int j = 0; j < 8; j++) bx[j] = *(const v4i*)(smem + sa + 4096 * j);
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-            const v8h sv = *(const v8h*)(smem + ss + 512 * t);
+            const v8h svh = *(const v8h*)(smem + ss + 1024 * t);
+            const v8h svl = *(const v8h*)(smem + ss + 1024 * t + 16);
             const float dy = *(const float*)(smem + sd + 128 * t) * dys;
             v16i lo, hi;
 #pragma unroll
@@ -337,7 +346,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
                 if (t + 1 < MT) bx[j] = *(const v4i*)(smem + sa + (4096 * j + 512 * (t + 1)));
             }
             const v16f zf = {};
-            const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(amin, sv, zf, 0, 0, 0);
+            const v16f dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                amin, svl, __builtin_amdgcn_mfma_f32_32x32x16_f16(amin, svh, zf, 0, 0, 0), 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 const float f = (float)(hi[v] * 8 + lo[v]);
@@ -372,12 +382,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
 
 hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
                           int epi, hipStream_t s) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4k_i8, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (hipError_t e = set_lds_limit((const void*)k_gemm_q4k_i8, LDS)) return e;
     const I8Ptrs p = i8_ptrs(ws, m, k);
     const int64_t nsb = k / 256;
     const int64_t waves2 = p.mp / 4 * (nsb / 2), waves1 = p.mp / 4 * nsb;

@@ -335,13 +335,7 @@ static int64_t q6_tiles(int64_t n, int64_t m) {
 template <class C>
 static hipError_t launch_q6_cfg(const void* w, const Q6Ptrs& p, float* y, int64_t n, int64_t k, int64_t m, int epi,
                                 hipStream_t s, float* psum, int sp) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e =
-            hipFuncSetAttribute((const void*)k_gemm_q6k<C>, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (hipError_t e = set_lds_limit((const void*)k_gemm_q6k<C>, C::LDS)) return e;
     const int64_t tiles = q6_tiles<C>(n, m), nsb = k / 256;
     const int sps = (int)((nsb + sp - 1) / sp);
     hipLaunchKernelGGL(k_gemm_q6k<C>, dim3((unsigned)tiles, sp), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.xq,

@@ -457,13 +457,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_q8_0_splitk(const uint8_t* 
 template <class C>
 static hipError_t launch_q8k_cfg(const void* w, const Q8Ptrs& p, float* y, int64_t n, int64_t k, int64_t m, int epi,
                                  hipStream_t s) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q8_0_splitk<C>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (hipError_t e = set_lds_limit((const void*)k_gemm_q8_0_splitk<C>, C::LDS)) return e;
     const dim3 grid((unsigned)((n + C::BN - 1) / C::BN), (unsigned)((m + C::BM - 1) / C::BM));
     hipLaunchKernelGGL(k_gemm_q8_0_splitk<C>, grid, dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
                        (int)m, (int)n, (int)k, (int)p.mp, epi);
@@ -478,13 +472,7 @@ bool q8_gemm_fits(int64_t n, int64_t k, int64_t m) {
 template <class C>
 static hipError_t launch_q8_cfg(const void* w, const Q8Ptrs& p, float* y, int64_t n, int64_t k, int64_t m, int epi,
                                 hipStream_t s) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q8_0<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           C::LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (hipError_t e = set_lds_limit((const void*)k_gemm_q8_0<C>, C::LDS)) return e;
     const unsigned grid = (unsigned)(((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN));
     hipLaunchKernelGGL(k_gemm_q8_0<C>, dim3(grid), dim3(C::THREADS), C::LDS, s, (const uint8_t*)w, p.xq, p.dxt, y,
                        (int)m, (int)n, (int)k, (int)p.mp, epi);

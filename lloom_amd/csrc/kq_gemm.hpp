@@ -44,4 +44,11 @@ __device__ __forceinline__ void dma4s(const void* base, uint32_t voff, uint32_t 
     asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
+// Raise a kernel's dynamic LDS limit.  Called before every launch: the call
+// is host-only and cheap, it holds for the current device whichever that
+// is, and no process-wide flag is shared between threads.
+inline hipError_t set_lds_limit(const void* kernel, int bytes) {
+    return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
 }  // namespace lloom

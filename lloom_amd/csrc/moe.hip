@@ -18,6 +18,7 @@
 #include "kq_mfma.hpp"
 #include "kq_tasks.hpp"
 #include "kernels.hpp"
+#include "kq_gemm.hpp"
 
 namespace lloom {
 
@@ -897,13 +898,7 @@ static hipError_t moe_mfma_cfg(const void* w, const float* x, float* y, const ui
                                int* sticky, int E, int n, int K, int in_dim1, int topk, int max_slots, int pgmax,
                                const void* w2, float* y2, int mode, bool route, int gw, hipStream_t s) {
     const size_t shm = (size_t)pgmax * moem_plane_bytes(K) + moem_fixed_bytes(4);
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_moe_mfma<DEPTH, GLU>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, MOEM_LDS + moem_fixed_bytes(4));
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (hipError_t e = set_lds_limit((const void*)k_moe_mfma<DEPTH, GLU>, MOEM_LDS + moem_fixed_bytes(4))) return e;
     const int rows_wg = 4 * gw * (GLU ? 16 : 32);
     dim3 grid((n + rows_wg - 1) / rows_wg, route ? max_slots : E + 1, mode == MOE_PAIR ? 2 : 1);
     hipLaunchKernelGGL((k_moe_mfma<DEPTH, GLU>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ids, planes, ws,
@@ -936,13 +931,7 @@ static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, int* ws, 
     constexpr int TPL = 1;
     constexpr int ROWS = 4 * (64 / LPR) * R;
     const size_t shm = (size_t)pgmax * (K + 2 * (K / 16)) * sizeof(float);
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_moe_lds<TYPE, LPR, R, TPL, GLU>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, MOE_LDS);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (hipError_t e = set_lds_limit((const void*)k_moe_lds<TYPE, LPR, R, TPL, GLU>, MOE_LDS)) return e;
     dim3 grid((n + ROWS - 1) / ROWS, o.route ? max_slots : E + 1, o.mode == MOE_PAIR ? 2 : 1);
     hipLaunchKernelGGL((k_moe_lds<TYPE, LPR, R, TPL, GLU>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ws, E,
                        n, K, in_dim1, topk, pgmax, (const uint8_t*)o.w2, o.y2, o.ids, o.planes, o.sticky,

@@ -5,9 +5,10 @@
 //
 // On the host, `scratch` names a stand-in for the device symbol, not a
 // device address: host code never passes it to a kernel or a copy.  The
-// address of each GPU's copy comes from hipGetSymbolAddress, called once
-// per device with that device current, on the entry point's first call
-// there; every later call uses that address.
+// address of each GPU's copy comes from hipGetSymbolAddress, called with
+// that device current on every call (it allocates nothing and is cheap, and
+// a module reloaded after hipDeviceReset may place the array elsewhere); the
+// last address is kept per device for the record.
 //
 // Nothing in the workspace must start at zero: every kernel of the qmatmul
 // routes writes what it later reads.  Calls on one GPU share the array, so
@@ -35,16 +36,14 @@ std::mutex g_scratch_mu;
 int scratch_of(int device, void** out) {
     if (device < 0 || device >= MAX_DEVICES)
         return fail(LLOOM_HIP_EDEVICE, "qmatmul_noalloc: device %d is past the scratch table", device);
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(LLOOM_HIP_EHIP, "qmatmul_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", device,
+                    hipGetErrorString(e));
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[device]) {
-        void* ptr = nullptr;
-        hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !ptr)
-            return fail(LLOOM_HIP_EHIP, "qmatmul_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", device,
-                        hipGetErrorString(e));
-        g_scratch_ptr[device] = ptr;
-    }
-    *out = g_scratch_ptr[device];
+    g_scratch_ptr[device] = ptr;
+    *out = ptr;
     return LLOOM_HIP_OK;
 }
 
@@ -54,16 +53,16 @@ extern "C" int lloom_hip_qmatmul_noalloc(lloom_hip_ctx* ctx, int ggml_type, cons
                                          const void* x_dev, int x_dtype, int64_t m, void* y_dev, int y_dtype,
                                          void* stream) {
     if (int rc = qmatmul_check(ctx, ggml_type, w_dev, n, k, x_dev, x_dtype, m, y_dev, y_dtype, EPI_STORE)) return rc;
+    HIP_OK(hipSetDevice(ctx->device));
+    void* ws = nullptr;
+    if (int rc = scratch_of(ctx->device, &ws)) return rc;
+    std::lock_guard<std::mutex> lock(ctx->mu);
     const QmmPlan p = qmm_plan(ctx->mv_rows_max, ctx->prefill_mma, ggml_type, n, k, m, x_dtype, y_dtype);
     if (p.total > SCRATCH_BYTES)
         return fail(LLOOM_HIP_ENOMEM,
                     "qmatmul_noalloc: the call needs %zu bytes of workspace and the static scratch holds %zu "
                     "(use lloom_hip_qmatmul, or fewer rows a call)",
                     p.total, SCRATCH_BYTES);
-    HIP_OK(hipSetDevice(ctx->device));
-    void* ws = nullptr;
-    if (int rc = scratch_of(ctx->device, &ws)) return rc;
-    std::lock_guard<std::mutex> lock(ctx->mu);
     return qmatmul_run(ctx, ggml_type, w_dev, n, k, x_dev, x_dtype, m, y_dev, y_dtype, EPI_STORE, (hipStream_t)stream,
                        p, ws, SCRATCH_BYTES);
 }

@@ -198,6 +198,45 @@ def test_prefill_q4k_few_rows_long_k(L, m, mma):
     assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"few rows long k {mma} m={m}")
 
 
+def _same_sign_inputs(kind, m, k, rng):
+    """Activations whose Q8_K sub-block sums reach the top of their range
+    (|S_j| up to 32 * 127 = 4064, past the integers fp16 holds exactly)."""
+    if kind == "bias":
+        return (1.0 + 0.05 * rng.standard_normal((m, k))).astype(np.float32)
+    if kind == "negbias":
+        return (-1.0 + 0.05 * rng.standard_normal((m, k))).astype(np.float32)
+    if kind == "ones":
+        return np.ones((m, k), np.float32)
+    # one huge outlier per 256-element block over a positive background
+    x = (0.5 + 0.1 * rng.random((m, k))).astype(np.float32)
+    x[:, 17::256] = 900.0
+    x[:, 200::256] = -1000.0
+    return x
+
+
+@pytest.mark.parametrize("dt,mma", [(O.Q4K, "f16"), (O.Q4K, "int8"), (O.Q4K, "auto"), (O.Q8_0, "auto"),
+                                    (O.Q6K, "auto")])
+@pytest.mark.parametrize("m", [17, 128, 600, 2048])
+@pytest.mark.parametrize("kind", ["bias", "negbias", "ones", "outlier"])
+def test_prefill_same_sign_activations(L, dt, mma, m, kind):
+    """Every prefill route on activations whose sub-block sums are large and
+    odd (a positive or negative bias), constant, or dominated by an outlier
+    per block, against the oracle.  Zero-mean inputs never push the Q8_K
+    sums past 2048, where an fp16 copy of them would round."""
+    from lloom_amd.quantized import MMA_AUTO, MMA_F16, MMA_INT8, set_prefill_mma
+
+    n, k = (72 if m >= 600 else 200), 2048
+    rng = np.random.default_rng(m * 13 + len(kind))
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = _same_sign_inputs(kind, m, k, rng)
+    set_prefill_mma({"f16": MMA_F16, "int8": MMA_INT8, "auto": MMA_AUTO}[mma])
+    try:
+        y, q = _qmm(L, dt, w, x)
+    finally:
+        set_prefill_mma(MMA_AUTO)
+    assert_rows_close(y, O.matmul(dt, x, q, n), what=f"same-sign {kind} dt={dt} {mma} m={m}")
+
+
 def _random_shapes(count, seed=20261202):
     """(dt, m, n, k) drawn across every routing band: m from each of
     1-2, 3-4, 5-16, 17-64, 65-128 and 129-600 rows; k in whole blocks up to
