@@ -1014,7 +1014,7 @@ size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode)
     if (type == T_Q6K && m >= q6_min_rows() && q6_gemm_fits(n, k, m)) return q6_gemm_workspace_bytes(n, k, m);
     if (use_mq(type, m)) return split_q8k_bytes(k, m);
     if (type == T_Q8_0 && q8_gemm_fits(n, k, m)) return q8_gemm_workspace_bytes(m, k);
-    if (type == T_Q4K && mode == GEMM_INT8 && gemm_i8_fits(n, k, m)) return gemm_i8_workspace_bytes(m, k);
+    if (type == T_Q4K && mode == GEMM_INT8 && gemm_i8_fits(n, k, m)) return gemm_i8_workspace_bytes(n, m, k);
     if (type == T_Q4K && fits_32bit(0, k, m)) return mode == GEMM_INT8 ? prep_bytes(m, k) : x16_bytes(m, k);
     return matvec_workspace_bytes(type, n, k, 16);
 }

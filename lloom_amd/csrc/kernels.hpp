@@ -71,9 +71,10 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                        void* qbuf, size_t ws_cap, int mode, int epi, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m, int mode);
 // gemm_i8.hip: Q4_K prefill on int8 MFMA (two scale planes, f16-MFMA min
-// term), 128 x 256 tiles; its activation prep runs in the same call.
+// term), 128 x 256 tiles; its activation and weight-record prep (one
+// launch) runs in the same call.
 bool gemm_i8_fits(int64_t n, int64_t k, int64_t m);
-size_t gemm_i8_workspace_bytes(int64_t m, int64_t k);
+size_t gemm_i8_workspace_bytes(int64_t n, int64_t m, int64_t k);
 hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
                           int epi, hipStream_t s);
 // gemm_q6.hip: Q6_K from Q6_GEMM_MIN_ROWS rows (below, k_mv_mfma with 64
