@@ -169,3 +169,90 @@ def test_patch_calls_match_the_binding():
         assert must in seen, must
     for const in re.findall(r"sys::(LLOOM_HIP_\w+)", added):
         assert const in crate_constants(), const
+
+
+# ------------------------------------------------ the lloom-tensor patch ---
+
+REFERENCE_TENSOR = "/root/reference/lloom-tensor"
+PATCH = os.path.join(ROOT, "rust", "patches", "lloom-tensor-hip.patch")
+
+
+def _rust_arms():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("rust_arms", os.path.join(ROOT, "rust", "patches", "rust_arms.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_rust_arms_parser_on_known_matches():
+    """The match scanner on small Rust snippets: a match over Storage with a
+    Metal arm and no catch-all is reported until it has a Hip arm; a
+    catch-all, an unrelated enum or a `matches!` needs none; a refusal arm
+    binds nothing and names the function."""
+    R = _rust_arms()
+    src = '''
+impl Storage {
+    pub fn dtype(&self) -> DType {
+        match self {
+            Self::Cpu(s) => s.dtype(),
+            Self::Cuda(s) => s.dtype(),
+            Self::Metal(s) => s.dtype(),
+        }
+    }
+    pub fn affine(&self, layout: &Layout, mul: f64) -> Result<Self> {
+        match self {
+            Self::Cpu(s) => Ok(Self::Cpu(s.affine(layout, mul)?)),
+            Self::Cuda(s) => { let s = s.affine(layout, mul)?; Ok(Self::Cuda(s)) }
+            Self::Metal(s) => { let s = s.affine(layout, mul)?; Ok(Self::Metal(s)) }
+        }
+    }
+    fn pair(&self, rhs: &Self) -> bool {
+        match (self, rhs) {
+            (Self::Metal(a), Self::Metal(b)) => a.same(b),
+            (lhs, rhs) => false,
+        }
+    }
+}
+fn other(b: Backend) -> u32 { match b { Backend::Metal => 1, Backend::Cuda => 2 } }
+fn is_metal(d: &Device) -> bool { matches!(d, Device::Metal(_)) }
+'''
+    bad = R.check(src)
+    assert len(bad) == 2 and all("fn dtype" in b or "fn affine" in b for b in bad), bad
+    out, n = R.add_hip_arms(src, "src/storage.rs")
+    assert n == 2 and R.check(out) == []
+    assert 'Self::Hip(_) => crate::bail!("affine is not supported on a hip Storage")' in out
+    assert "Self::Hip(s) => s.dtype()" in out  # served: dtype is an accessor
+    assert out.count('#[cfg(feature = "hip")]') == 2
+
+
+def test_patch_gives_every_device_match_a_hip_arm(tmp_path):
+    """The lloom-tensor patch applied to a copy of the reference crate: the
+    Hip variants exist and every match over Device, DeviceLocation, Storage
+    or QStorage that names Metal has a Hip arm or a catch-all (what the
+    `hip` feature needs to compile past them)."""
+    import shutil
+    import subprocess
+
+    import pytest
+
+    if not os.path.isdir(REFERENCE_TENSOR):
+        pytest.skip("the reference checkout is not present")
+    dst = tmp_path / "lloom-tensor"
+    shutil.copytree(REFERENCE_TENSOR, dst, ignore=shutil.ignore_patterns("target"))
+    r = subprocess.run(["patch", "-p1", "-s", "-i", PATCH], cwd=tmp_path, capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    src = dst / "src"
+    dev = (src / "device.rs").read_text()
+    assert re.search(r'#\[cfg\(feature = "hip"\)\]\s*Hip\(crate::HipDevice\)', dev)
+    assert re.search(r'#\[cfg\(feature = "hip"\)\]\s*Hip \{ gpu_id: usize \}', dev)
+    assert re.search(r'#\[cfg\(feature = "hip"\)\]\s*Hip\(', (src / "storage.rs").read_text())
+    assert re.search(r'#\[cfg\(feature = "hip"\)\]\s*Hip\(', (src / "quantized" / "mod.rs").read_text())
+    R = _rust_arms()
+    missing = []
+    for path in R.rust_files(str(dst)):
+        text = open(path, encoding="utf-8").read()
+        if "Metal" in text:
+            missing += ["{}: {}".format(os.path.relpath(path, dst), b) for b in R.check(text)]
+    assert not missing, "matches without a Hip arm:\n" + "\n".join(missing)
