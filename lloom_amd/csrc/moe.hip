@@ -377,6 +377,10 @@ __device__ __forceinline__ float group_sum(float v) {
 constexpr int MOE_PG = 8;          // planes staged per pass
 constexpr int MOE_FUSE_MAX = 1024;  // planes routed inside k_moe_lds (an LDS list per workgroup)
 constexpr int MOE_LDS = 72 * 1024;  // bytes of staged planes and run sums
+// Floats of a staged plane: element e at e + 4 (e / 64) + 16 (e / 256), then
+// the K / 16 run sums come after all the planes.
+__host__ __device__ constexpr int moe_plane_floats(int K) { return K + K / 8; }
+__host__ __device__ inline int moe_plane_idx(int e) { return e + 4 * (e >> 6) + 16 * (e >> 8); }
 
 // One workgroup (4 waves) per (block of rows, active-expert slot).  In a
 // wave, 64 / LPR groups of LPR lanes each own R consecutive rows and walk
@@ -449,11 +453,12 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
         list = sorted + start[e];
     }
     // [pgmax][KP] planes, then [pgmax][K / 16] run sums.  A plane stores
-    // element e at e + 4 (e / 64): the eight tasks of a superblock read
-    // 16-byte pieces 16 or 48 elements apart, which this spreads over
-    // distinct banks.
+    // element e at e + 4 (e / 64) + 16 (e / 256): the eight tasks of a
+    // superblock (16 lanes: two superblocks) read 16-byte pieces that this
+    // spreads over distinct banks, the second superblock's 32 banks from the
+    // first's.
     extern __shared__ __align__(16) float xs[];
-    const int KP = K + K / 16;
+    const int KP = moe_plane_floats(K);
     float* sx = xs + pgmax * KP;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane / LPR, tl = lane % LPR;
@@ -500,7 +505,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
             float4 v[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) v[u] = xr[u];
-            float4* dst = (float4*)(xs + q * KP + 16 * c + 4 * (c >> 2));
+            float4* dst = (float4*)(xs + q * KP + moe_plane_idx(16 * c));
             float sum = 0.0f;
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -538,7 +543,7 @@ __global__ __launch_bounds__(256) void k_moe_lds(const uint8_t* __restrict__ W, 
                                 for (int r = 0; r < RR; r++) dq[r] = 0.0f;
 #pragma unroll
                                 for (int i4 = 0; i4 < 4; i4++) {
-                                    const float4 xv = *(const float4*)(xq + off[u] + 4 * (off[u] >> 6) + 4 * i4);
+                                    const float4 xv = *(const float4*)(xq + moe_plane_idx(off[u]) + 4 * i4);
 #pragma unroll
                                     for (int r = 0; r < RR; r++) {
                                         dq[r] = __builtin_fmaf(qv[r][u][4 * i4], xv.x, dq[r]);
@@ -930,7 +935,7 @@ static hipError_t moe_lds_cfg(const void* w, const float* x, float* y, int* ws, 
     // for two tasks unpipelined and 46.5 for four)
     constexpr int TPL = 1;
     constexpr int ROWS = 4 * (64 / LPR) * R;
-    const size_t shm = (size_t)pgmax * (K + 2 * (K / 16)) * sizeof(float);
+    const size_t shm = (size_t)pgmax * (moe_plane_floats(K) + K / 16) * sizeof(float);
     if (hipError_t e = set_lds_limit((const void*)k_moe_lds<TYPE, LPR, R, TPL, GLU>, MOE_LDS)) return e;
     dim3 grid((n + ROWS - 1) / ROWS, o.route ? max_slots : E + 1, o.mode == MOE_PAIR ? 2 : 1);
     hipLaunchKernelGGL((k_moe_lds<TYPE, LPR, R, TPL, GLU>), grid, dim3(256), shm, s, (const uint8_t*)w, x, y, ws, E,
@@ -990,7 +995,7 @@ size_t moe_workspace_bytes(int64_t n_experts, int64_t planes, int64_t n, int64_t
 }
 
 bool moe_stages(int64_t k) {
-    const int64_t per_plane = (k + 2 * (k / 16)) * (int64_t)sizeof(float);
+    const int64_t per_plane = (moe_plane_floats((int)k) + k / 16) * (int64_t)sizeof(float);
     return MOE_LDS / per_plane >= 1 && (k & 15) == 0;
 }
 
@@ -1009,7 +1014,7 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
         if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     int max_slots = (int)(E < planes ? E : planes);
-    const int64_t per_plane = (k + 2 * (k / 16)) * (int64_t)sizeof(float);
+    const int64_t per_plane = (moe_plane_floats((int)k) + k / 16) * (int64_t)sizeof(float);
     int pgmax = MOE_LDS / per_plane < MOE_PG ? (int)(MOE_LDS / per_plane) : MOE_PG;
     // a decode-like routing (at most four planes per active expert on
     // average) stages four planes at a time: half the LDS, so more
