@@ -94,6 +94,22 @@ def moe_ids(L, np, T, E, topk):
     return np.argsort(-p, axis=1, kind="stable")[:, :topk].astype(np.int32)
 
 
+def csrc_digest():
+    """sha256 of the kernel sources (lloom_amd/csrc, sorted by name): the
+    committed traffic profiles record the digest of the build they measured,
+    so a profile taken on other kernels is reported as stale, not quoted."""
+    import hashlib
+
+    h = hashlib.sha256()
+    d = os.path.join(ROOT, "lloom_amd", "csrc")
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".hip", ".hpp", ".cpp", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(d, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def copies_for(packed_bytes):
     return max(2, math.ceil(ROTATE_BYTES / packed_bytes))
 
@@ -243,19 +259,29 @@ def main():
     # time, from the per-B graphs above (events on the replay stream).
     # traffic: measured HBM bytes per call, from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE calibration when present.
+    digest = csrc_digest()
+
     def traffic_of(b):
+        """(HBM bytes per launch, or None; a note when the profile is of
+        other kernel sources than these)."""
         tpath = os.path.join(ROOT, "profiles", "traffic_c2_b%d.json" % b)
         if not os.path.exists(tpath):
-            return None
+            return None, "no profile"
         with open(tpath) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+            prof = json.load(f)
+        if prof.get("csrc_digest") != digest:
+            return None, "stale: %s measured kernel sources %s (commit %s), these are %s" % (
+                os.path.basename(tpath), prof.get("csrc_digest"), prof.get("commit"), digest)
+        return prof.get("hbm_bytes_per_launch"), "profiles/%s (commit %s)" % (os.path.basename(tpath),
+                                                                            prof.get("commit"))
 
     def roof(b, kernel):
         t = per_b[str(b)]["us"] * 1e-6
         ach = algo[b] / t / 1e9
+        traffic, tnote = traffic_of(b)
         return {"bound": "hbm", "kernel": kernel, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "algorithmic_bytes": algo[b],
-                "us_per_launch": per_b[str(b)]["us"], "traffic": traffic_of(b)}
+                "us_per_launch": per_b[str(b)]["us"], "traffic": traffic, "traffic_source": tnote}
 
     roofline = roof(1, "k_matvec<Q4_K, 1 row> (C2, B=1)")
     roofline["also"] = [roof(b, "k_quantize_split_q8k + k_mv_dma_ma<8 superblocks, 2 weight tiles, 1 activation "
@@ -487,7 +513,9 @@ def cpu_baseline(L, qt, xs, n, k, Bs, algo, budget_s):
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(threads), "kind": "port",
             "sample": f"C2 sweep B in {{1,2,4,8,16}} x {iters} iterations ({el:.1f} s), same Q4_K bytes, "
                       f"restatement of lloom-tensor CPU QMatMul (AVX2, barrier pool); "
-                      f"physical cores {phys}, nproc {os.cpu_count()}, {cpu_model}"}
+                      f"physical cores {phys}, nproc {os.cpu_count()}, {cpu_model}; one 7 MB weight "
+                      f"replayed, so it stays resident in the host caches (the GPU figure streams 512 MB "
+                      f"of rotating copies from HBM)"}
 
 
 if __name__ == "__main__":
