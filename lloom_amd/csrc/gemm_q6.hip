@@ -22,6 +22,8 @@
 
 namespace lloom {
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
 // Activation prep (Q8_K of every (row, superblock), bit-exact):
 //   xq  int8 [m][k]
 //   dyt f32  [k/256][mp]   mp = m rounded up to 4, then 128 floats of pad
@@ -31,35 +33,46 @@ struct Q6Ptrs {
     int64_t mp;
 };
 
-static Q6Ptrs q6_ptrs(void* base, int64_t m, int64_t k) {
+// (xq_rows >= m: rows of xq allocated, the two-plane route's tiles read
+// whole 256-row blocks)
+static Q6Ptrs q6_ptrs(void* base, int64_t m, int64_t k, int64_t xq_rows = 0) {
     Q6Ptrs p;
     p.xq = (int8_t*)base;
-    p.dyt = (float*)((uint8_t*)base + (((size_t)m * k + 255) & ~(size_t)255));
+    p.dyt = (float*)((uint8_t*)base + (((size_t)(xq_rows > m ? xq_rows : m) * k + 255) & ~(size_t)255));
     p.mp = (m + 3) & ~(int64_t)3;
     return p;
 }
 
-static size_t q6_prep_bytes(int64_t m, int64_t k) {
+static size_t q6_prep_bytes(int64_t m, int64_t k, int64_t xq_rows = 0) {
     const int64_t mp = (m + 3) & ~(int64_t)3;
-    return (((size_t)m * k + 255) & ~(size_t)255) + (((size_t)(k / 256) * mp + 128) * sizeof(float) + 255 & ~(size_t)255);
+    return (((size_t)(xq_rows > m ? xq_rows : m) * k + 255) & ~(size_t)255) + (((size_t)(k / 256) * mp + 128) * sizeof(float) + 255 & ~(size_t)255);
 }
 
 
-// One wave a (row, superblock).
+// One wave four consecutive (row, superblock) blocks (x is [m][k], so
+// they are 4 KB of contiguous input), all four loads issued first.
+constexpr int Q6_PREP_BLOCKS = 16;  // a workgroup's blocks
 __global__ __launch_bounds__(256) void k_gemm_prep_q6(const float* __restrict__ x, int8_t* __restrict__ xq,
                                                       float* __restrict__ dyt, int m, int k, int mp) {
     const int lane = threadIdx.x & 63;
     const int nsb = k >> 8;
-    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (blk >= (int64_t)m * nsb) return;
-    const int mi = (int)(blk / nsb), sb = (int)(blk - (int64_t)mi * nsb);
-    const int64_t off = (int64_t)mi * k + 256 * sb + 4 * lane;
-    const float4 v = *(const float4*)(x + off);
-    float d;
-    int bs;
-    const uint32_t q = q8k_block_wave(v, &d, &bs);
-    *(uint32_t*)(xq + off) = q;
-    if (lane == 0) dyt[(int64_t)sb * mp + mi] = d;
+    const int64_t nblk = (int64_t)m * nsb;
+    const int64_t blk0 = (int64_t)blockIdx.x * Q6_PREP_BLOCKS + 4 * (threadIdx.x >> 6);
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        v[j] = blk0 + j < nblk ? *(const float4*)(x + (blk0 + j) * 256 + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int64_t blk = blk0 + j;
+        if (blk >= nblk) return;
+        float d;
+        int bs;
+        const uint32_t q = q8k_block_wave(v[j], &d, &bs);
+        *(uint32_t*)(xq + blk * 256 + 4 * lane) = q;
+        const int mi = (int)(blk / nsb), sb = (int)(blk - (int64_t)mi * nsb);
+        if (lane == 0) dyt[(int64_t)sb * mp + mi] = d;
+    }
 }
 
 // Tiling: WM x WN waves, each MT x NT tiles of 32 x 32 (BM = 32 WM MT, BN =
@@ -319,6 +332,297 @@ __global__ __launch_bounds__(256) void k_q6_sum_splits(const float* __restrict__
     store_epi(&Y[i], v, epi);
 }
 
+// ------------------------------------------------ two-plane route ----
+// From a few hundred rows the per-sub-block VALU work above (the scale
+// multiply-add on every output, the per-lane weight realignment) bounds
+// k_gemm_q6k.  Here a prep launch folds each weight's scale into it once a
+// call: v = sc[e / 16] * (q6[e] - 32) lies in [-4096, 4096] and splits
+// exactly as v = 64 hi + lo with lo in [-32, 31] and hi in [-64, 64], two
+// int8 planes.  Then every superblock of every 32 x 32 tile is sixteen
+// chained v_mfma_i32_32x32x32_i8 (eight 32-element chunks, two planes)
+// whose sums are exact (|64 Dhi + Dlo| <= 256 * 128 * 4096 = 2^27), and the
+// VALU work is four instructions an output and superblock: 64 hi + lo,
+// convert, d * dy, fma.  The integer sum is the reference's per-superblock
+// isum (sum_j sc_j sum_{k in j} x8 (q6 - 32)), the float part its
+// d_x * d_w scaling (k_quants.rs:2115-2172).
+//
+// Weight prep (per call, into the workspace):
+//   planes int8 [n][k/256][4][2][64]: superblock sb of column c is 512
+//          bytes, quarter q (elements 64 q ..) at 128 q: hi plane then lo
+//   dwt    f32 [k/256][np]  f32(d), np = n rounded up to 4, 128 floats of pad
+struct Q6PPtrs {
+    int8_t* planes;
+    float* dwt;
+    int64_t np;
+};
+
+// (columns rounded up to whole 128-column blocks, read by the last block)
+static size_t q6p_plane_bytes(int64_t n, int64_t k) { return (size_t)((n + 127) & ~(int64_t)127) * 2 * k; }
+static size_t q6p_dw_bytes(int64_t n, int64_t k) {
+    const int64_t np = (n + 3) & ~(int64_t)3;
+    return (((size_t)(k / 256) * np + 128) * sizeof(float) + 255) & ~(size_t)255;
+}
+static Q6PPtrs q6p_ptrs(void* base, int64_t n, int64_t k) {
+    Q6PPtrs p;
+    p.planes = (int8_t*)base;
+    p.dwt = (float*)((uint8_t*)base + q6p_plane_bytes(n, k));
+    p.np = (n + 3) & ~(int64_t)3;
+    return p;
+}
+
+// One wave four consecutive (column, superblock) blocks: W is [n][k/256]
+// blocks, so they are 840 contiguous bytes (2-byte aligned), which come in
+// as the 212 dwords around them (four loads a lane, all issued first)
+// through LDS; then each lane makes four elements of each block (4 l ..
+// 4 l + 3 share their scale and bit positions).
+__global__ __launch_bounds__(256) void k_q6_planes(const uint8_t* __restrict__ W, int8_t* __restrict__ planes,
+                                                   float* __restrict__ dwt, int n, int k, int np) {
+    __shared__ uint32_t raw[4][4 * 64];
+    const int lane = threadIdx.x & 63, wq = threadIdx.x >> 6;
+    const int nsb = k >> 8;
+    const int64_t nblk = (int64_t)n * nsb;
+    const int64_t blk0 = (int64_t)blockIdx.x * Q6_PREP_BLOCKS + 4 * wq;
+    const int64_t first = blk0 < nblk ? blk0 * Q6K_BYTES : 0;
+    const uint32_t* src = (const uint32_t*)(W + (first & ~(int64_t)3));
+    const int sh = (int)(first & 3);  // 0 or 2
+    // (W's last block may end 2 bytes into its last dword)
+    const int64_t left = ((nblk * Q6K_BYTES + 3) >> 2) - (first >> 2);
+    uint32_t wd[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) wd[j] = 64 * j + lane < min(left, (int64_t)212) ? src[64 * j + lane] : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; j++) raw[wq][64 * j + lane] = wd[j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int64_t blk = blk0 + j;
+        if (blk >= nblk) return;
+        const uint8_t* b = (const uint8_t*)raw[wq] + sh + j * Q6K_BYTES;
+        const int c = (int)(blk / nsb), sb = (int)(blk - (int64_t)c * nsb);
+        const int e0 = 4 * lane, hh = e0 >> 7, r = e0 & 127, g = r >> 5, l = r & 31;
+        const int sc = (int)(int8_t)b[Q6K_SC + (e0 >> 4)];
+        uint32_t hi4 = 0, lo4 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int qlo = (b[64 * hh + 32 * (g & 1) + l + i] >> (4 * (g >> 1))) & 15;
+            const int qhi = (b[Q6K_QH + 32 * hh + l + i] >> (2 * g)) & 3;
+            const int v = sc * ((qlo | (qhi << 4)) - 32);
+            const int lo = ((v + 32) & 63) - 32;
+            const int hi = (v - lo) >> 6;
+            lo4 |= (uint32_t)(lo & 255) << (8 * i);
+            hi4 |= (uint32_t)(hi & 255) << (8 * i);
+        }
+        int8_t* o = planes + (int64_t)c * 2 * k + 512 * sb + 128 * (e0 >> 6) + (e0 & 63);
+        *(uint32_t*)o = hi4;
+        *(uint32_t*)(o + 64) = lo4;
+        if (lane == 0) dwt[(int64_t)sb * np + c] = f16_to_f32(*(const uint16_t*)(b + Q6K_D));
+    }
+}
+
+// Tiling: 4 x 2 waves of 64 x 64 (2 x 2 tiles of 32 x 32): a 256 x 128
+// block of y.  K moves a quarter superblock (64) a stage through a ring of
+// four, three in flight, every byte by global_load_lds:
+//   A   [256][64] int8: row r's 16-byte piece p at p ^ (((r >> 1) ^ (r >> 3)) & 3)
+//   B   [128][128] the column's hi then lo plane: piece p at p ^ (c & 7) ^ ((c >> 3) & 1)
+//   DY  [256] f32, DW [128] f32 (a superblock's scales, in every stage; the
+//       four stages' scales sit together at the start of LDS)
+// The swizzles put the lanes of one ds_read_b128 on distinct 16-byte bank
+// groups (both for 8 and for 16 lanes a pass), and neither key changes
+// 32 rows or columns on, so a lane's second tile is an immediate offset.  Every wave issues 5 loads a
+// stage (A 2, B 2, one scale chunk: wave 0 DY, the others DW, the same
+// bytes to the same place), so a counted vmcnt wait leaves exactly the two
+// later stages in flight.
+// MFMA operands: lane l holds row (column) l % 32, elements 16 (l / 32) ..
+// +15 of the 32-element chunk; the result's lane l holds column l % 32 and
+// rows 8 (i / 4) + 4 (l / 32) + i % 4.
+struct Q6P {
+    static constexpr int WM = 4, WN = 2, WAVES = 8, THREADS = 512, BM = 256, BN = 128, S = 4;
+    // LDS: the four scale slots first (so a slot's scales are an immediate
+    // offset from one address), then the four A + B slots
+    static constexpr int A = BM * 64, B = BN * 128, SC = 2048, STAGE = A + B, AB0 = S * SC, LDS = AB0 + S * STAGE;
+    static constexpr int A_PER_WAVE = A / 1024 / WAVES, B_PER_WAVE = B / 1024 / WAVES;
+    static constexpr int DMA = A_PER_WAVE + B_PER_WAVE + 1;
+    static_assert(LDS <= 160 * 1024, "LDS");
+    static_assert((S - 2) * DMA <= 63, "vmcnt counts to 63");
+};
+
+__device__ __forceinline__ int q6p_akey(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+__device__ __forceinline__ int q6p_bkey(int col) { return (col & 7) ^ ((col >> 3) & 1); }
+
+__global__ __launch_bounds__(Q6P::THREADS) void k_gemm_q6p(const int8_t* __restrict__ P, const float* __restrict__ dwt,
+                                                          const int8_t* __restrict__ xq,
+                                                          const float* __restrict__ dyt, float* __restrict__ Y, int m,
+                                                          int n, int k, int mp, int np, int epi, int sps,
+                                                          float* __restrict__ psum) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave / Q6P::WN, wn = wave % Q6P::WN;
+    const int h = lane >> 5, c32 = lane & 31;
+    int bm, bn;
+    tile_of((m + Q6P::BM - 1) / Q6P::BM, (n + Q6P::BN - 1) / Q6P::BN, bm, bn);
+    const int m0 = bm * Q6P::BM, n0 = bn * Q6P::BN;
+    const int nsb = k >> 8;
+    const int s0 = blockIdx.y * sps, nst = 4 * min(sps, nsb - s0);  // quarter superblocks
+
+    // chunk q (1 KB) of A is rows 16 q .., of B columns 8 q ..; wave w loads
+    // chunks w and w + 8, so a lane's swizzled piece is the same in both and
+    // they differ by a uniform offset (128 rows, 64 columns).  Rows and
+    // columns of the last block past m and n read the padding of xq and the
+    // planes: their sums land in rows and columns that are not stored.
+    const int arow0 = 16 * wave + (lane >> 2), bcol0 = 8 * wave + (lane >> 3);
+    const uint32_t aoff = (uint32_t)(m0 + arow0) * (uint32_t)k + 16u * ((lane & 3) ^ q6p_akey(arow0));
+    const uint32_t boff = (uint32_t)(n0 + bcol0) * (uint32_t)(2 * k) + 16u * ((lane & 7) ^ q6p_bkey(bcol0));
+    // wave 0: 64 lanes x 4 activation scales; the others: 32 lanes x 4
+    // weight scales (lanes 32.. repeat lane 31's into the chunk's upper
+    // half), clamped into the padded rows
+    const uint32_t scoff = wave == 0 ? (uint32_t)min(m0 + 4 * lane, mp - 4) * 4u
+                                     : (uint32_t)min(n0 + 4 * min(lane, 31), np - 4) * 4u;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds0 = lds_addr(smem);
+
+    auto issue = [&](int i, int slot) {
+        const int s = s0 + (i >> 2), qq = i & 3;
+        const uint32_t st = lds0 + Q6P::AB0 + slot * Q6P::STAGE, sc = lds0 + slot * Q6P::SC;
+        const int8_t* ab = xq + (uint32_t)s * 256u + 64u * qq;
+#pragma unroll
+        for (int j = 0; j < Q6P::A_PER_WAVE; j++)
+            dma16s(ab + (uint32_t)(128 * j) * (uint32_t)k, aoff, st + 1024 * (wv + Q6P::WAVES * j));
+        const int8_t* bb = P + (uint32_t)s * 512u + 128u * qq;
+#pragma unroll
+        for (int j = 0; j < Q6P::B_PER_WAVE; j++)
+            dma16s(bb + (uint32_t)(64 * j) * (uint32_t)(2 * k), boff, st + Q6P::A + 1024 * (wv + Q6P::WAVES * j));
+        // the scales of the superblock stage i - 1 belongs to (see below)
+        const int ss = s0 + (max(i - 1, 0) >> 2);
+        if (wv == 0) dma16s(dyt + (int64_t)ss * mp, scoff, sc);
+        else dma16s(dwt + (int64_t)ss * np, scoff, sc + 1024);
+    };
+
+    float out[2][2][16];
+    v16i hi[2][2], lo[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) out[a][b][r] = 0.0f;
+    // this lane's operand addresses in a stage, per chunk c of the quarter:
+    // A rows r0 and r0 + 32, B columns c0 and c0 + 32 (hi and lo planes)
+    const int r0 = wm * 64 + c32, c0 = wn * 64 + c32;
+    int aad[2], bhad[2], blad[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        aad[c] = r0 * 64 + 16 * ((2 * c + h) ^ q6p_akey(r0));
+        bhad[c] = Q6P::A + c0 * 128 + 16 * ((2 * c + h) ^ q6p_bkey(c0));
+        blad[c] = Q6P::A + c0 * 128 + 16 * ((4 + 2 * c + h) ^ q6p_bkey(c0));
+    }
+
+    // quarter Q of a superblock, from slot Q of the ring
+    auto quarter = [&](auto qc) {
+        constexpr int Q = decltype(qc)::value;
+        const uint8_t* st = smem + Q6P::AB0 + Q * Q6P::STAGE;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            v4i av[2], bh[2], bl[2];
+#pragma unroll
+            for (int a = 0; a < 2; a++) av[a] = *(const v4i*)(st + aad[c] + 32 * 64 * a);
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                bh[b] = *(const v4i*)(st + bhad[c] + 32 * 128 * b);
+                bl[b] = *(const v4i*)(st + blad[c] + 32 * 128 * b);
+            }
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    const v16i z = {};
+                    hi[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bh[b], (Q == 0 && c == 0) ? z : hi[a][b], 0, 0, 0);
+                    lo[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bl[b], (Q == 0 && c == 0) ? z : lo[a][b], 0, 0, 0);
+                }
+        }
+    };
+    // a finished superblock: out += f32(64 hi + lo) * (d * dy), its scales
+    // from the stage in `slot`
+    auto epilogue = [&](int slot) {
+        {
+            const float* DY = (const float*)(smem + slot * Q6P::SC);
+            const float* DW = DY + 256;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const float dw = DW[wn * 64 + b * 32 + c32];
+#pragma unroll
+                for (int a = 0; a < 2; a++) {
+                    const float* dyp = DY + wm * 64 + a * 32 + 4 * h;
+#pragma unroll
+                    for (int gq = 0; gq < 4; gq++) {
+                        const float4 d4 = *(const float4*)(dyp + 8 * gq);
+                        const float dys[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const int r = 4 * gq + u;
+                            const int v = hi[a][b][r] * 64 + lo[a][b][r];
+                            out[a][b][r] = __builtin_fmaf((float)v, dw * dys[u], out[a][b][r]);
+                        }
+                    }
+                }
+            }
+        }
+    };
+    // stage i + 3 goes into the slot stage i - 1 used (its readers passed
+    // the last barrier); past the end it reloads the last stage into a slot
+    // nobody reads, so the counts never change.  The two waves of a SIMD
+    // (w and w + 4) take their superblock epilogues a quarter apart, so one
+    // runs its VALU work under the other's MFMAs: waves 0-3 after quarter 3,
+    // waves 4-7 before quarter 0 of the next superblock (and after the
+    // loop).  A stage carries the scales of the superblock of the stage
+    // before it, which is the finished one at both points.
+    const bool grpB = wave >= 4;
+    auto step = [&](int i, auto qc) {
+        constexpr int Q = decltype(qc)::value;
+        issue(min(i + 3, nst - 1), (Q + 3) & 3);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (Q == 0) {
+            if (grpB && i > 0) epilogue(0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        quarter(qc);
+        if constexpr (Q == 3) {
+            if (!grpB) epilogue(3);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((Q6P::S - 2) * Q6P::DMA) : "memory");
+        __builtin_amdgcn_s_barrier();
+    };
+
+#pragma unroll
+    for (int i = 0; i < 3; i++) issue(min(i, nst - 1), i);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((Q6P::S - 2) * Q6P::DMA) : "memory");
+    __builtin_amdgcn_s_barrier();
+    for (int i = 0; i < nst; i += 4) {
+        step(i, std::integral_constant<int, 0>{});
+        step(i + 1, std::integral_constant<int, 1>{});
+        step(i + 2, std::integral_constant<int, 2>{});
+        step(i + 3, std::integral_constant<int, 3>{});
+    }
+    if (grpB) epilogue(3);
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int col = n0 + wn * 64 + b * 32 + c32;
+            if (col >= n) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < m) {
+                    if (psum) psum[((int64_t)blockIdx.y * m + row) * n + col] = out[a][b][r];
+                    else if (epi == EPI_STORE) Y[(int64_t)row * n + col] = out[a][b][r];
+                    else store_epi_slow(&Y[(int64_t)row * n + col], out[a][b][r], epi);
+                }
+            }
+        }
+}
+
 // Splits of K for a grid of `tiles` workgroups: up to ~256 workgroups, at
 // least 4 superblocks each, at most 8.
 static int q6_splits(int64_t tiles, int64_t nsb) {
@@ -351,6 +655,65 @@ static hipError_t launch_q6_cfg(const void* w, const Q6Ptrs& p, float* y, int64_
 // DMA offsets.
 bool q6_gemm_fits(int64_t n, int64_t k, int64_t m) {
     return k % 256 == 0 && n * (k / 256) * Q6K_BYTES + 256 < ((int64_t)1 << 32) && m * k < ((int64_t)1 << 32);
+}
+
+// LLOOM_HIP_Q6_PLANES (read once): "0" never the two-plane route, "1" from
+// the GEMM's first row count; unset: from Q6P_MIN_ROWS rows.  Measured on
+// [2048, 8192] (n 2048, k 8192), whole calls, graph replay, rotating weight
+// copies: m = 256 52.9 us against 38.7 for k_gemm_q6k, 512 62.4 / 62.3,
+// 1024 85.6 / 107.1, 2048 136.3 / 185.7 (of which k_gemm_q6p 87, the
+// activation prep 19, the weight planes 18, the split-K sum 10).
+constexpr int64_t Q6P_MIN_ROWS = 640;
+static int q6p_env() {
+    static const int v = [] {
+        const char* e = getenv("LLOOM_HIP_Q6_PLANES");
+        return e ? atoi(e) : -1;
+    }();
+    return v;
+}
+static int64_t q6p_rows(int64_t m) { return (m + Q6P::BM - 1) / Q6P::BM * Q6P::BM; }
+// (32-bit DMA offsets into the padded xq and planes)
+static bool q6p_route(int64_t n, int64_t k, int64_t m) {
+    const int e = q6p_env();
+    return e != 0 && (e == 1 || m >= Q6P_MIN_ROWS) && ((n + 127) & ~(int64_t)127) * 2 * k < ((int64_t)1 << 32) &&
+           q6p_rows(m) * k < ((int64_t)1 << 32);
+}
+static int q6p_launch_splits(int64_t n, int64_t k, int64_t m) {
+    const int64_t tiles = ((m + Q6P::BM - 1) / Q6P::BM) * ((n + Q6P::BN - 1) / Q6P::BN), nsb = k / 256;
+    const int sp = q6_splits(tiles, nsb);
+    const int64_t sps = (nsb + sp - 1) / sp;
+    return (int)((nsb + sps - 1) / sps);
+}
+static size_t q6p_workspace_bytes(int64_t n, int64_t k, int64_t m) {
+    const int sp = q6p_launch_splits(n, k, m);
+    return q6_prep_bytes(m, k, q6p_rows(m)) + q6p_plane_bytes(n, k) + q6p_dw_bytes(n, k) +
+           (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0);
+}
+
+static hipError_t launch_q6p(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
+                             size_t ws_cap, int epi, hipStream_t s) {
+    if (q6p_workspace_bytes(n, k, m) > ws_cap) return hipErrorInvalidValue;
+    const int sp = q6p_launch_splits(n, k, m);
+    const Q6Ptrs p = q6_ptrs(qbuf, m, k, q6p_rows(m));
+    uint8_t* wbase = (uint8_t*)qbuf + q6_prep_bytes(m, k, q6p_rows(m));
+    const Q6PPtrs pp = q6p_ptrs(wbase, n, k);
+    float* psum = (float*)(wbase + q6p_plane_bytes(n, k) + q6p_dw_bytes(n, k));
+    const int64_t nsb = k / 256, nb = m * nsb, wb = n * nsb;
+    hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + Q6_PREP_BLOCKS - 1) / Q6_PREP_BLOCKS)), dim3(256), 0, s, x,
+                       p.xq, p.dyt, (int)m, (int)k, (int)p.mp);
+    hipLaunchKernelGGL(k_q6_planes, dim3((unsigned)((wb + Q6_PREP_BLOCKS - 1) / Q6_PREP_BLOCKS)), dim3(256), 0, s, (const uint8_t*)w, pp.planes,
+                       pp.dwt, (int)n, (int)k, (int)pp.np);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if ((e = set_lds_limit((const void*)k_gemm_q6p, Q6P::LDS))) return e;
+    const int64_t tiles = ((m + Q6P::BM - 1) / Q6P::BM) * ((n + Q6P::BN - 1) / Q6P::BN);
+    const int sps = (int)((nsb + sp - 1) / sp);
+    hipLaunchKernelGGL(k_gemm_q6p, dim3((unsigned)tiles, sp), dim3(Q6P::THREADS), Q6P::LDS, s, pp.planes, pp.dwt, p.xq,
+                       p.dyt, y, (int)m, (int)n, (int)k, (int)p.mp, (int)pp.np, epi, sps, sp > 1 ? psum : nullptr);
+    if ((e = hipGetLastError()) != hipSuccess || sp == 1) return e;
+    const int64_t mn = m * n;
+    hipLaunchKernelGGL(k_q6_sum_splits, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, psum, sp, mn, y, epi);
+    return hipGetLastError();
 }
 
 // LLOOM_HIP_Q6_TILE (read once) picks the tile for tuning; -1 (default)
@@ -388,20 +751,22 @@ static int q6_launch_splits(int64_t n, int64_t k, int64_t m) {
 // The prepared activations, then the split-K partial sums when the launch
 // splits K.
 size_t q6_gemm_workspace_bytes(int64_t n, int64_t k, int64_t m) {
+    if (q6p_route(n, k, m)) return q6p_workspace_bytes(n, k, m);
     const int sp = q6_launch_splits(n, k, m);
     return q6_prep_bytes(m, k) + (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0);
 }
 
 hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
                           size_t ws_cap, int epi, hipStream_t s) {
+    if (q6p_route(n, k, m)) return launch_q6p(w, x, y, n, k, m, qbuf, ws_cap, epi, s);
     // the split count sizes the partial-sum region: one computation serves
     // the workspace size and the launch, and the caller's capacity is checked
     const int sp = q6_launch_splits(n, k, m);
     if (q6_prep_bytes(m, k) + (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0) > ws_cap) return hipErrorInvalidValue;
     const Q6Ptrs p = q6_ptrs(qbuf, m, k);
     const int64_t nb = m * (k / 256);
-    hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, p.xq, p.dyt, (int)m, (int)k,
-                       (int)p.mp);
+    hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + Q6_PREP_BLOCKS - 1) / Q6_PREP_BLOCKS)), dim3(256), 0, s, x,
+                       p.xq, p.dyt, (int)m, (int)k, (int)p.mp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     float* psum = (float*)((uint8_t*)qbuf + q6_prep_bytes(m, k));

@@ -300,7 +300,8 @@ def test_prefill_gemm_q8_0_shapes(L, m, n, k):
     assert_rows_close(y, O.matmul(O.Q8_0, x, q, n), what=f"q8_0 gemm m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 768), (300, 70, 1280), (200, 100, 8448), (129, 64, 4096)])
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 768), (300, 70, 1280), (200, 100, 8448), (129, 64, 4096),
+                                                 (520, 130, 2304), (2048, 136, 8192)])
 def test_prefill_gemm_q6k_shapes(L, m, n, k):
     """The Q6_K prefill GEMM on ragged tiles, an odd number of superblocks a
     row (rows then start 2 bytes off a 4-byte boundary), K split over
@@ -575,10 +576,11 @@ def _silu32(v):
     return (v / (np.float32(1) + np.exp(-v))).astype(np.float32)
 
 
-@pytest.mark.parametrize("m", [64, 160])
+@pytest.mark.parametrize("m", [64, 160, 700])
 def test_q6k_split_k_epilogues(L, m):
     """SiLU and multiply-into stores where the Q6_K GEMM splits K over
-    workgroups (one or two column tiles, 16 superblocks a row): the stores
+    workgroups (one or two column tiles, 16 superblocks a row; m = 700 on
+    the two-plane route, whose last row block is ragged): the stores
     are applied once, by the pass that adds the partial sums in split order,
     and a second, smaller call reuses the workspace the first one sized."""
     rng = np.random.default_rng(70 + m)
