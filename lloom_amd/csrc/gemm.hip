@@ -1129,7 +1129,7 @@ hipError_t launch_gemm(int type, const void* w, const float* x, float* y, int64_
                            y, (int)m, (int)n, (int)k, epi);
         return hipGetLastError();
     }
-    if (type == T_Q8_0 && q8_gemm_fits(n, k, m)) return launch_q8_gemm(w, x, y, n, k, m, qbuf, epi, s);
+    if (type == T_Q8_0 && q8_gemm_fits(n, k, m)) return launch_q8_gemm(w, x, y, n, k, m, qbuf, ws_cap, epi, s);
     // Q8_0 (and Q4_K past 32-bit offsets): tiles of 16 activation rows
     // through the decode kernels
     for (int64_t r = 0; r < m; r += 16) {

@@ -13,6 +13,7 @@
 namespace lloom {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------ Q8_0 GEMM ----
 // y[m, n] = sum_b (sum_{k in b} x8[m,k] w8[n,k]) * dx[m,b] * dw[n,b] over
@@ -21,9 +22,12 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // BlockQ8_0::from_float (k_quants.rs:738-767) and both scales taken as
 // f32(f16 d), as the reference does.  One v_mfma_i32_32x32x32_i8 is one block
 // of one 32 x 32 tile (its K is the block's 32), so every block's integer sum
-// is exact and the scales apply per block in f32: out += f32(S) * (dx * dw),
-// three VALU instructions per output and block, which bound this kernel
-// (the MFMAs take a sixth of that time).
+// is exact and the scales apply per block in f32: out += f32(S) * (dx * dw).
+// The tile's dx * dw products come from the matrix core too (a K = 2 f32
+// MFMA, below), which leaves two VALU instructions per output and block,
+// convert and fma.  Measured at m = 2048 on [8192, 2048], VALU and MFMA
+// work do not overlap much here: 41.7 M VALU and 100.7 M MFMA-busy cycles a
+// call (3 VALU: 57.4 M and 33.6 M) take the same ~155 us.
 //
 // Activation prep (bit-exact Q8_0, the weights' own block layout stays):
 //   xq  int8 [m][k]
@@ -42,9 +46,10 @@ static Q8Ptrs q8_ptrs(void* base, int64_t m, int64_t k) {
     return p;
 }
 
-size_t q8_gemm_workspace_bytes(int64_t m, int64_t k) {
+static size_t q8_prep_bytes(int64_t m, int64_t k) {
     const int64_t mp = (m + 3) & ~(int64_t)3;
-    return (((size_t)m * k + 255) & ~(size_t)255) + ((size_t)(k / 32) * mp + 128) * sizeof(float);
+    return (((size_t)m * k + 255) & ~(size_t)255) +
+           ((((size_t)(k / 32) * mp + 128) * sizeof(float) + 255) & ~(size_t)255);
 }
 
 // One wave a (row, 256 elements): eight blocks of eight lanes.
@@ -230,22 +235,30 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_q8_0(const uint8_t* __restr
                     const v16i z = {};
                     d[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bv[b], z, 0, 0, 0);
                 }
+            // the scale products dx * dw of the tile, on the matrix core: a
+            // K = 2 f32 MFMA whose two k-slots (lanes 0-31, 32-63) both hold
+            // the lane's row scale and column scale gives 2 dx dw, exactly
+            // (two products of 11-bit significands, summed), in the layout
+            // of the integer sums; the factor 2 leaves with one exact
+            // halving at the store
+            v16f p2[C::MT][C::NT];
 #pragma unroll
             for (int a = 0; a < C::MT; a++) {
-                const float* dxp = DX + j * C::BM + wm * 32 * C::MT + a * 32 + 4 * h;
+                const float dxl = DX[j * C::BM + wm * 32 * C::MT + a * 32 + c32];
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 d4 = *(const float4*)(dxp + 8 * g);
-                    const float dxs[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const int r = 4 * g + u;
-#pragma unroll
-                        for (int b = 0; b < C::NT; b++)
-                            out[a][b][r] = __builtin_fmaf((float)d[a][b][r], dxs[u] * dw[b], out[a][b][r]);
-                    }
+                for (int b = 0; b < C::NT; b++) {
+                    const v16f zf = {};
+                    p2[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(dxl, dw[b], zf, 0, 0, 0);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int a = 0; a < C::MT; a++)
+#pragma unroll
+                for (int b = 0; b < C::NT; b++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        out[a][b][r] = __builtin_fmaf((float)d[a][b][r], p2[a][b][r], out[a][b][r]);
         };
         block(std::integral_constant<int, 0>{});
         block(std::integral_constant<int, 1>{});
@@ -270,9 +283,10 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_q8_0(const uint8_t* __restr
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm * 32 * C::MT + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const float v = 0.5f * out[a][b][r];
                 if (row < m) {
-                    if (epi == EPI_STORE) Y[(int64_t)row * n + col] = out[a][b][r];
-                    else store_epi_slow(&Y[(int64_t)row * n + col], out[a][b][r], epi);
+                    if (epi == EPI_STORE) Y[(int64_t)row * n + col] = v;
+                    else store_epi_slow(&Y[(int64_t)row * n + col], v, epi);
                 }
             }
         }
@@ -489,8 +503,11 @@ static int q8_tile_env() {
     return v;
 }
 
+size_t q8_gemm_workspace_bytes(int64_t m, int64_t k) { return q8_prep_bytes(m, k); }
+
 hipError_t launch_q8_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
-                          int epi, hipStream_t s) {
+                          size_t ws_cap, int epi, hipStream_t s) {
+    if (q8_prep_bytes(m, k) > ws_cap) return hipErrorInvalidValue;
     const Q8Ptrs p = q8_ptrs(qbuf, m, k);
     const int64_t nc = m * (k / 256);
     hipLaunchKernelGGL(k_gemm_prep_q8_0, dim3((unsigned)((nc + 3) / 4)), dim3(256), 0, s, x, p.xq, p.dxt, (int)m,

@@ -90,7 +90,7 @@ constexpr int Q8_GEMM_MIN_ROWS = 5;
 bool q8_gemm_fits(int64_t n, int64_t k, int64_t m);
 size_t q8_gemm_workspace_bytes(int64_t m, int64_t k);
 hipError_t launch_q8_gemm(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* qbuf,
-                          int epi, hipStream_t s);
+                          size_t ws_cap, int epi, hipStream_t s);
 
 // moe.hip
 // The router keeps two ints per expert in LDS.
