@@ -514,7 +514,7 @@ def cpu_baseline(L, qt, xs, n, k, Bs, algo, budget_s):
             "sample": f"C2 sweep B in {{1,2,4,8,16}} x {iters} iterations ({el:.1f} s), same Q4_K bytes, "
                       f"restatement of lloom-tensor CPU QMatMul (AVX2, barrier pool); "
                       f"physical cores {phys}, nproc {os.cpu_count()}, {cpu_model}; one 7 MB weight "
-                      f"replayed, so it stays resident in the host caches (the GPU figure streams 512 MB "
+                      f"replayed, so it stays resident in the host caches (the GPU figure streams at least 512 MB "
                       f"of rotating copies from HBM)"}
 
 
