@@ -317,6 +317,23 @@ def test_prefill_gemm_q6k_shapes(L, m, n, k):
     assert_rows_close(y, O.matmul(O.Q6K, x, q, n), what=f"q6k gemm m={m} n={n} k={k}")
 
 
+def test_q6k_plane_route_forced(L):
+    """The Q6_K two-plane route forced on from the GEMM's first row count
+    (LLOOM_HIP_Q6_PLANES=1 is read once per process, so in a child pytest):
+    the Q6_K GEMM shape and split-K store tests again, which puts their
+    shapes of 48 rows and up on it: single and ragged 256-row blocks, ragged
+    columns, odd superblock counts, and up to eight K splits."""
+    import subprocess
+    import sys
+
+    env = dict(os.environ, LLOOM_HIP_Q6_PLANES="1")
+    r = subprocess.run([sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider", os.path.abspath(__file__),
+                        "-k", "prefill_gemm_q6k_shapes or q6k_split_k_epilogues"],
+                       env=env, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
+    assert " passed" in r.stdout and "skipped" not in r.stdout.splitlines()[-1], r.stdout[-500:]
+
+
 def test_prefill_gemm_q8_0_epilogues(L):
     """SiLU and multiply-into stores on the Q8_0 GEMM route."""
     rng = np.random.default_rng(21)
