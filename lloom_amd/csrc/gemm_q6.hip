@@ -23,6 +23,8 @@
 namespace lloom {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // Activation prep (Q8_K of every (row, superblock), bit-exact):
 //   xq  int8 [m][k]
@@ -49,30 +51,48 @@ static size_t q6_prep_bytes(int64_t m, int64_t k, int64_t xq_rows = 0) {
 }
 
 
-// One wave four consecutive (row, superblock) blocks (x is [m][k], so
-// they are 4 KB of contiguous input), all four loads issued first.
-constexpr int Q6_PREP_BLOCKS = 16;  // a workgroup's blocks
-__global__ __launch_bounds__(256) void k_gemm_prep_q6(const float* __restrict__ x, int8_t* __restrict__ xq,
-                                                      float* __restrict__ dyt, int m, int k, int mp) {
-    const int lane = threadIdx.x & 63;
-    const int nsb = k >> 8;
-    const int64_t nblk = (int64_t)m * nsb;
-    const int64_t blk0 = (int64_t)blockIdx.x * Q6_PREP_BLOCKS + 4 * (threadIdx.x >> 6);
-    float4 v[4];
+// Each 16-lane row of a wave quantizes one (row, superblock) block
+// (q8k_block_row16: lane j holds elements 16j .. 16j+15, which are 16
+// contiguous bytes of xq), two blocks a row: a workgroup takes 32
+// consecutive blocks of x ([m][k], so 32 KB of contiguous input), every
+// load issued first.  (Block indices are 32-bit: m * k / 256 < 2^31.)
+constexpr int Q6_XPREP_BLOCKS = 32;  // blocks a workgroup
+__device__ __forceinline__ void q6_prep_x(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                          float* __restrict__ dyt, int m, int k, int mp, uint32_t bid) {
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const uint32_t nsb = (uint32_t)k >> 8, nblk = (uint32_t)m * nsb;
+    const uint32_t b0 = bid * Q6_XPREP_BLOCKS + 4 * (threadIdx.x >> 6) + (lane >> 4);
+    float xs[2][16];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-        v[j] = blk0 + j < nblk ? *(const float4*)(x + (blk0 + j) * 256 + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int r = 0; r < 2; r++) {
+        const uint32_t blk = min(b0 + 16 * r, nblk - 1);  // past the end: a duplicate, not stored
+        const float4* src = (const float4*)(x + (size_t)blk * 256 + 16 * j);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int64_t blk = blk0 + j;
-        if (blk >= nblk) return;
+        for (int u = 0; u < 4; u++) {
+            const float4 v = src[u];
+            xs[r][4 * u] = v.x;
+            xs[r][4 * u + 1] = v.y;
+            xs[r][4 * u + 2] = v.z;
+            xs[r][4 * u + 3] = v.w;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint32_t blk = b0 + 16 * r;
         float d;
         int bs;
-        const uint32_t q = q8k_block_wave(v[j], &d, &bs);
-        *(uint32_t*)(xq + blk * 256 + 4 * lane) = q;
-        const int mi = (int)(blk / nsb), sb = (int)(blk - (int64_t)mi * nsb);
-        if (lane == 0) dyt[(int64_t)sb * mp + mi] = d;
+        const uint4 q = q8k_block_row16(xs[r], &d, &bs);  // every lane of the row: DPP inside
+        if (blk < nblk) {
+            *(uint4*)(xq + (size_t)blk * 256 + 16 * j) = q;
+            const uint32_t mi = blk / nsb, sb = blk - mi * nsb;
+            if (j == 0) dyt[(size_t)sb * mp + mi] = d;
+        }
     }
+}
+
+__global__ __launch_bounds__(256) void k_gemm_prep_q6(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                      float* __restrict__ dyt, int m, int k, int mp) {
+    q6_prep_x(x, xq, dyt, m, k, mp, blockIdx.x);
 }
 
 // Tiling: WM x WN waves, each MT x NT tiles of 32 x 32 (BM = 32 WM MT, BN =
@@ -322,14 +342,36 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_q6k(const uint8_t* __restri
 }
 
 // The split-K partial sums, added in split order, then the call's store
-// epilogue.
+// epilogue; four consecutive outputs a thread (16-byte loads and stores
+// where the four are in range and aligned, one at a time otherwise).
 __global__ __launch_bounds__(256) void k_q6_sum_splits(const float* __restrict__ psum, int splits, int64_t mn,
                                                        float* __restrict__ Y, int epi) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
     if (i >= mn) return;
-    float v = psum[i];
-    for (int z = 1; z < splits; z++) v += psum[z * mn + i];
-    store_epi(&Y[i], v, epi);
+    if (i + 4 <= mn && (mn & 3) == 0 && ((uintptr_t)Y & 15) == 0) {
+        float4 v = *(const float4*)(psum + i);
+        for (int z = 1; z < splits; z++) {
+            const float4 u = *(const float4*)(psum + z * mn + i);
+            v.x += u.x;
+            v.y += u.y;
+            v.z += u.z;
+            v.w += u.w;
+        }
+        if (epi == EPI_STORE) {
+            *(float4*)(Y + i) = v;
+        } else {
+            store_epi(&Y[i], v.x, epi);
+            store_epi(&Y[i + 1], v.y, epi);
+            store_epi(&Y[i + 2], v.z, epi);
+            store_epi(&Y[i + 3], v.w, epi);
+        }
+        return;
+    }
+    for (int64_t t = i; t < min(i + 4, mn); t++) {
+        float v = psum[t];
+        for (int z = 1; z < splits; z++) v += psum[z * mn + t];
+        store_epi(&Y[t], v, epi);
+    }
 }
 
 // ------------------------------------------------ two-plane route ----
@@ -374,49 +416,85 @@ static Q6PPtrs q6p_ptrs(void* base, int64_t n, int64_t k) {
 // blocks, so they are 840 contiguous bytes (2-byte aligned), which come in
 // as the 212 dwords around them (four loads a lane, all issued first)
 // through LDS; then each lane makes four elements of each block (4 l ..
-// 4 l + 3 share their scale and bit positions).
-__global__ __launch_bounds__(256) void k_q6_planes(const uint8_t* __restrict__ W, int8_t* __restrict__ planes,
-                                                   float* __restrict__ dwt, int n, int k, int np) {
-    __shared__ uint32_t raw[4][4 * 64];
+// 4 l + 3 share their scale and bit positions; two elements a 16-bit lane).
+// This half of the prep is bound by its VALU work, so it runs in
+// the same launch as the activations' (bound by memory), on the grid's last
+// workgroups.  (Block indices are 32-bit.)
+constexpr int Q6P_PLANE_WG = 16;  // blocks a workgroup
+__device__ __forceinline__ void q6_planes(const uint8_t* __restrict__ W, int8_t* __restrict__ planes,
+                                          float* __restrict__ dwt, int n, int k, int np, uint32_t bid,
+                                          uint32_t (&raw)[4][256]) {
     const int lane = threadIdx.x & 63, wq = threadIdx.x >> 6;
-    const int nsb = k >> 8;
-    const int64_t nblk = (int64_t)n * nsb;
-    const int64_t blk0 = (int64_t)blockIdx.x * Q6_PREP_BLOCKS + 4 * wq;
-    const int64_t first = blk0 < nblk ? blk0 * Q6K_BYTES : 0;
+    const uint32_t nsb = (uint32_t)k >> 8, nblk = (uint32_t)n * nsb;
+    const uint32_t blk0 = bid * Q6P_PLANE_WG + 4 * wq;
+    const int64_t first = blk0 < nblk ? (int64_t)blk0 * Q6K_BYTES : 0;
     const uint32_t* src = (const uint32_t*)(W + (first & ~(int64_t)3));
     const int sh = (int)(first & 3);  // 0 or 2
     // (W's last block may end 2 bytes into its last dword)
-    const int64_t left = ((nblk * Q6K_BYTES + 3) >> 2) - (first >> 2);
+    const int64_t left = (((int64_t)nblk * Q6K_BYTES + 3) >> 2) - (first >> 2);
+    const int lim = (int)min(left, (int64_t)212);
     uint32_t wd[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) wd[j] = 64 * j + lane < min(left, (int64_t)212) ? src[64 * j + lane] : 0u;
+    for (int i = 0; i < 4; i++) wd[i] = 64 * i + lane < lim ? src[64 * i + lane] : 0u;
 #pragma unroll
-    for (int j = 0; j < 4; j++) raw[wq][64 * j + lane] = wd[j];
+    for (int i = 0; i < 4; i++) raw[wq][64 * i + lane] = wd[i];
     __syncthreads();
+    const int e0 = 4 * lane, hh = e0 >> 7, r = e0 & 127, g = r >> 5, l = r & 31;
+    const uint8_t* rb = (const uint8_t*)raw[wq];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int64_t blk = blk0 + j;
+        const uint32_t blk = blk0 + j;
         if (blk >= nblk) return;
-        const uint8_t* b = (const uint8_t*)raw[wq] + sh + j * Q6K_BYTES;
-        const int c = (int)(blk / nsb), sb = (int)(blk - (int64_t)c * nsb);
-        const int e0 = 4 * lane, hh = e0 >> 7, r = e0 & 127, g = r >> 5, l = r & 31;
+        // the block starts sh + 210 j bytes into the wave's LDS copy (an even
+        // offset); its four ql bytes and four qh bytes of this lane's
+        // elements are 4-byte aligned within the block
+        const int bo = sh + j * Q6K_BYTES, al = bo & 3;
+        const uint32_t* q1 = (const uint32_t*)(rb + ((bo + 64 * hh + 32 * (g & 1) + l) & ~3));
+        const uint32_t* q2 = (const uint32_t*)(rb + ((bo + Q6K_QH + 32 * hh + l) & ~3));
+        const uint32_t qlw = __builtin_amdgcn_alignbyte(q1[1], q1[0], al);
+        const uint32_t qhw = __builtin_amdgcn_alignbyte(q2[1], q2[0], al);
+        const uint8_t* b = rb + bo;
+        const uint32_t c = blk / nsb, sb = blk - c * nsb;
         const int sc = (int)(int8_t)b[Q6K_SC + (e0 >> 4)];
-        uint32_t hi4 = 0, lo4 = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int qlo = (b[64 * hh + 32 * (g & 1) + l + i] >> (4 * (g >> 1))) & 15;
-            const int qhi = (b[Q6K_QH + 32 * hh + l + i] >> (2 * g)) & 3;
-            const int v = sc * ((qlo | (qhi << 4)) - 32);
-            const int lo = ((v + 32) & 63) - 32;
-            const int hi = (v - lo) >> 6;
-            lo4 |= (uint32_t)(lo & 255) << (8 * i);
-            hi4 |= (uint32_t)(hi & 255) << (8 * i);
-        }
-        int8_t* o = planes + (int64_t)c * 2 * k + 512 * sb + 128 * (e0 >> 6) + (e0 & 63);
+        // q6 of the four elements, one a byte (0..63)
+        const uint32_t q = ((qlw >> (4 * (g >> 1))) & 0x0f0f0f0fu) | (((qhw >> (2 * g)) & 0x03030303u) << 4);
+        // v = sc q - 32 sc in 16-bit lanes (|sc q| <= 8064: the low 16 bits
+        // of the product are the signed result), elements 0, 2 and 1, 3
+        const u16x2 sc2 = {(uint16_t)sc, (uint16_t)sc};
+        const u16x2 sc32 = {(uint16_t)(32 * sc), (uint16_t)(32 * sc)};
+        const u16x2 ve = __builtin_bit_cast(u16x2, q & 0x00ff00ffu) * sc2 - sc32;
+        const u16x2 vo = __builtin_bit_cast(u16x2, (q >> 8) & 0x00ff00ffu) * sc2 - sc32;
+        // lo = ((v + 32) & 63) - 32, hi = (v - lo) >> 6 (arithmetic)
+        const u16x2 c32 = {32, 32}, m63 = {63, 63};
+        const u16x2 le = ((ve + c32) & m63) - c32, lo_ = ((vo + c32) & m63) - c32;
+        const s16x2 he = __builtin_bit_cast(s16x2, (u16x2)(ve - le)) >> (s16x2){6, 6};
+        const s16x2 ho = __builtin_bit_cast(s16x2, (u16x2)(vo - lo_)) >> (s16x2){6, 6};
+        // bytes 0-3 = elements 0-3: the low bytes of (even, odd, even, odd)
+        const uint32_t lo4 = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, lo_), __builtin_bit_cast(uint32_t, le),
+                                                   0x06020400u);
+        const uint32_t hi4 = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he),
+                                                   0x06020400u);
+        int8_t* o = planes + (size_t)c * 2 * k + 512 * sb + 128 * (e0 >> 6) + (e0 & 63);
         *(uint32_t*)o = hi4;
         *(uint32_t*)(o + 64) = lo4;
-        if (lane == 0) dwt[(int64_t)sb * np + c] = f16_to_f32(*(const uint16_t*)(b + Q6K_D));
+        if (lane == 0) dwt[(size_t)sb * np + c] = f16_to_f32(*(const uint16_t*)(b + Q6K_D));
     }
+}
+
+// The two-plane route's prep, one launch: xwg workgroups quantize the
+// activations (as k_gemm_prep_q6) and the others build the weight planes,
+// spread evenly through the grid (workgroup b is activation workgroup
+// floor(b xwg / grid) when that count steps up at b, else a plane one), so
+// the memory-bound and the VALU-bound halves share the CUs.
+__global__ __launch_bounds__(256) void k_q6p_prep(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                  float* __restrict__ dyt, int m, int k, int mp, uint32_t xwg,
+                                                  const uint8_t* __restrict__ W, int8_t* __restrict__ planes,
+                                                  float* __restrict__ dwt, int n, int np) {
+    __shared__ uint32_t raw[4][256];
+    const uint64_t b = blockIdx.x, T = gridDim.x;
+    const uint32_t xi = (uint32_t)(b * xwg / T);
+    if ((uint32_t)((b + 1) * xwg / T) > xi) q6_prep_x(x, xq, dyt, m, k, mp, xi);  // uniform
+    else q6_planes(W, planes, dwt, n, k, np, (uint32_t)b - xi, raw);
 }
 
 // Tiling: 4 x 2 waves of 64 x 64 (2 x 2 tiles of 32 x 32): a 256 x 128
@@ -647,7 +725,7 @@ static hipError_t launch_q6_cfg(const void* w, const Q6Ptrs& p, float* y, int64_
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || sp == 1) return e;
     const int64_t mn = m * n;
-    hipLaunchKernelGGL(k_q6_sum_splits, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, psum, sp, mn, y, epi);
+    hipLaunchKernelGGL(k_q6_sum_splits, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, s, psum, sp, mn, y, epi);
     return hipGetLastError();
 }
 
@@ -699,10 +777,10 @@ static hipError_t launch_q6p(const void* w, const float* x, float* y, int64_t n,
     const Q6PPtrs pp = q6p_ptrs(wbase, n, k);
     float* psum = (float*)(wbase + q6p_plane_bytes(n, k) + q6p_dw_bytes(n, k));
     const int64_t nsb = k / 256, nb = m * nsb, wb = n * nsb;
-    hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + Q6_PREP_BLOCKS - 1) / Q6_PREP_BLOCKS)), dim3(256), 0, s, x,
-                       p.xq, p.dyt, (int)m, (int)k, (int)p.mp);
-    hipLaunchKernelGGL(k_q6_planes, dim3((unsigned)((wb + Q6_PREP_BLOCKS - 1) / Q6_PREP_BLOCKS)), dim3(256), 0, s, (const uint8_t*)w, pp.planes,
-                       pp.dwt, (int)n, (int)k, (int)pp.np);
+    const uint32_t xwg = (uint32_t)((nb + Q6_XPREP_BLOCKS - 1) / Q6_XPREP_BLOCKS);
+    const uint32_t pwg = (uint32_t)((wb + Q6P_PLANE_WG - 1) / Q6P_PLANE_WG);
+    hipLaunchKernelGGL(k_q6p_prep, dim3(xwg + pwg), dim3(256), 0, s, x, p.xq, p.dyt, (int)m, (int)k, (int)p.mp, xwg,
+                       (const uint8_t*)w, pp.planes, pp.dwt, (int)n, (int)pp.np);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if ((e = set_lds_limit((const void*)k_gemm_q6p, Q6P::LDS))) return e;
@@ -712,7 +790,7 @@ static hipError_t launch_q6p(const void* w, const float* x, float* y, int64_t n,
                        p.dyt, y, (int)m, (int)n, (int)k, (int)p.mp, (int)pp.np, epi, sps, sp > 1 ? psum : nullptr);
     if ((e = hipGetLastError()) != hipSuccess || sp == 1) return e;
     const int64_t mn = m * n;
-    hipLaunchKernelGGL(k_q6_sum_splits, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, psum, sp, mn, y, epi);
+    hipLaunchKernelGGL(k_q6_sum_splits, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, s, psum, sp, mn, y, epi);
     return hipGetLastError();
 }
 
@@ -765,7 +843,7 @@ hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, in
     if (q6_prep_bytes(m, k) + (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0) > ws_cap) return hipErrorInvalidValue;
     const Q6Ptrs p = q6_ptrs(qbuf, m, k);
     const int64_t nb = m * (k / 256);
-    hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + Q6_PREP_BLOCKS - 1) / Q6_PREP_BLOCKS)), dim3(256), 0, s, x,
+    hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + Q6_XPREP_BLOCKS - 1) / Q6_XPREP_BLOCKS)), dim3(256), 0, s, x,
                        p.xq, p.dyt, (int)m, (int)k, (int)p.mp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
