@@ -94,15 +94,16 @@ def moe_ids(L, np, T, E, topk):
     return np.argsort(-p, axis=1, kind="stable")[:, :topk].astype(np.int32)
 
 
-def csrc_digest():
-    """sha256 of the kernel sources (lloom_amd/csrc, sorted by name): the
-    committed traffic profiles record the digest of the build they measured,
-    so a profile taken on other kernels is reported as stale, not quoted."""
+def csrc_digest(names=None):
+    """sha256 of kernel sources in lloom_amd/csrc (the named files, or every
+    source file; sorted by name).  A committed traffic profile records the
+    files its measured kernels are built from and their digest, so a profile
+    taken on other kernels is reported as stale, not quoted."""
     import hashlib
 
     h = hashlib.sha256()
     d = os.path.join(ROOT, "lloom_amd", "csrc")
-    for name in sorted(os.listdir(d)):
+    for name in sorted(names or os.listdir(d)):
         if name.endswith((".hip", ".hpp", ".cpp", ".h")):
             h.update(name.encode())
             with open(os.path.join(d, name), "rb") as f:
@@ -259,16 +260,15 @@ def main():
     # time, from the per-B graphs above (events on the replay stream).
     # traffic: measured HBM bytes per call, from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE calibration when present.
-    digest = csrc_digest()
-
     def traffic_of(b):
-        """(HBM bytes per launch, or None; a note when the profile is of
-        other kernel sources than these)."""
+        """(HBM bytes per launch, or None; where the figure comes from, or why
+        it is not quoted: a profile of other kernel sources than these)."""
         tpath = os.path.join(ROOT, "profiles", "traffic_c2_b%d.json" % b)
         if not os.path.exists(tpath):
             return None, "no profile"
         with open(tpath) as f:
             prof = json.load(f)
+        digest = csrc_digest(prof.get("digest_files"))
         if prof.get("csrc_digest") != digest:
             return None, "stale: %s measured kernel sources %s (commit %s), these are %s" % (
                 os.path.basename(tpath), prof.get("csrc_digest"), prof.get("commit"), digest)
