@@ -53,18 +53,20 @@ static size_t q6_prep_bytes(int64_t m, int64_t k, int64_t xq_rows = 0) {
 
 // Each 16-lane row of a wave quantizes one (row, superblock) block
 // (q8k_block_row16: lane j holds elements 16j .. 16j+15, which are 16
-// contiguous bytes of xq), two blocks a row: a workgroup takes 32
-// consecutive blocks of x ([m][k], so 32 KB of contiguous input), every
-// load issued first.  (Block indices are 32-bit: m * k / 256 < 2^31.)
-constexpr int Q6_XPREP_BLOCKS = 32;  // blocks a workgroup
+// contiguous bytes of xq), RB blocks a row: a workgroup takes 16 RB
+// consecutive blocks of x ([m][k], so 16 RB KB of contiguous input), every
+// load issued first; two a row once there are enough blocks to fill the
+// GPU with workgroups of 32.  (Block indices are 32-bit: m * k / 256 < 2^31.)
+constexpr int64_t Q6_XPREP_RB2 = 256 * 32;  // blocks from which a row takes two
+template <int RB>
 __device__ __forceinline__ void q6_prep_x(const float* __restrict__ x, int8_t* __restrict__ xq,
                                           float* __restrict__ dyt, int m, int k, int mp, uint32_t bid) {
     const int lane = threadIdx.x & 63, j = lane & 15;
     const uint32_t nsb = (uint32_t)k >> 8, nblk = (uint32_t)m * nsb;
-    const uint32_t b0 = bid * Q6_XPREP_BLOCKS + 4 * (threadIdx.x >> 6) + (lane >> 4);
-    float xs[2][16];
+    const uint32_t b0 = bid * (16 * RB) + 4 * (threadIdx.x >> 6) + (lane >> 4);
+    float xs[RB][16];
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
+    for (int r = 0; r < RB; r++) {
         const uint32_t blk = min(b0 + 16 * r, nblk - 1);  // past the end: a duplicate, not stored
         const float4* src = (const float4*)(x + (size_t)blk * 256 + 16 * j);
 #pragma unroll
@@ -77,7 +79,7 @@ __device__ __forceinline__ void q6_prep_x(const float* __restrict__ x, int8_t* _
         }
     }
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
+    for (int r = 0; r < RB; r++) {
         const uint32_t blk = b0 + 16 * r;
         float d;
         int bs;
@@ -90,9 +92,21 @@ __device__ __forceinline__ void q6_prep_x(const float* __restrict__ x, int8_t* _
     }
 }
 
+template <int RB>
 __global__ __launch_bounds__(256) void k_gemm_prep_q6(const float* __restrict__ x, int8_t* __restrict__ xq,
                                                       float* __restrict__ dyt, int m, int k, int mp) {
-    q6_prep_x(x, xq, dyt, m, k, mp, blockIdx.x);
+    q6_prep_x<RB>(x, xq, dyt, m, k, mp, blockIdx.x);
+}
+// The launch for nb blocks.
+static hipError_t launch_prep_q6(const float* x, int8_t* xq, float* dyt, int64_t m, int64_t k, int64_t mp, hipStream_t s) {
+    const int64_t nb = m * (k / 256);
+    if (nb >= Q6_XPREP_RB2)
+        hipLaunchKernelGGL(k_gemm_prep_q6<2>, dim3((unsigned)((nb + 31) / 32)), dim3(256), 0, s, x, xq, dyt, (int)m,
+                           (int)k, (int)mp);
+    else
+        hipLaunchKernelGGL(k_gemm_prep_q6<1>, dim3((unsigned)((nb + 15) / 16)), dim3(256), 0, s, x, xq, dyt, (int)m,
+                           (int)k, (int)mp);
+    return hipGetLastError();
 }
 
 // Tiling: WM x WN waves, each MT x NT tiles of 32 x 32 (BM = 32 WM MT, BN =
@@ -493,7 +507,7 @@ __global__ __launch_bounds__(256) void k_q6p_prep(const float* __restrict__ x, i
     __shared__ uint32_t raw[4][256];
     const uint64_t b = blockIdx.x, T = gridDim.x;
     const uint32_t xi = (uint32_t)(b * xwg / T);
-    if ((uint32_t)((b + 1) * xwg / T) > xi) q6_prep_x(x, xq, dyt, m, k, mp, xi);  // uniform
+    if ((uint32_t)((b + 1) * xwg / T) > xi) q6_prep_x<2>(x, xq, dyt, m, k, mp, xi);  // uniform
     else q6_planes(W, planes, dwt, n, k, np, (uint32_t)b - xi, raw);
 }
 
@@ -738,9 +752,10 @@ bool q6_gemm_fits(int64_t n, int64_t k, int64_t m) {
 // LLOOM_HIP_Q6_PLANES (read once): "0" never the two-plane route, "1" from
 // the GEMM's first row count; unset: from Q6P_MIN_ROWS rows.  Measured on
 // [2048, 8192] (n 2048, k 8192), whole calls, graph replay, rotating weight
-// copies: m = 256 52.9 us against 38.7 for k_gemm_q6k, 512 62.4 / 62.3,
-// 1024 85.6 / 107.1, 2048 136.3 / 185.7 (of which k_gemm_q6p 87, the
-// activation prep 19, the weight planes 18, the split-K sum 10).
+// copies: m = 512 60.7 us, the same as k_gemm_q6k; 1024 77.5 against
+// 105.1, 2048 122.0 against 182.0 (of which k_gemm_q6p ~82, the prep
+// launch ~25, the split-K sum ~9); at 256 the first form of this route
+// measured 52.9 against 38.7.
 constexpr int64_t Q6P_MIN_ROWS = 640;
 static int q6p_env() {
     static const int v = [] {
@@ -777,7 +792,7 @@ static hipError_t launch_q6p(const void* w, const float* x, float* y, int64_t n,
     const Q6PPtrs pp = q6p_ptrs(wbase, n, k);
     float* psum = (float*)(wbase + q6p_plane_bytes(n, k) + q6p_dw_bytes(n, k));
     const int64_t nsb = k / 256, nb = m * nsb, wb = n * nsb;
-    const uint32_t xwg = (uint32_t)((nb + Q6_XPREP_BLOCKS - 1) / Q6_XPREP_BLOCKS);
+    const uint32_t xwg = (uint32_t)((nb + 31) / 32);
     const uint32_t pwg = (uint32_t)((wb + Q6P_PLANE_WG - 1) / Q6P_PLANE_WG);
     hipLaunchKernelGGL(k_q6p_prep, dim3(xwg + pwg), dim3(256), 0, s, x, p.xq, p.dyt, (int)m, (int)k, (int)p.mp, xwg,
                        (const uint8_t*)w, pp.planes, pp.dwt, (int)n, (int)pp.np);
@@ -842,10 +857,7 @@ hipError_t launch_q6_gemm(const void* w, const float* x, float* y, int64_t n, in
     const int sp = q6_launch_splits(n, k, m);
     if (q6_prep_bytes(m, k) + (sp > 1 ? (size_t)sp * m * n * sizeof(float) : 0) > ws_cap) return hipErrorInvalidValue;
     const Q6Ptrs p = q6_ptrs(qbuf, m, k);
-    const int64_t nb = m * (k / 256);
-    hipLaunchKernelGGL(k_gemm_prep_q6, dim3((unsigned)((nb + Q6_XPREP_BLOCKS - 1) / Q6_XPREP_BLOCKS)), dim3(256), 0, s, x,
-                       p.xq, p.dyt, (int)m, (int)k, (int)p.mp);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_prep_q6(x, p.xq, p.dyt, m, k, p.mp, s);
     if (e != hipSuccess) return e;
     float* psum = (float*)((uint8_t*)qbuf + q6_prep_bytes(m, k));
     const int tile = q6_tile_of(m);
