@@ -53,21 +53,22 @@ static size_t q6_prep_bytes(int64_t m, int64_t k, int64_t xq_rows = 0) {
 
 // Each 16-lane row of a wave quantizes one (row, superblock) block
 // (q8k_block_row16: lane j holds elements 16j .. 16j+15, which are 16
-// contiguous bytes of xq), RB blocks a row: a workgroup takes 16 RB
-// consecutive blocks of x ([m][k], so 16 RB KB of contiguous input), every
-// load issued first; two a row once there are enough blocks to fill the
-// GPU with workgroups of 32.  (Block indices are 32-bit: m * k / 256 < 2^31.)
+// contiguous bytes of xq), RB blocks a row: a workgroup of W waves takes
+// 4 W RB consecutive blocks of x ([m][k], so 4 W RB KB of contiguous input),
+// every load issued first, two a row; calls with fewer blocks than fill the
+// GPU with such workgroups take one block a wave (k_gemm_prep_q6_wave).
+// (Block indices are 32-bit: m * k / 256 < 2^31.)
 constexpr int64_t Q6_XPREP_RB2 = 256 * 32;  // blocks from which a row takes two
-template <int RB>
+template <int RB, int W>
 __device__ __forceinline__ void q6_prep_x(const float* __restrict__ x, int8_t* __restrict__ xq,
                                           float* __restrict__ dyt, int m, int k, int mp, uint32_t bid) {
     const int lane = threadIdx.x & 63, j = lane & 15;
     const uint32_t nsb = (uint32_t)k >> 8, nblk = (uint32_t)m * nsb;
-    const uint32_t b0 = bid * (16 * RB) + 4 * (threadIdx.x >> 6) + (lane >> 4);
+    const uint32_t b0 = bid * (4 * W * RB) + 4 * (threadIdx.x >> 6) + (lane >> 4);
     float xs[RB][16];
 #pragma unroll
     for (int r = 0; r < RB; r++) {
-        const uint32_t blk = min(b0 + 16 * r, nblk - 1);  // past the end: a duplicate, not stored
+        const uint32_t blk = min(b0 + 4 * W * r, nblk - 1);  // past the end: a duplicate, not stored
         const float4* src = (const float4*)(x + (size_t)blk * 256 + 16 * j);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -80,7 +81,7 @@ __device__ __forceinline__ void q6_prep_x(const float* __restrict__ x, int8_t* _
     }
 #pragma unroll
     for (int r = 0; r < RB; r++) {
-        const uint32_t blk = b0 + 16 * r;
+        const uint32_t blk = b0 + 4 * W * r;
         float d;
         int bs;
         const uint4 q = q8k_block_row16(xs[r], &d, &bs);  // every lane of the row: DPP inside
@@ -92,19 +93,35 @@ __device__ __forceinline__ void q6_prep_x(const float* __restrict__ x, int8_t* _
     }
 }
 
-template <int RB>
-__global__ __launch_bounds__(256) void k_gemm_prep_q6(const float* __restrict__ x, int8_t* __restrict__ xq,
-                                                      float* __restrict__ dyt, int m, int k, int mp) {
-    q6_prep_x<RB>(x, xq, dyt, m, k, mp, blockIdx.x);
+template <int RB, int W>
+__global__ __launch_bounds__(64 * W) void k_gemm_prep_q6(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                         float* __restrict__ dyt, int m, int k, int mp) {
+    q6_prep_x<RB, W>(x, xq, dyt, m, k, mp, blockIdx.x);
+}
+// The same blocks, one a wave (its 64 lanes four elements each), for calls
+// with few blocks: more waves, each with less to do.
+__global__ __launch_bounds__(256) void k_gemm_prep_q6_wave(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                           float* __restrict__ dyt, int m, int k, int mp) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t nsb = (uint32_t)k >> 8, nblk = (uint32_t)m * nsb;
+    const uint32_t blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;
+    const float4 v = *(const float4*)(x + (size_t)blk * 256 + 4 * lane);
+    float d;
+    int bs;
+    const uint32_t q = q8k_block_wave(v, &d, &bs);
+    *(uint32_t*)(xq + (size_t)blk * 256 + 4 * lane) = q;
+    const uint32_t mi = blk / nsb, sb = blk - mi * nsb;
+    if (lane == 0) dyt[(size_t)sb * mp + mi] = d;
 }
 // The launch for nb blocks.
 static hipError_t launch_prep_q6(const float* x, int8_t* xq, float* dyt, int64_t m, int64_t k, int64_t mp, hipStream_t s) {
     const int64_t nb = m * (k / 256);
     if (nb >= Q6_XPREP_RB2)
-        hipLaunchKernelGGL(k_gemm_prep_q6<2>, dim3((unsigned)((nb + 31) / 32)), dim3(256), 0, s, x, xq, dyt, (int)m,
-                           (int)k, (int)mp);
-    else
-        hipLaunchKernelGGL(k_gemm_prep_q6<1>, dim3((unsigned)((nb + 15) / 16)), dim3(256), 0, s, x, xq, dyt, (int)m,
+        hipLaunchKernelGGL((k_gemm_prep_q6<2, 4>), dim3((unsigned)((nb + 31) / 32)), dim3(256), 0, s, x, xq, dyt,
+                           (int)m, (int)k, (int)mp);
+    else  // few blocks: one a wave (more waves in flight)
+        hipLaunchKernelGGL(k_gemm_prep_q6_wave, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, xq, dyt, (int)m,
                            (int)k, (int)mp);
     return hipGetLastError();
 }
@@ -507,7 +524,7 @@ __global__ __launch_bounds__(256) void k_q6p_prep(const float* __restrict__ x, i
     __shared__ uint32_t raw[4][256];
     const uint64_t b = blockIdx.x, T = gridDim.x;
     const uint32_t xi = (uint32_t)(b * xwg / T);
-    if ((uint32_t)((b + 1) * xwg / T) > xi) q6_prep_x<2>(x, xq, dyt, m, k, mp, xi);  // uniform
+    if ((uint32_t)((b + 1) * xwg / T) > xi) q6_prep_x<2, 4>(x, xq, dyt, m, k, mp, xi);  // uniform
     else q6_planes(W, planes, dwt, n, k, np, (uint32_t)b - xi, raw);
 }
 
