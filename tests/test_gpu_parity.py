@@ -301,7 +301,7 @@ def test_prefill_gemm_q8_0_shapes(L, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES + [(40, 33, 768), (300, 70, 1280), (200, 100, 8448), (129, 64, 4096),
-                                                 (520, 130, 2304), (2048, 136, 8192)])
+                                                 (520, 130, 2304), (2048, 136, 8192), (320, 70, 8192)])
 def test_prefill_gemm_q6k_shapes(L, m, n, k):
     """The Q6_K prefill GEMM on ragged tiles, an odd number of superblocks a
     row (rows then start 2 bytes off a 4-byte boundary), K split over
