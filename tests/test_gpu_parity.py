@@ -239,11 +239,12 @@ def test_prefill_same_sign_activations(L, dt, mma, m, kind):
 
 def _random_shapes(count, seed=20261202):
     """(dt, m, n, k) drawn across every routing band: m from each of
-    1-2, 3-4, 5-16, 17-64, 65-128 and 129-600 rows; k in whole blocks up to
+    1-2, 3-4, 5-16, 17-64, 65-128, 129-600 and 601-1100 rows (the last: the
+    int8 Q4_K route and the two-plane Q6_K route); k in whole blocks up to
     4608 (Q4_K / Q6_K in superblocks, Q8_0 in 32-element blocks); n ragged;
     m * n * k kept below 2.5e8 so the oracle stays fast."""
     rng = np.random.default_rng(seed)
-    bands = [(1, 2), (3, 4), (5, 16), (17, 64), (65, 128), (129, 600)]
+    bands = [(1, 2), (3, 4), (5, 16), (17, 64), (65, 128), (129, 600), (601, 1100)]
     out = []
     while len(out) < count:
         dt = [O.Q8_0, O.Q4K, O.Q6K][len(out) % 3]
@@ -261,7 +262,7 @@ def _random_shapes(count, seed=20261202):
 _SEEDS = int(os.environ.get("LLOOM_HIP_PARITY_SEEDS", "1"))
 
 
-@pytest.mark.parametrize("dt,m,n,k", [c for i in range(_SEEDS) for c in _random_shapes(54, seed=20261202 + i)])
+@pytest.mark.parametrize("dt,m,n,k", [c for i in range(_SEEDS) for c in _random_shapes(63, seed=20261202 + i)])
 def test_random_shapes_all_routes(L, dt, m, n, k):
     """Seeded random shapes through every route against the oracle."""
     rng = np.random.default_rng(m * 131 + n * 7 + k)
