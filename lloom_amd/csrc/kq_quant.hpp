@@ -131,4 +131,39 @@ __device__ __forceinline__ uint32_t q8_0_block_8lanes(float4 x, uint16_t* d16) {
     return packed;
 }
 
+// One wave quantizes block (mi, sb) of x [m][k] (Q8_K, bit-exact) into the
+// split layout: qs permuted so one MFMA lane group's 8 bytes of every
+// 32-element chunk are contiguous (or, tiled, into [mp/16][k/256][4][64][16]
+// so a 16-row tile's operand pieces are 1 KB each), d into dt[sb][mp], and,
+// with bsp, the eight 32-element sums as int8 (sum & 63, sum >> 6) into
+// bsp[sb][mp][16].
+__device__ __forceinline__ void q8k_split_block(const float* __restrict__ x, int8_t* __restrict__ qs,
+                                                float* __restrict__ dt, int8_t* __restrict__ bsp, int k, int mp,
+                                                int tiled, int mi, int sb, int lane) {
+    const int nsb = k >> 8;
+    const float4 v = *(const float4*)(x + (int64_t)mi * k + sb * 256 + 4 * lane);
+    float d;
+    int bs;
+    const uint32_t q = q8k_block_wave(v, &d, &bs);
+    // lane owns elements 4*lane..: sub-block lane/8, group (lane%8)/2, byte 4*(lane%2)
+    const int off = 64 * ((lane & 7) >> 1) + 8 * (lane >> 3) + 4 * (lane & 1);
+    if (tiled) {  // uniform
+        const int64_t piece = (((int64_t)(mi >> 4) * nsb + sb) * 4 + ((off >> 4) & 3)) * 64 + 16 * (off >> 6) + (mi & 15);
+        *(uint32_t*)(qs + piece * 16 + (off & 15)) = q;
+    } else {
+        *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + off) = q;
+    }
+    if (lane == 0) dt[(int64_t)sb * mp + mi] = d;
+    if (bsp) {
+        // bs is the 16-element sum of the lane's quad; the 8 lanes of
+        // sub-block lane / 8 are two quads
+        const int s32 = bs + dppi<DPP_HALF_MIRROR>(bs);
+        if ((lane & 7) == 0) {
+            int8_t* o = bsp + ((int64_t)sb * mp + mi) * 16 + (lane >> 3);
+            o[0] = (int8_t)(s32 & 63);
+            o[8] = (int8_t)(s32 >> 6);
+        }
+    }
+}
+
 }  // namespace lloom

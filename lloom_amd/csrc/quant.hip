@@ -49,33 +49,10 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float* __restrict__ 
 __global__ __launch_bounds__(256) void k_quantize_split_q8k(const float* __restrict__ x, int8_t* __restrict__ qs,
                                                             float* __restrict__ dt, int8_t* __restrict__ bsp, int m,
                                                             int k, int mp, int tiled) {
-    const int lane = threadIdx.x & 63;
     const int nsb = k >> 8;
     const int sb = blockIdx.y * 4 + (threadIdx.x >> 6), mi = blockIdx.x;
     if (sb >= nsb) return;
-    const float4 v = *(const float4*)(x + (int64_t)mi * k + sb * 256 + 4 * lane);
-    float d;
-    int bs;
-    const uint32_t q = q8k_block_wave(v, &d, &bs);
-    // lane owns elements 4*lane..: sub-block lane/8, group (lane%8)/2, byte 4*(lane%2)
-    const int off = 64 * ((lane & 7) >> 1) + 8 * (lane >> 3) + 4 * (lane & 1);
-    if (tiled) {  // uniform
-        const int64_t piece = (((int64_t)(mi >> 4) * nsb + sb) * 4 + ((off >> 4) & 3)) * 64 + 16 * (off >> 6) + (mi & 15);
-        *(uint32_t*)(qs + piece * 16 + (off & 15)) = q;
-    } else {
-        *(uint32_t*)(qs + (int64_t)mi * k + sb * 256 + off) = q;
-    }
-    if (lane == 0) dt[(int64_t)sb * mp + mi] = d;
-    if (bsp) {
-        // bs is the 16-element sum of the lane's quad; the 8 lanes of
-        // sub-block lane / 8 are two quads
-        const int s32 = bs + dppi<DPP_HALF_MIRROR>(bs);
-        if ((lane & 7) == 0) {
-            int8_t* o = bsp + ((int64_t)sb * mp + mi) * 16 + (lane >> 3);
-            o[0] = (int8_t)(s32 & 63);
-            o[8] = (int8_t)(s32 >> 6);
-        }
-    }
+    q8k_split_block(x, qs, dt, bsp, k, mp, tiled, mi, sb, threadIdx.x & 63);
 }
 
 static int64_t pad16(int64_t m) { return (m + 15) & ~(int64_t)15; }
