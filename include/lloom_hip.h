@@ -81,7 +81,7 @@ int lloom_hip_ctx_set_mv_rows_max(lloom_hip_ctx* ctx, int rows);
  *   the min term as one more MFMA;
  * LLOOM_HIP_MMA_INT8: v_mfma_i32_32x32x32_i8 with the weights split into
  *   two int8 planes (sc = 8 sc_hi + sc_lo);
- * LLOOM_HIP_MMA_AUTO (default): F16 up to 512 rows, INT8 past (each the
+ * LLOOM_HIP_MMA_AUTO (default): F16 up to 320 rows, INT8 past (each the
  *   faster there).
  * LLOOM_HIP_PREFILL_MMA=f16|int8|auto sets the default of new contexts.
  * No counterpart in the reference (its CUDA arm has one MMQ kernel). */

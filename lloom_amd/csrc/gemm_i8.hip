@@ -80,23 +80,32 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 256, WAVES = 8, THREADS = 64 * WAVES;
+constexpr int BM = 128, WAVES = 8, THREADS = 64 * WAVES;
 constexpr int REC = 40;  // bytes per (column, superblock) record: min hi[8], min lo[8] (fp16), sc[8]
-// LDS.  Weight slot: qs [256 columns][128 B] with piece p of column c at
-// slot p ^ (c & 7) (16 lanes reading one piece of 16 columns spread over the
-// banks), the records [256][40 B], d [256] f32, the eight 32-column groups'
-// dy scales [8] f32.  Activation half slot: x8 [16 pieces][64 rows][16 B],
-// S [64 rows][64 S_hi[8], S_lo[8]] fp16, dy [64] f32.
-constexpr int WQ_OFF = 0, REC_OFF = 32768, DT_OFF = REC_OFF + BN * REC, ES_OFF = DT_OFF + BN * 4;
-constexpr int W_SLOT = ES_OFF + 64;
+// LDS, for a tile of BN = 128 NCW weight columns (NCW = 2: each wave 32
+// columns; NCW = 1: 16).  Weight slot: qs [BN columns][128 B] with piece p
+// of column c at slot p ^ (c & 7) (16 lanes reading one piece of 16 columns
+// spread over the banks), the records [BN][40 B], d [BN] f32, the 32-column
+// groups' dy scales [BN / 32] f32.  Activation half slot: x8 [16 pieces][64
+// rows][16 B], S [64 rows][64 S_hi[8], S_lo[8]] fp16, dy [64] f32.
+constexpr int WQ_OFF = 0;
 constexpr int AX_OFF = 0, AS_OFF = 16384, AD_OFF = AS_OFF + 2048, A_HALF = AD_OFF + 256;
-constexpr int ALO_OFF = 2 * W_SLOT, AHI_OFF = ALO_OFF + 2 * A_HALF;
-constexpr int LDS = AHI_OFF + 2 * A_HALF;
-static_assert(LDS <= 160 * 1024, "staging layout");
-// DMA instructions a wave issues: weight slot 4 (qs) + 1 or 2 (records, d,
-// exponents); activation half 2 (x8) + 0 or 1 (S, dy).  The waits use the
-// smallest counts, which is stricter for the waves that issue more.
-constexpr int WAIT_START = 4 + 1 + 2, WAIT_HALF = 2;
+// DMA instructions a wave issues per weight slot: qs BN / 64, then the
+// records, d and exponents: NCW = 2 one or two, NCW = 1 none or one; per
+// activation half: x8 2 + S or dy 0 or 1.  The waits use the smallest
+// counts, which is stricter for the waves that issue more.
+constexpr int WAIT_HALF = 2;
+template <int NCW>
+struct I8C {
+    static constexpr int BN = 128 * NCW;
+    static constexpr int REC_OFF = BN * 128, DT_OFF = REC_OFF + BN * REC, ES_OFF = DT_OFF + BN * 4;
+    static constexpr int W_SLOT = ES_OFF + 64;
+    static constexpr int ALO_OFF = 2 * W_SLOT, AHI_OFF = ALO_OFF + 2 * A_HALF, LDS = AHI_OFF + 2 * A_HALF;
+    static constexpr int WAIT_START = NCW == 2 ? 4 + 1 + 2 : 2 + 0 + 2;
+    static_assert(LDS <= 160 * 1024, "staging layout");
+};
+// the workspace layout is sized by the wider tile
+constexpr int BN = I8C<2>::BN;
 
 // Each 16-bit half of q times f (both halves' products below 2^16).
 __device__ __forceinline__ int pk_mul(uint32_t q, uint32_t f2) {
@@ -114,9 +123,10 @@ __device__ __forceinline__ uint32_t byte_pair(uint32_t w, int b) {
 //   xq   int8 [mp/64][k/256][16 pieces][64 rows][16 B]  x8, piece p = elements 16p .. 16p+15
 //   s16  fp16 [k/256][mp][16]  64 S_hi_j then S_lo_j, S_j = bsums[2j] + bsums[2j+1]
 //   dyt  f32  [k/256][mp]
-//   rec  [np/256][k/256][256][40 B]  -dmin mn_j as fp16 hi[8], lo[8]; sc_j [8]
-//   dt   f32  [np/256][k/256][256]   d (times the group's 2^-e)
-//   es   f32  [np/256][k/256][8]     2^e of each 32-column group
+//   rec  [np/BN][k/256][BN][40 B]  -dmin mn_j as fp16 hi[8], lo[8]; sc_j [8]
+//   dt   f32  [np/BN][k/256][BN]   d (times the group's 2^-e)
+//   es   f32  [np/BN][k/256][BN/32]  2^e of each 32-column group
+// for the column tile width BN of the call (np a multiple of 256 either way)
 // with rows m .. mp-1 zero and columns n .. np-1 zero.
 struct I8Ptrs {
     int8_t* xq;
@@ -170,7 +180,7 @@ bool gemm_i8_fits(int64_t n, int64_t k, int64_t m) {
 // from_float (k_quants.rs:2400-2438).
 // Weight prep (the blocks after): one thread per (column, superblock), a
 // wave's lanes 64 consecutive columns of one superblock.
-template <int NB>
+template <int NB, int BNR>
 __global__ __launch_bounds__(256) void k_gemm_prep_i8(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                       I8Ptrs p, int m, int n, int k, int act_blocks) {
     const int lane = threadIdx.x & 63;
@@ -212,14 +222,14 @@ __global__ __launch_bounds__(256) void k_gemm_prep_i8(const float* __restrict__ 
             hi[j >> 1] = h2;
             lo[j >> 1] = l2;
         }
-        const int tile = col / BN, c = col % BN;
-        uint8_t* r = p.rec + (((int64_t)tile * nsb + sb) * BN + c) * REC;
+        const int tile = col / BNR, c = col % BNR;
+        uint8_t* r = p.rec + (((int64_t)tile * nsb + sb) * BNR + c) * REC;
         *(uint4*)(r) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         *(uint4*)(r + 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
         *(uint2*)(r + 32) = make_uint2(sc0, sc1);
-        p.dt[((int64_t)tile * nsb + sb) * BN + c] = d * down;
+        p.dt[((int64_t)tile * nsb + sb) * BNR + c] = d * down;
         if ((lane & 31) == 0)
-            p.es[((int64_t)tile * nsb + sb) * (BN / 32) + c / 32] = __builtin_bit_cast(float, (uint32_t)(127 + e) << 23);
+            p.es[((int64_t)tile * nsb + sb) * (BNR / 32) + c / 32] = __builtin_bit_cast(float, (uint32_t)(127 + e) << 23);
         return;
     }
     const int j = lane & 15;
@@ -263,8 +273,14 @@ __global__ __launch_bounds__(256) void k_gemm_prep_i8(const float* __restrict__ 
     }
 }
 
+template <int NCW>
 __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restrict__ W, I8Ptrs p,
                                                          float* __restrict__ Y, int m, int n, int k, int epi) {
+    // NCW 16-column halves a wave: a tile of 8 x 16 NCW weight columns
+    using C = I8C<NCW>;
+    constexpr int BN = C::BN, WC = 16 * NCW;
+    constexpr int REC_OFF = C::REC_OFF, DT_OFF = C::DT_OFF, ES_OFF = C::ES_OFF, W_SLOT = C::W_SLOT;
+    constexpr int ALO_OFF = C::ALO_OFF, AHI_OFF = C::AHI_OFF, WAIT_START = C::WAIT_START;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4, G = g >> 1;
@@ -293,8 +309,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
         const uint32_t st = lds0 + (uint32_t)slot * W_SLOT;
         const uint8_t* wb = W + (size_t)n0 * rowbytes + (uint32_t)sb * Q4K_BYTES + 16;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (part != i / 2) continue;
+        for (int i = 0; i < BN / 64; i++) {
+            if (part != (NCW == 2 ? i / 2 : i)) continue;
             const int q = wv + WAVES * i;  // 0 .. 31
             if (!ragged_n) {
                 dma16s(wb + (size_t)8 * q * rowbytes, qlane, st + WQ_OFF + 1024u * (uint32_t)q);
@@ -305,13 +321,21 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
             }
         }
         if (part != 2) return;
-        // records (10 KB), d (1 KB), group exponents (32 B): 12 more
-        // instructions, waves 0-3 two each, 4-7 one each
         const uint8_t* rb = recb + (size_t)sb * (BN * REC);
-        dma16s(rb + 1024u * (uint32_t)wv, lane16, st + REC_OFF + 1024u * (uint32_t)wv);
-        if (wv < 2) dma16s(rb + 1024u * (uint32_t)(8 + wv), lane16, st + REC_OFF + 1024u * (uint32_t)(8 + wv));
-        if (wv == 2) dma16s(dtb + (size_t)sb * (BN * 4), lane16, st + DT_OFF);
-        if (wv == 3 && lane < 8) dma4s(esb + (size_t)sb * 32, 4u * (uint32_t)lane, st + ES_OFF);
+        if constexpr (NCW == 2) {
+            // records (10 KB), d (1 KB), group exponents (32 B): 12 more
+            // instructions, waves 0-3 two each, 4-7 one each
+            dma16s(rb + 1024u * (uint32_t)wv, lane16, st + REC_OFF + 1024u * (uint32_t)wv);
+            if (wv < 2) dma16s(rb + 1024u * (uint32_t)(8 + wv), lane16, st + REC_OFF + 1024u * (uint32_t)(8 + wv));
+            if (wv == 2) dma16s(dtb + (size_t)sb * (BN * 4), lane16, st + DT_OFF);
+            if (wv == 3 && lane < 8) dma4s(esb + (size_t)sb * 32, 4u * (uint32_t)lane, st + ES_OFF);
+        } else {
+            // records 5 KB (waves 0-4), d 512 B (wave 5, lanes 0-31),
+            // exponents 16 B (wave 6)
+            if (wv < 5) dma16s(rb + 1024u * (uint32_t)wv, lane16, st + REC_OFF + 1024u * (uint32_t)wv);
+            if (wv == 5 && lane < 32) dma16s(dtb + (size_t)sb * (BN * 4), lane16, st + DT_OFF);
+            if (wv == 6 && lane < 4) dma4s(esb + (size_t)sb * 16, 4u * (uint32_t)lane, st + ES_OFF);
+        }
     };
     // activation rows 64 hf .. 64 hf + 63: x8 16 KB (two instructions a
     // wave), S 2 KB (waves 4, 5), dy 256 B (wave 6)
@@ -330,19 +354,19 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
         if (wv == 6) dma4s((const uint8_t*)(p.dyt + row0), 4u * (uint32_t)lane, st + AD_OFF);
     };
 
-    v4f out[8][2];
+    v4f out[8][NCW];
 #pragma unroll
     for (int r = 0; r < 8; r++)
 #pragma unroll
-        for (int c = 0; c < 2; c++) out[r][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < NCW; c++) out[r][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     // per-wave state of the superblock whose planes are built
-    v4i plo[2][4], phi[2][4];
-    v8h amin[2];
-    v4f dv[2];
+    v4i plo[NCW][4], phi[NCW][4];
+    v8h amin[NCW];
+    v4f dv[NCW];
     float esc = 1.0f;
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
+    for (int c = 0; c < NCW; c++) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) plo[c][ks] = phi[c][ks] = v4i{0, 0, 0, 0};
         amin[c] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
@@ -352,17 +376,17 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
     // planes of a superblock from weight slot `slot` (the wave's 32 columns)
     auto build = [&](int slot) {
         const int sw = slot * W_SLOT;
-        esc = *(const float*)(smem + sw + ES_OFF + 4 * wv);
+        esc = *(const float*)(smem + sw + ES_OFF + 4 * ((WC * wv) >> 5));
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int col = 32 * wv + 16 * c + l16;
+        for (int c = 0; c < NCW; c++) {
+            const int col = WC * wv + 16 * c + l16;
             const uint8_t* cq = smem + sw + WQ_OFF + 128 * col;
             const uint4 r0 = *(const uint4*)(cq + 16 * (g ^ (col & 7)));
             const uint4 r1 = *(const uint4*)(cq + 16 * ((4 + g) ^ (col & 7)));
             const uint8_t* rc = smem + sw + REC_OFF + REC * col;
             amin[c] = *(const v8h*)(rc + 16 * G);
             const uint2 scb = *(const uint2*)(rc + 32);
-            dv[c] = *(const v4f*)(smem + sw + DT_OFF + 4 * (32 * wv + 16 * c + 4 * g));
+            dv[c] = *(const v4f*)(smem + sw + DT_OFF + 4 * (WC * wv + 16 * c + 4 * g));
             // the lane's four scales: sub-blocks 2G, 2G + 1, 4 + 2G, 5 + 2G (steps 0..3)
             const uint32_t s4 = __builtin_amdgcn_perm(scb.y, scb.x, G ? 0x07060302u : 0x05040100u);
             const uint32_t s0w = s4 & 0x07070707u, s1w = (s4 >> 3) & 0x07070707u;
@@ -423,31 +447,61 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
         v4f dm1;
         float dy1 = 0.0f;
         load_b(0, bx);
+        if constexpr (NCW == 2) {
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-            const int ml = 16 * rr + l16;
-            v4i bn[4];
-            if (rr < 3) load_b(rr + 1, bn);
-            const v8h sv = *(const v8h*)(smem + ah + AS_OFF + 32 * ml + 16 * (g & 1));
-            const float dy = *(const float*)(smem + ah + AD_OFF + 4 * ml) * ys;
-            v4i lo0, hi0;
-            v4f dm0;
-            mfmas(0, bx, sv, lo0, hi0, dm0);
-            if (rr > 0) epi(R0 + rr - 1, 1, lo1, hi1, dm1, dy1);
-            mfmas(1, bx, sv, lo1, hi1, dm1);
-            epi(R0 + rr, 0, lo0, hi0, dm0, dy);
-            dy1 = dy;
-            if (rr > 0)
-                asm volatile("" : "+v"(out[R0 + rr - 1][1]), "+v"(out[R0 + rr][0]));
-            else
-                asm volatile("" : "+v"(out[R0 + rr][0]));
-            hook(rr);
-            if (rr < 3)
+            for (int rr = 0; rr < 4; rr++) {
+                const int ml = 16 * rr + l16;
+                v4i bn[4];
+                if (rr < 3) load_b(rr + 1, bn);
+                const v8h sv = *(const v8h*)(smem + ah + AS_OFF + 32 * ml + 16 * (g & 1));
+                const float dy = *(const float*)(smem + ah + AD_OFF + 4 * ml) * ys;
+                v4i lo0, hi0;
+                v4f dm0;
+                mfmas(0, bx, sv, lo0, hi0, dm0);
+                if (rr > 0) epi(R0 + rr - 1, 1, lo1, hi1, dm1, dy1);
+                mfmas(1, bx, sv, lo1, hi1, dm1);
+                epi(R0 + rr, 0, lo0, hi0, dm0, dy);
+                dy1 = dy;
+                if (rr > 0)
+                    asm volatile("" : "+v"(out[R0 + rr - 1][1]), "+v"(out[R0 + rr][0]));
+                else
+                    asm volatile("" : "+v"(out[R0 + rr][0]));
+                hook(rr);
+                if (rr < 3)
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++) bx[ks] = bn[ks];
+                    for (int ks = 0; ks < 4; ks++) bx[ks] = bn[ks];
+            }
+            epi(R0 + 3, 1, lo1, hi1, dm1, dy1);
+            asm volatile("" : "+v"(out[R0 + 3][1]));
+        } else {
+            // one 16-column half: row block rr's MFMAs run beside the
+            // epilogue of rr - 1
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+                const int ml = 16 * rr + l16;
+                v4i bn[4];
+                if (rr < 3) load_b(rr + 1, bn);
+                const v8h sv = *(const v8h*)(smem + ah + AS_OFF + 32 * ml + 16 * (g & 1));
+                const float dy = *(const float*)(smem + ah + AD_OFF + 4 * ml) * ys;
+                v4i lo0, hi0;
+                v4f dm0;
+                mfmas(0, bx, sv, lo0, hi0, dm0);
+                if (rr > 0) {
+                    epi(R0 + rr - 1, 0, lo1, hi1, dm1, dy1);
+                    asm volatile("" : "+v"(out[R0 + rr - 1][0]));
+                }
+                lo1 = lo0;
+                hi1 = hi0;
+                dm1 = dm0;
+                dy1 = dy;
+                hook(rr);
+                if (rr < 3)
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++) bx[ks] = bn[ks];
+            }
+            epi(R0 + 3, 0, lo1, hi1, dm1, dy1);
+            asm volatile("" : "+v"(out[R0 + 3][0]));
         }
-        epi(R0 + 3, 1, lo1, hi1, dm1, dy1);
-        asm volatile("" : "+v"(out[R0 + 3][1]));
     };
 
     // workgroup barrier after this wave's own waits; the empty asm keeps the
@@ -515,8 +569,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
         if (row >= m) continue;
         float* yr = Y + (int64_t)row * n;
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int col = n0 + 32 * wave + 16 * c + 4 * g;
+        for (int c = 0; c < NCW; c++) {
+            const int col = n0 + WC * wave + 16 * c + 4 * g;
             if (epi == EPI_STORE && col + 3 < n) {
                 *(float4*)(yr + col) = make_float4(out[R][c][0], out[R][c][1], out[R][c][2], out[R][c][3]);
             } else {
@@ -528,27 +582,43 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
     }
 }
 
-hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
-                          int epi, hipStream_t s) {
-    if (hipError_t e = set_lds_limit((const void*)k_gemm_q4k_i8, LDS)) return e;
+// The 128-column tiling is used while its grid fits one workgroup a CU (at
+// most 256, so the 256-column one leaves at least half the CUs idle): one
+// workgroup holds a CU either way (LDS), and a 128-column one takes ~0.7 of
+// the time of a 256-column one (C3 shape, m 256 / 512: 26 / 29 us against
+// 40 / 42), so past one round the 256-column tiling's fewer rounds win.
+constexpr int64_t I8_NARROW_MAX = 128;
+
+template <int NCW>
+static hipError_t launch_i8(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
+                            int epi, hipStream_t s) {
+    constexpr int BNT = I8C<NCW>::BN, LDST = I8C<NCW>::LDS;
+    if (hipError_t e = set_lds_limit((const void*)k_gemm_q4k_i8<NCW>, LDST)) return e;
     const I8Ptrs p = i8_ptrs(ws, n, m, k);
     const int64_t nsb = k / 256;
     const int64_t wblocks = p.np * nsb / 256;
     if (nsb % 2 == 0) {
         const int64_t ablocks = (p.mp / 4 * (nsb / 2) + 3) / 4;
-        hipLaunchKernelGGL(k_gemm_prep_i8<2>, dim3((unsigned)(ablocks + wblocks)), dim3(256), 0, s, x,
+        hipLaunchKernelGGL((k_gemm_prep_i8<2, BNT>), dim3((unsigned)(ablocks + wblocks)), dim3(256), 0, s, x,
                            (const uint8_t*)w, p, (int)m, (int)n, (int)k, (int)ablocks);
     } else {
         const int64_t ablocks = (p.mp / 4 * nsb + 3) / 4;
-        hipLaunchKernelGGL(k_gemm_prep_i8<1>, dim3((unsigned)(ablocks + wblocks)), dim3(256), 0, s, x,
+        hipLaunchKernelGGL((k_gemm_prep_i8<1, BNT>), dim3((unsigned)(ablocks + wblocks)), dim3(256), 0, s, x,
                            (const uint8_t*)w, p, (int)m, (int)n, (int)k, (int)ablocks);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const unsigned grid = (unsigned)((p.mp / BM) * ((n + BN - 1) / BN));
-    hipLaunchKernelGGL(k_gemm_q4k_i8, dim3(grid), dim3(THREADS), LDS, s, (const uint8_t*)w, p, y, (int)m, (int)n,
-                       (int)k, epi);
+    const unsigned grid = (unsigned)((p.mp / BM) * ((n + BNT - 1) / BNT));
+    hipLaunchKernelGGL(k_gemm_q4k_i8<NCW>, dim3(grid), dim3(THREADS), LDST, s, (const uint8_t*)w, p, y, (int)m,
+                       (int)n, (int)k, epi);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_i8(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m, void* ws,
+                          int epi, hipStream_t s) {
+    const int64_t mp = i8_ptrs(ws, n, m, k).mp;
+    if ((mp / BM) * ((n + BN - 1) / BN) <= I8_NARROW_MAX) return launch_i8<1>(w, x, y, n, k, m, ws, epi, s);
+    return launch_i8<2>(w, x, y, n, k, m, ws, epi, s);
 }
 
 }  // namespace lloom

@@ -53,10 +53,11 @@ hipError_t launch_mq(int type, const void* w, const float* x, float* y, int64_t 
 // operands on fp16 MFMA, or GEMM_INT8, two int8 scale planes), the
 // other types through decode tiles; qbuf is workspace for the prepared x.
 constexpr int GEMM_F16 = 0, GEMM_INT8 = 1, GEMM_AUTO = 2;
-// GEMM_AUTO's choice: the fp16 route to 512 rows (m = 512 on [8192, 2048]:
-// 40.2 against 47.3 us), the int8 planes past (m = 768 49.5 / 51.8, 1024
-// 53.7 / 57.2, 2048 101.5 / 104.0)
-constexpr int64_t GEMM_AUTO_INT8_ROWS = 512;
+// GEMM_AUTO's choice: the fp16 route to 320 rows (m = 256 on [8192, 2048]:
+// 27.2 against 32.2 us), the int8 planes past (fp16 / int8: m = 352 33.8 /
+// 33.5, 512 36.8 / 35.5, 768 52.1 / 50.4, 1024 56.1 / 54.9, 2048 108.8 /
+// 102.4)
+constexpr int64_t GEMM_AUTO_INT8_ROWS = 320;
 inline int gemm_mode(int mode, int64_t m) {
     return mode == GEMM_AUTO ? (m > GEMM_AUTO_INT8_ROWS ? GEMM_INT8 : GEMM_F16) : mode;
 }

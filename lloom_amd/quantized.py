@@ -144,7 +144,7 @@ MMA_F16, MMA_INT8, MMA_AUTO = 0, 1, 2
 def set_prefill_mma(mode, device=0):
     """Matrix-core family of the Q4_K prefill GEMM: MMA_F16 (the exact
     integer operands on fp16 MFMA), MMA_INT8 (two int8 scale planes) or
-    MMA_AUTO (the default: F16 up to 512 rows, INT8 past).  All compute the
+    MMA_AUTO (the default: F16 up to 320 rows, INT8 past).  All compute the
     CPU arm's integer sums exactly."""
     check(lib().lloom_hip_ctx_set_prefill_mma(_ctx(device), mode))
 

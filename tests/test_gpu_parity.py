@@ -142,7 +142,10 @@ def test_qmatmul_matches_oracle(L, dt, m):
 
 GEMM_SHAPES = [(17, 1, 256), (64, 128, 2048), (100, 7, 768), (128, 300, 512), (96, 200, 2048), (129, 40, 2048),
                (64, 8200, 512), (128, 8200, 256), (200, 129, 1024), (1030, 130, 512), (257, 64, 256),
-               (512, 256, 2048), (129, 520, 768), (256, 1000, 2048)]
+               (512, 256, 2048), (129, 520, 768), (256, 1000, 2048),
+               # int8 planes: more than 128 workgroups of 128 x 256, so the
+               # 256-column tiling (the shapes above take the 128-column one)
+               (520, 8200, 512), (1100, 4100, 256)]
 
 
 @pytest.mark.parametrize("m,n,k,mma", [s + (mma,) for s in GEMM_SHAPES for mma in ("f16", "int8")])
@@ -235,6 +238,25 @@ def test_prefill_same_sign_activations(L, dt, mma, m, kind):
     finally:
         set_prefill_mma(MMA_AUTO)
     assert_rows_close(y, O.matmul(dt, x, q, n), what=f"same-sign {kind} dt={dt} {mma} m={m}")
+
+
+@pytest.mark.parametrize("kind", ["bias", "negbias", "ones", "outlier"])
+def test_prefill_int8_wide_tiles_same_sign(L, kind):
+    """The int8 planes' 256-column tiling (more than 128 workgroups of
+    128 x 256; the shapes above take the 128-column one) on the same
+    large-sum activations, ragged in m and n."""
+    from lloom_amd.quantized import MMA_AUTO, MMA_INT8, set_prefill_mma
+
+    m, n, k = 1100, 4100, 256
+    rng = np.random.default_rng(len(kind) + 5)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = _same_sign_inputs(kind, m, k, rng)
+    set_prefill_mma(MMA_INT8)
+    try:
+        y, q = _qmm(L, O.Q4K, w, x)
+    finally:
+        set_prefill_mma(MMA_AUTO)
+    assert_rows_close(y, O.matmul(O.Q4K, x, q, n), what=f"int8 wide tiles same-sign {kind}")
 
 
 def _random_shapes(count, seed=20261202):
