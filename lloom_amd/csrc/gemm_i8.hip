@@ -474,33 +474,62 @@ __global__ __launch_bounds__(THREADS) void k_gemm_q4k_i8(const uint8_t* __restri
             epi(R0 + 3, 1, lo1, hi1, dm1, dy1);
             asm volatile("" : "+v"(out[R0 + 3][1]));
         } else {
-            // one 16-column half: row block rr's MFMAs run beside the
-            // epilogue of rr - 1
+            // one 16-column half, two row blocks a step: their four MFMA
+            // chains interleave, and the previous step's two epilogues run
+            // beside them
+            v4i bx2[4], lo1b, hi1b;
+            v4f dm1b;
+            float dy1b = 0.0f;
+            load_b(1, bx2);
 #pragma unroll
-            for (int rr = 0; rr < 4; rr++) {
-                const int ml = 16 * rr + l16;
-                v4i bn[4];
-                if (rr < 3) load_b(rr + 1, bn);
+            for (int rp = 0; rp < 2; rp++) {
+                const int r0 = 2 * rp;
+                v4i bn[4], bn2[4];
+                if (rp == 0) {
+                    load_b(2, bn);
+                    load_b(3, bn2);
+                }
+                const int ml = 16 * r0 + l16;
                 const v8h sv = *(const v8h*)(smem + ah + AS_OFF + 32 * ml + 16 * (g & 1));
+                const v8h sv2 = *(const v8h*)(smem + ah + AS_OFF + 32 * (ml + 16) + 16 * (g & 1));
                 const float dy = *(const float*)(smem + ah + AD_OFF + 4 * ml) * ys;
-                v4i lo0, hi0;
-                v4f dm0;
-                mfmas(0, bx, sv, lo0, hi0, dm0);
-                if (rr > 0) {
-                    epi(R0 + rr - 1, 0, lo1, hi1, dm1, dy1);
-                    asm volatile("" : "+v"(out[R0 + rr - 1][0]));
+                const float dy2 = *(const float*)(smem + ah + AD_OFF + 4 * (ml + 16)) * ys;
+                v4i lo0 = v4i{0, 0, 0, 0}, hi0 = lo0, lo0b = lo0, hi0b = lo0;
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    lo0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(plo[0][ks], bx[ks], lo0, 0, 0, 0);
+                    lo0b = __builtin_amdgcn_mfma_i32_16x16x64_i8(plo[0][ks], bx2[ks], lo0b, 0, 0, 0);
+                    hi0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(phi[0][ks], bx[ks], hi0, 0, 0, 0);
+                    hi0b = __builtin_amdgcn_mfma_i32_16x16x64_i8(phi[0][ks], bx2[ks], hi0b, 0, 0, 0);
+                }
+                const v4f z = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                const v4f dm0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin[0], sv, z, 0, 0, 0);
+                const v4f dm0b = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin[0], sv2, z, 0, 0, 0);
+                if (rp > 0) {
+                    epi(R0 + r0 - 2, 0, lo1, hi1, dm1, dy1);
+                    epi(R0 + r0 - 1, 0, lo1b, hi1b, dm1b, dy1b);
+                    asm volatile("" : "+v"(out[R0 + r0 - 2][0]), "+v"(out[R0 + r0 - 1][0]));
                 }
                 lo1 = lo0;
                 hi1 = hi0;
                 dm1 = dm0;
                 dy1 = dy;
-                hook(rr);
-                if (rr < 3)
+                lo1b = lo0b;
+                hi1b = hi0b;
+                dm1b = dm0b;
+                dy1b = dy2;
+                hook(r0);
+                hook(r0 + 1);
+                if (rp == 0)
 #pragma unroll
-                    for (int ks = 0; ks < 4; ks++) bx[ks] = bn[ks];
+                    for (int ks = 0; ks < 4; ks++) {
+                        bx[ks] = bn[ks];
+                        bx2[ks] = bn2[ks];
+                    }
             }
-            epi(R0 + 3, 0, lo1, hi1, dm1, dy1);
-            asm volatile("" : "+v"(out[R0 + 3][0]));
+            epi(R0 + 2, 0, lo1, hi1, dm1, dy1);
+            epi(R0 + 3, 0, lo1b, hi1b, dm1b, dy1b);
+            asm volatile("" : "+v"(out[R0 + 2][0]), "+v"(out[R0 + 3][0]));
         }
     };
 
