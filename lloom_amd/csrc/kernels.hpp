@@ -43,6 +43,14 @@ constexpr int MV_DMA_MA_MAX_ROWS = 128;
 bool mv_dma_ma_fits(int type, int64_t k, int64_t m);
 hipError_t launch_mv_dma_ma(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                             void* ws, int epi, hipStream_t s);
+// stream.hip: Q4_K with 2..16 rows on weights of at least
+// LLOOM_HIP_STREAM_MIN_MB (default 24) MB, k = 4096, 6144 or 8192 (and
+// k = 2048 with 2..4 rows):
+// the persistent pipelined MFMA decode kernel (the split quantizer in its
+// tiled layout, then one launch; workspace split_q8k_bytes).
+bool mv_stream_fits(int type, int64_t n, int64_t k, int64_t m);
+hipError_t launch_mv_stream(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
+                            void* ws, int epi, hipStream_t s);
 // matvec.hip: Q4_K / Q6_K with any number of rows on the MFMA decode kernel,
 // 64 activation rows per workgroup layer (the weights are re-read per
 // layer): the workspace quantizer, then one launch.

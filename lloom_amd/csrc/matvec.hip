@@ -382,112 +382,8 @@ __global__ __launch_bounds__(64 * WV) void k_matvec(const uint8_t* __restrict__ 
 // k_quantize_split_q8k, laid out so a lane's 64 bytes of a superblock (its
 // 8 bytes of each chunk) are contiguous: one A tile serves NT weight tiles.
 // The loads of a wave's next superblock are issued before the current one
-// is computed.
-// q6 (0..63) per byte -> q6 - 32 as int8: t = q6 ^ 32 is q6 - 32 in 6-bit
-// two's complement; copying bit 5 into bits 6 and 7 (0x20 * 6 = 0xC0, no
-// carry between bytes) sign-extends it to 8 bits.
-__device__ __forceinline__ uint32_t q6_to_i8(uint32_t q6) {
-    const uint32_t t = q6 ^ 0x20202020u;
-    return t | ((t & 0x20202020u) * 6u);
-}
-
-// One superblock of one 16-row tile: returns the f32 contributions of the
-// lane's four outputs.
-template <int TYPE>
-__device__ __forceinline__ void mf_compute(const MfW<TYPE>& w, const long (&a)[8], const float4& dy, int g,
-                                           float (&out)[4]) {
-    const v4i zero = {0, 0, 0, 0};
-    if constexpr (TYPE == T_Q4K) {
-        const float d = f16_to_f32(w.hdr.x & 0xffffu), dmin = f16_to_f32(w.hdr.x >> 16);
-        v4i accs = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int sc, mn;
-            if (j < 4) {
-                sc = byte_of(w.hdr.y, j) & 63;
-                mn = byte_of(w.hdr.z, j) & 63;
-            } else {
-                sc = (byte_of(w.hdr.w, j - 4) & 0xF) | ((byte_of(w.hdr.y, j - 4) >> 6) << 4);
-                mn = (byte_of(w.hdr.w, j - 4) >> 4) | ((byte_of(w.hdr.z, j - 4) >> 6) << 4);
-            }
-            const int c = j >> 1, sh = (j & 1) * 4;
-            const uint32_t lo = (w.q[c].x >> sh) & 0x0F0F0F0Fu, hi = (w.q[c].y >> sh) & 0x0F0F0F0Fu;
-            const long bw = (long)(((uint64_t)hi << 32) | lo);
-            const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
-            const uint32_t mrep = (uint32_t)mn * 0x01010101u;
-            const long bm = (long)(((uint64_t)mrep << 32) | mrep);
-            accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bm, accm, 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < 4; t++) accs[t] += __mul24(sc, dj[t]);
-        }
-        out[0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
-        out[1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
-        out[2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
-        out[3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
-    } else {
-        const float d = f16_to_f32(w.d);
-        const bool lo_half = g < 2;  // this lane's k range is sub-block 2j, else 2j + 1
-        v4i accs = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int h = j >> 2, gq = j & 3, c = 2 * h + (gq & 1);
-            const uint32_t nx = gq < 2 ? (w.ql[c].x & 0x0F0F0F0Fu) : ((w.ql[c].x >> 4) & 0x0F0F0F0Fu);
-            const uint32_t ny = gq < 2 ? (w.ql[c].y & 0x0F0F0F0Fu) : ((w.ql[c].y >> 4) & 0x0F0F0F0Fu);
-            const uint32_t hx = (w.qh[h].x >> (2 * gq)) & 0x03030303u, hy = (w.qh[h].y >> (2 * gq)) & 0x03030303u;
-            const uint32_t vx = q6_to_i8(nx | (hx << 4)), vy = q6_to_i8(ny | (hy << 4));
-            const long bw = (long)(((uint64_t)vy << 32) | vx);
-            const v4i da = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], lo_half ? bw : 0l, zero, 0, 0, 0);
-            const v4i db = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], lo_half ? 0l : bw, zero, 0, 0, 0);
-            // scales[2j], scales[2j + 1]: dword j / 2, bytes 2(j & 1) and 2(j & 1) + 1
-            const uint32_t sw = j < 2 ? w.sc.x : j < 4 ? w.sc.y : j < 6 ? w.sc.z : w.sc.w;
-            const int sa = (int)(int8_t)byte_of(sw, 2 * (j & 1)), sb = (int)(int8_t)byte_of(sw, 2 * (j & 1) + 1);
-#pragma unroll
-            for (int t = 0; t < 4; t++) accs[t] += __mul24(sa, da[t]) + __mul24(sb, db[t]);
-        }
-        out[0] += (d * dy.x) * (float)accs[0];
-        out[1] += (d * dy.y) * (float)accs[1];
-        out[2] += (d * dy.z) * (float)accs[2];
-        out[3] += (d * dy.w) * (float)accs[3];
-    }
-}
-
-// mf_compute's Q4_K arithmetic with the min term on two MFMAs instead of
-// eight: bsum_j = sum of the 32 quantized x of sub-block j = 64 hi_j + lo_j
-// (both int8, from k_quantize_split_q8k's bsp); the activation operand `ab`
-// holds lo_0..7 in lane group 0 and hi_0..7 in group 1 (zero in 2, 3), the
-// weight operand the eight 6-bit mins in group 0 (for the lo sums) or group
-// 1 (for the hi sums), so sum_j m_j bsum_j = D(lo) + 64 D(hi), exact.  The
-// scales and mins are unpacked as whole dwords (scales 0-3 are bytes of
-// hdr.y & 0x3f..., 4-7 are the low nibbles of hdr.w with hdr.y's top bits).
-// Every integer sum equals mf_compute's, so do the outputs.
-__device__ __forceinline__ void mf_compute_q4k_b(const MfW<T_Q4K>& w, const long (&a)[8], long ab, const float4& dy,
-                                                 int g, float (&out)[4]) {
-    const v4i zero = {0, 0, 0, 0};
-    const float d = f16_to_f32(w.hdr.x & 0xffffu), dmin = f16_to_f32(w.hdr.x >> 16);
-    const uint32_t sc_lo = w.hdr.y & 0x3F3F3F3Fu, sc_hi = (w.hdr.w & 0x0F0F0F0Fu) | ((w.hdr.y >> 2) & 0x30303030u);
-    const uint32_t mn_lo = w.hdr.z & 0x3F3F3F3Fu,
-                   mn_hi = ((w.hdr.w >> 4) & 0x0F0F0F0Fu) | ((w.hdr.z >> 2) & 0x30303030u);
-    const long mins = (long)(((uint64_t)mn_hi << 32) | mn_lo);
-    v4i accs = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int sc = (int)byte_of(j < 4 ? sc_lo : sc_hi, j & 3);
-        const int c = j >> 1, sh = (j & 1) * 4;
-        const uint32_t lo = (w.q[c].x >> sh) & 0x0F0F0F0Fu, hi = (w.q[c].y >> sh) & 0x0F0F0F0Fu;
-        const long bw = (long)(((uint64_t)hi << 32) | lo);
-        const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], bw, zero, 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; t++) accs[t] += __mul24(sc, dj[t]);
-    }
-    v4i mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ab, g == 1 ? mins : 0l, zero, 0, 0, 0);
-#pragma unroll
-    for (int t = 0; t < 4; t++) mh[t] <<= 6;
-    const v4i accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(ab, g == 0 ? mins : 0l, mh, 0, 0, 0);
-    out[0] += dy.x * ((float)accs[0] * d - (float)accm[0] * dmin);
-    out[1] += dy.y * ((float)accs[1] * d - (float)accm[1] * dmin);
-    out[2] += dy.z * ((float)accs[2] * d - (float)accm[2] * dmin);
-    out[3] += dy.w * ((float)accs[3] * d - (float)accm[3] * dmin);
-}
+// is computed.  The per-superblock arithmetic (mf_compute,
+// mf_compute_q4k_b) is in kq_mfma.hpp.
 
 // MA > 1 (prefill): a workgroup layer (grid y) covers MA 16-row activation
 // tiles against the same weight tiles, so each weight superblock is unpacked
@@ -834,6 +730,7 @@ static int mv_splits(int64_t n, int64_t k) {
 }
 
 size_t matvec_workspace_bytes(int type, int64_t n, int64_t k, int64_t m) {
+    if (mv_stream_fits(type, n, k, m)) return (split_q8k_bytes(k, m) + 255) & ~(size_t)255;
     if (type == T_Q8_0 || m <= MV_DOT_MAX_ROWS) return 0;
     const size_t q = (split_q8k_bytes(k, m) + 255) & ~(size_t)255;
     const int sp = mv_splits(n, k);
@@ -1126,6 +1023,8 @@ static bool mv_dot(int type, int64_t n, int64_t k, int64_t m) {
 
 hipError_t launch_matvec(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                          void* ws, int epi, hipStream_t s) {
+    // large Q4_K weights: the persistent streaming kernel
+    if (mv_stream_fits(type, n, k, m)) return launch_mv_stream(type, w, x, y, n, k, m, ws, epi, s);
     if (type != T_Q8_0 && !mv_dot(type, n, k, m) && m <= FUSED_MAX_ROWS && (k == 2048 || k == 1024))
         return type == T_Q4K ? launch_fused<T_Q4K>(w, x, y, n, k, m, epi, s)
                              : launch_fused<T_Q6K>(w, x, y, n, k, m, epi, s);
