@@ -264,19 +264,21 @@ static int64_t stream_min_bytes() {
     return v;
 }
 
-// Measured on rotating copies: Q4_K [28672, 8192] (132 MB) 35.5-38.3 us at
-// B = 2..16 against 44-60 us on the split-K MFMA kernel; at B = 1 the dot4
-// kernel keeps it (28.4 against 35.7 us).  At k = 2048 ([57344, 2048],
-// 66 MB) it takes B = 2..4 (24.5-25.0 us against 25.4 on the dot4 kernel
-// and 32.9 on the fused MFMA kernel); from 5 rows the one-shot DMA kernel
-// k_mv_dma_ma is faster (B = 16 22.6 against 26.9 us).
+// Where it wins (measured on rotating copies, against the kernels that take
+// the call otherwise): from 4 rows at k = 4096 .. 8192 and 24 MB up ([14336,
+// 4096] B = 4 / 16: 17.9 / 18.1 against 19.1 / 20.6 us; [57344, 4096]
+// 38.6 / 40.1 against 55.7 / 60.3), 2-3 rows only from ~96 MB ([28672, 8192]
+// B = 2 36.0 against 44.1 us; at 54-63 MB it ties or loses), and at k = 2048
+// 2-4 rows from ~48 MB ([57344, 2048] B = 4 25.4 against 32.9 us; from 5
+// rows k_mv_dma_ma is faster).  One row stays on the dot4 kernel.
 bool mv_stream_fits(int type, int64_t n, int64_t k, int64_t m) {
     const int64_t minb = stream_min_bytes();
     if (type != T_Q4K || minb <= 0 || m < 2 || m > 16 || n < 16) return false;
     if (k % 2048 || k > 4 * 2048 || (k == 2048 && m > 4)) return false;
-    if (n * (k / 256) * Q4K_BYTES < minb) return false;
-    // 32-bit DMA offsets within a tile, int row indices
-    return n < ((int64_t)1 << 30);
+    const int64_t bytes = n * (k / 256) * Q4K_BYTES;
+    if (k == 2048) return bytes >= 2 * minb && n < ((int64_t)1 << 30);
+    if (m < 4) return bytes >= 4 * minb && n < ((int64_t)1 << 30);
+    return bytes >= minb && n < ((int64_t)1 << 30);
 }
 
 template <int S>

@@ -50,18 +50,19 @@ def _x(seed, m, k):
     return x
 
 
-# (n, k): every k the kernel takes (S = k / 2048 superblocks a wave), each
-# above the 24 MB threshold, with n not a multiple of 16 (the last tile is
-# shifted back and stores only its new rows) where it matters
-SHAPES = [(24581, 2048), (12301, 4096), (8200, 6144), (5470, 8192)]
+# (n, k, m): every k the kernel takes (S = k / 2048 superblocks a wave) and
+# each row-count rule, with n not a multiple of 16 (the last tile is shifted
+# back and stores only its new rows)
+CASES = [(43701, 2048, 2), (43701, 2048, 4), (12301, 4096, 4), (12301, 4096, 16), (8200, 6144, 5),
+         (8200, 6144, 16), (5470, 8192, 16), (21847, 8192, 2), (21847, 8192, 3)]
 
 
-@pytest.mark.parametrize("n,k", SHAPES)
-@pytest.mark.parametrize("m", [2, 3, 4, 16])
+@pytest.mark.parametrize("n,k,m", CASES)
 def test_stream_matches_oracle(L, n, k, m):
     w = _weights(n + k, n, k)
     qt = L.QTensor.quantize(torch.from_numpy(w).cuda(), L.GgmlDType.Q4K)
-    assert qt.packed_bytes() >= 24 << 20
+    mib = qt.packed_bytes() / 2**20
+    assert mib >= (48 if k == 2048 else 96 if m < 4 else 24)
     x = _x(m * 7 + k, m, k)
     y = L.QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
     _rows_close(y, O.matmul(O.Q4K, x, qt.data(), n), f"stream n={n} k={k} m={m}")
@@ -70,7 +71,7 @@ def test_stream_matches_oracle(L, n, k, m):
 def test_stream_rows_batch_invariant_and_repeatable(L):
     """Each activation row is computed on its own and the eight waves'
     partial sums meet in a fixed order: a row's output is the same bits in
-    a batch of 2 or of 16, and from call to call."""
+    a batch of 4 or of 16, and from call to call."""
     n, k = 5470, 8192
     w = _weights(5, n, k)
     qt = L.QTensor.quantize(torch.from_numpy(w).cuda(), L.GgmlDType.Q4K)
@@ -79,9 +80,9 @@ def test_stream_rows_batch_invariant_and_repeatable(L):
     full = mm.forward(x).cpu().numpy()
     again = mm.forward(x).cpu().numpy()
     assert np.array_equal(full.view(np.uint32), again.view(np.uint32))
-    for r in (0, 5, 14):
-        two = mm.forward(x[r:r + 2].contiguous()).cpu().numpy()
-        assert np.array_equal(two.view(np.uint32), full[r:r + 2].view(np.uint32)), f"rows {r}, {r + 1}"
+    for r in (0, 5, 12):
+        four = mm.forward(x[r:r + 4].contiguous()).cpu().numpy()
+        assert np.array_equal(four.view(np.uint32), full[r:r + 4].view(np.uint32)), f"rows {r}..{r + 3}"
 
 
 def test_stream_epilogues(L):
