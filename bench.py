@@ -20,8 +20,9 @@ take half of a sweep step; `traffic` is the measured HBM bytes of a call
 
 `details` adds the other BASELINE configs (C1 Q8_0 decode, C3 Q4_K prefill
 TFLOP/s, C4 decoder-layer decode, C5 routed experts) measured the same way,
-plus the prefill of the Q8_0 and Q6_K weights on their own GEMMs and the C5
-experts at prefill routing (512 tokens), and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
+plus the prefill of the Q8_0 and Q6_K weights on their own GEMMs, Q4_K decode
+on a 132 MB weight (not launch-bound) and the C5 experts at prefill routing
+(512 tokens), and `cpu_baseline` times the C++ restatement of lloom-tensor's CPU QMatMul
 (oracle/kq_cpubase.c) on the same weights on a bounded sample.
 """
 import argparse
@@ -376,6 +377,26 @@ def run_details(L, cu, np, torch, dev, args):
         out["prefill_" + name + "_%dx%d" % (n, k)] = pf
         del rot
         torch.cuda.empty_cache()
+    # decode on a large weight (not a BASELINE config): Q4_K [28672, 8192],
+    # 132 MB, the FFN projection of a 70B-class model, where a call is not
+    # launch-bound; 4-16 rows (and 2-3 at this size) take the streaming
+    # MFMA kernel, one row the dot4 kernel
+    n, k = 28672, 8192
+    qt = L.QTensor.quantize(cu(L.synth_normal(6, n * k, 0.0, 0.02)).view(n, k), L.GgmlDType.Q4K)
+    rot = Rotation(qt, copies_for(qt.packed_bytes()))
+    big = {}
+    for bsz in (1, 2, 4, 8, 16):
+        x = cu(L.synth_normal(3000 + bsz, bsz * k)).view(bsz, k)
+        y = torch.empty((bsz, n), device=dev)
+        fns = [lambda t=t: L.QMatMul(t).forward_into(x, y) for t in rot.tensors] * 2
+        t = time_graph(fns, 3, 1) / len(fns)
+        b = qt.packed_bytes() + bsz * (k + n) * 4
+        big[str(bsz)] = {"us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1),
+                         "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+    big["note"] = "Q4_K [28672, 8192] (132 MB), rotating copies; not a BASELINE config"
+    out["decode_q4k_28672x8192"] = big
+    del rot
+    torch.cuda.empty_cache()
     # C4 decoder layer decode (q,k,v,o,gate,up in Q4_K; down in Q6_K)
     shapes = [("q", 2048, 2048, 12), ("k", 512, 2048, 12), ("v", 512, 2048, 12), ("o", 2048, 2048, 12),
               ("gate", 8192, 2048, 12), ("up", 8192, 2048, 12), ("down", 2048, 8192, 14)]

@@ -1,7 +1,8 @@
 """lloom_hip_qmatmul_noalloc (the allocation-free variant of lloom_hip_qmatmul,
 its workspace a static per-GPU device array) against lloom_hip_qmatmul,
 through the C ABI: two calls in a row, the second smaller, every route
-(decode dot4, MFMA decode with split K, the prefill GEMMs), bit for bit the
+(decode dot4, MFMA decode with split K, the streaming decode kernel, the
+prefill GEMMs), bit for bit the
 allocating entry point's output and within the matmul bar of the oracle; a
 call needing more than the scratch holds is refused by name."""
 import numpy as np
@@ -33,9 +34,10 @@ def _call(L, fn, qt, x, y):
     return fn(_ctx(0), int(qt.dtype), _ptr(qt.storage), n, k, _ptr(x), a, m, _ptr(y), a, _stream(x))
 
 
-# (dtype, n, k, first m, second m): decode, split-K decode, prefill GEMMs
+# (dtype, n, k, first m, second m): decode, split-K decode, prefill GEMMs,
+# and the streaming decode kernel (a 28 MB Q4_K weight at 16 and 4 rows)
 CASES = [(O.Q4K, 6144, 2048, 16, 1), (O.Q6K, 2048, 8192, 9, 4), (O.Q4K, 1024, 2048, 600, 40),
-         (O.Q8_0, 512, 2048, 300, 7), (O.Q6K, 256, 4096, 200, 64)]
+         (O.Q8_0, 512, 2048, 300, 7), (O.Q6K, 256, 4096, 200, 64), (O.Q4K, 12301, 4096, 16, 4)]
 
 
 @pytest.mark.parametrize("dt,n,k,m1,m2", CASES)
