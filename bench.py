@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--pmc-probe-moe", action="store_true",
                     help="launch only the C5 gate call (routed Q4_K experts, 32 tokens top-8), six times on two "
                          "alternating copies of the experts, for rocprofv3 --pmc runs on the routed kernel")
+    ap.add_argument("--pmc-probe-large", action="store_true",
+                    help="launch only the Q4_K [28672, 8192] decode (132 MB; --pmc-probe-b rows) on three cold "
+                         "weight copies, after a 64 MiB device copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     ap.add_argument("--pmc-probe-prefill", action="store_true",
                     help="launch only the C3 prefill GEMM at m=2048 (5 calls), for rocprofv3 --pmc runs on the "
                          "MFMA kernel")
@@ -205,6 +208,24 @@ def main():
             L.QMatMul(qt3).forward_into(x3, y3)
         torch.cuda.synchronize()
         print(json.dumps({"pmc_probe": "prefill_%s_m2048" % args.pmc_probe_type, "ops_per_call": 2 * m3 * n3 * k3}))
+        return
+
+    if args.pmc_probe_large:
+        nl, kl = 28672, 8192
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        qtl = L.QTensor.quantize(cu(L.synth_normal(6, nl * kl, 0.0, 0.02)).view(nl, kl), L.GgmlDType.Q4K)
+        rotl = Rotation(qtl, 3)
+        pb = args.pmc_probe_b
+        xl = cu(L.synth_normal(3000 + pb, pb * kl)).view(pb, kl)
+        yl = torch.empty((pb, nl), device=dev)
+        for i in range(6):
+            L.QMatMul(rotl.tensors[i % 3]).forward_into(xl, yl)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": "large_b%d" % pb, "algorithmic_bytes": qtl.packed_bytes() + pb * (kl + nl) * 4,
+                          "copy_bytes": 64 << 20}))
         return
 
     if args.pmc_probe:
