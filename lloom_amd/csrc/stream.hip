@@ -144,20 +144,24 @@ __global__ __launch_bounds__(64 * ST_WAVES) void k_mv_stream(const uint8_t* __re
     // per slot: arrivals (8 a tile, never reset) and tiles added so far
     uint32_t* arrived = (uint32_t*)(smem + C::RING + C::PART);
     uint32_t* added = arrived + R;
-    // prologue: the run's first D tiles, one a ring slot
-#pragma unroll
-    for (int d = 0; d < D; d++)
-        if (d < T) issue(tile_of(d), d, 0, NI);
-    // a use of every operand register: the compiler's waits for the loads
-    // above go here (behind the prologue DMAs, so they also wait for those
-    // tiles), not at the registers' first use inside the loop, where its
-    // counts would ignore the DMAs in flight
+    // prologue: the run's first tile, then a use of every operand register,
+    // where the compiler puts its waits for the loads above (they come
+    // after the first tile's DMAs, so it waits for that tile too, which the
+    // first dots need anyway; at the registers' first use inside the loop
+    // its counts would ignore the DMAs in flight), then tiles 1 .. D - 1.
+    // Issuing all D tiles first made every wave wait for all of them before
+    // its first dots (k = 8192: the first tile ready at 7.1 us, 10.6 for the
+    // second wave of each SIMD)
+    if (T > 0) issue(tile_of(0), 0, 0, NI);
 #pragma unroll
     for (int i = 0; i < S; i++) {
 #pragma unroll
         for (int q = 0; q < 8; q++) asm volatile("" : "+v"(av[i][q]));
         asm volatile("" : "+v"(ab[i]), "+v"(dy[i].x), "+v"(dy[i].y), "+v"(dy[i].z), "+v"(dy[i].w));
     }
+#pragma unroll
+    for (int d = 1; d < D; d++)
+        if (d < T) issue(tile_of(d), d, 0, NI);
 
     // Ring discipline, per superblock i of tile t (slot t mod D): wait until
     // the DMA instruction holding its last byte, need(i), has landed; compute
