@@ -414,6 +414,17 @@ def run_details(L, cu, np, torch, dev, args):
         b = qt.packed_bytes() + bsz * (k + n) * 4
         big[str(bsz)] = {"us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1),
                          "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+    for bsz in (1, 16):
+        # measured HBM bytes of the call (profiles/traffic_large_b*.json),
+        # quoted only for the kernel sources it measured
+        tpath = os.path.join(ROOT, "profiles", "traffic_large_b%d.json" % bsz)
+        if os.path.exists(tpath):
+            with open(tpath) as f:
+                prof = json.load(f)
+            if prof.get("csrc_digest") == csrc_digest(prof.get("digest_files")):
+                big[str(bsz)]["traffic"] = prof.get("hbm_bytes_per_launch")
+            else:
+                big[str(bsz)]["traffic_source"] = "stale: %s measured other kernel sources" % os.path.basename(tpath)
     big["note"] = "Q4_K [28672, 8192] (132 MB), rotating copies; not a BASELINE config"
     out["decode_q4k_28672x8192"] = big
     del rot
