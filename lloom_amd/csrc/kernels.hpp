@@ -48,6 +48,8 @@ hipError_t launch_mv_dma_ma(int type, const void* w, const float* x, float* y, i
 // k = 2048 with 2..4 rows):
 // the persistent pipelined MFMA decode kernel (the split quantizer in its
 // tiled layout, then one launch; workspace split_q8k_bytes).
+// CUs of the current device (asked once per device).
+int cu_count();
 bool mv_stream_fits(int type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_mv_stream(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t m,
                             void* ws, int epi, hipStream_t s);

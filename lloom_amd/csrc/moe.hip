@@ -14,6 +14,8 @@
 //     once per call and each activation element from L2 once per workgroup.
 //     k_moe_rows (activations read from L2 per row) is kept for rows too long
 //     to stage.
+#include <cstdlib>
+
 #include "kq_common.hpp"
 #include "kq_mfma.hpp"
 #include "kq_tasks.hpp"
@@ -898,6 +900,385 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MOEM_WAVES_
     }
 }
 
+// --------------------- Q4_K experts, decode-like routing, K split by wave --
+// A few planes an expert (decode: C5 routes 2.25 planes to each of 114
+// experts) on the fp16 MFMA arithmetic of k_moe_mfma, shaped like the dense
+// decode kernels instead: one workgroup per (expert, run of `tpw` pairs of
+// 16-row weight tiles; GLU: 16 rows of the gate and the same 16 of the up
+// weight), K/256 waves, wave w owning superblock w of every row.
+//  * the workgroup routes its expert's planes once, then streams its tile
+//    pairs through an LDS ring of S stages by 1 KB global_load_lds DMAs of
+//    whole rows, S - 1 pairs ahead of the pair it computes (every wave
+//    issues the same number of DMAs a stage, so a counted vmcnt wait and a
+//    barrier say a stage has landed);
+//  * each wave loads only its superblock of each routed plane (lane l: plane
+//    l % 8, the 8 elements 8 (l / 16) .. of each sub-block), scales it by
+//    its own power of two (max |x'| in [2^13, 2^14) over the superblock:
+//    exact) and splits it into fp16 hi + lo, with the 32-element sums / 32
+//    for the min term.  The hi parts of 8 planes fill MFMA rows 0-7 and
+//    their lo parts rows 8-15, so one 16x16x32 MFMA a sub-block gives both
+//    (decode routes fewer than 8 planes to most experts); with at most 8
+//    planes these operands stay in registers for the whole run;
+//  * per tile: sum_j sc_j S_j as 8 MFMAs (sc_j q exact fp16 integers), hi
+//    and lo rows added, and the min term as one more MFMA, then
+//    (d acc - 32 dmin accm) 2^-s; the K/256 partial sums meet in LDS and are
+//    added in superblock order.
+// More than 8 planes an expert take further passes over each staged pair.
+// Served for rows of 2048 elements (8 waves); see moe_dma_fits.
+
+// LDS pitch of a row of `bytes` (a multiple of 16): its dword count 4 mod 8,
+// so a 16-row b128 read takes two passes over the 32 banks, not sixteen.
+constexpr int lds_pitch16(int bytes) {
+    int p = (bytes + 15) & ~15;
+    while ((p / 4) % 8 != 4) p += 16;
+    return p;
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait_moe() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int NSB>
+struct MoedCfg {
+    static constexpr int RB = NSB * Q4K_BYTES;
+    static constexpr int WP = lds_pitch16(RB);
+    static constexpr int NI = (16 * WP + 1023) / 1024;  // 1 KB DMA instructions a tile
+    static constexpr int TILE = NI * 1024, STAGE = 2 * TILE;
+    static constexpr int DPW = (2 * NI + NSB - 1) / NSB;  // DMAs a wave issues a stage
+    static constexpr int PART = NSB * 2 * 64 * 16;
+    static constexpr int FIXED = PART + MOEM_FUSE_MAX * 4 + 16;
+    static constexpr int S = (160 * 1024 - FIXED) / STAGE >= 4 ? 4 : 3;
+    static constexpr int LDS = S * STAGE + FIXED;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert((S - 2) * DPW <= 63, "vmcnt counts to 63");
+};
+
+template <int NSB, bool GLU>
+__global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                      float* __restrict__ Y, const uint32_t* __restrict__ ids,
+                                                      int planes, int* ws, int* sticky, int E, int n, int in_dim1,
+                                                      int topk, const uint8_t* __restrict__ W2,
+                                                      float* __restrict__ Y2, int tpw) {
+    using C = MoedCfg<NSB>;
+    constexpr int K = NSB * 256, RB = C::RB, WP = C::WP, NI = C::NI, S = C::S, DPW = C::DPW;
+    constexpr int ROWS = GLU ? 16 : 32;  // weight rows of a tile pair (of each weight, GLU)
+    extern __shared__ __align__(16) uint8_t smem[];
+    float4* part = (float4*)(smem + S * C::STAGE);  // [NSB][2][64]
+    int* s_list = (int*)(smem + S * C::STAGE + C::PART);
+    int* s_np = s_list + MOEM_FUSE_MAX;
+    if (!GLU && blockIdx.z) {
+        W = W2;
+        Y = Y2;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int ntp = (n + ROWS - 1) / ROWS;
+    const int tp0 = blockIdx.x * tpw, T = min(tpw, ntp - tp0);
+    if (T <= 0) return;  // uniform
+    if ((int)blockIdx.y == E) {
+        // out-of-range ids: their planes are zero in every output
+        const int r0 = tp0 * ROWS, r1 = min(r0 + T * ROWS, n);
+        int bad = 0;
+        for (int p = tid; p < planes; p += 64 * NSB) {
+            if (ids[p] >= (uint32_t)E) {
+                bad = 1;
+                for (int r = r0; r < r1; r++) Y[(int64_t)p * n + r] = 0.0f;
+            }
+        }
+        bad = __syncthreads_or(bad);
+        if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) {
+            ws[0] = bad;  // this call: read back by a strict call
+            if (bad) sticky[0] = 1;
+        }
+        return;
+    }
+    const int e = blockIdx.y;
+    if (tid == 0) *s_np = 0;
+    __syncthreads();
+    // the list's order follows the LDS atomics; every plane's dot is
+    // computed on its own, so no result depends on it
+    for (int p = tid; p < planes; p += 64 * NSB)
+        if (ids[p] == (uint32_t)e) s_list[atomicAdd(s_np, 1)] = p;
+    __syncthreads();
+    const int np = *s_np;
+    if (np == 0) return;  // uniform
+
+    // this wave's DMA instructions of a stage: chunk q = wave + NSB i of the
+    // stage's 2 NI (tile q / NI, instruction q % NI; waves past the end
+    // repeat the last); a lane's 16 bytes are row r, byte cc of the tile
+    // (pad lanes reload the row's last piece, rows past n repeat row n - 1)
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    int rr[DPW], tsel[DPW];
+    uint32_t cc[DPW], ldo[DPW];
+#pragma unroll
+    for (int i = 0; i < DPW; i++) {
+        const int q = min(wv + NSB * i, 2 * NI - 1);
+        const int t = q / NI, ii = q - t * NI;
+        const int L = ii * 1024 + 16 * lane;
+        rr[i] = min(L / WP, 15);
+        cc[i] = (uint32_t)min(L - (L / WP) * WP, RB - 16);
+        tsel[i] = t;
+        ldo[i] = (uint32_t)(t * C::TILE + ii * 1024);
+    }
+    const uint32_t lds0 = lds_addr(smem);
+    const int64_t ebase = (int64_t)e * n * RB;
+    auto issue = [&](int it, int slot) {
+        const int tp = tp0 + min(it, T - 1);
+#pragma unroll
+        for (int i = 0; i < DPW; i++) {
+            const uint8_t* base = (GLU && tsel[i] ? W2 : W) + ebase;
+            const int trow0 = GLU ? tp * 16 : tp * 32 + 16 * tsel[i];
+            const uint32_t off = (uint32_t)min(trow0 + rr[i], n - 1) * (uint32_t)RB + cc[i];
+            dma16s(base, off, lds0 + (uint32_t)(slot * C::STAGE) + ldo[i]);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < S - 1; i++) issue(i, i);
+
+    const int sb = wave;
+    mh8 ax[8], am;
+    float inv[4];
+    // With one pass (at most 8 planes) a pair's outputs are stored at the
+    // start of the next iteration, before its DMAs: stores count in vmcnt,
+    // and a store issued after a stage's DMAs would make the counted wait
+    // for the stage before it wait for that stage too.
+    // (a wave adds one tile's partials, or both tiles' with one wave)
+    float pend[2][4];
+    int prow[2] = {-1, -1};
+    auto flush = [&]() {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            if (prow[u] >= 0 && prow[u] < n) {
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    if (g < 2 && 4 * g + v < np) Y[(int64_t)s_list[4 * g + v] * n + prow[u]] = pend[u][v];
+            }
+            prow[u] = -1;
+        }
+    };
+    for (int it = 0; it < T; it++) {
+        const int slot = it % S, tp = tp0 + it;
+        // pair it has landed (this wave's share, S - 2 later stages in
+        // flight; then everyone's), and every wave is done with slot it - 1
+        vm_wait_moe<(S - 2) * DPW>();
+        __syncthreads();
+        flush();
+        issue(it + S - 1, (it + S - 1) % S);
+        const uint8_t* st = smem + slot * C::STAGE;
+        for (int g0 = 0; g0 < np; g0 += 8) {
+            const int pg = min(8, np - g0);
+            if (it == 0 || np > 8) {  // uniform
+                // this lane's plane (c16 % 8: MFMA rows 0-7 take the planes'
+                // fp16 hi parts, rows 8-15 the lo parts) and its 64 elements
+                // of superblock sb; lanes past the pass's planes hold zeros
+                // (their MFMA rows are not stored)
+                const int pq = c16 & 7;
+                const int pl = s_list[g0 + min(pq, pg - 1)];
+                const int b = pl / topk, tk = pl - b * topk;
+                const float* xr = X + (int64_t)(b * in_dim1 + (in_dim1 == 1 ? 0 : tk)) * K + 256 * sb + 8 * g;
+                float4 xa[8][2];
+                const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                for (int j = 0; j < 8; j++) xa[j][0] = xa[j][1] = z4;
+                if (pq < pg) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        xa[j][0] = *(const float4*)(xr + 32 * j);
+                        xa[j][1] = *(const float4*)(xr + 32 * j + 4);
+                    }
+                }
+                float mx = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xa[j][h].x), fabsf(xa[j][h].y)),
+                                             fmaxf(fabsf(xa[j][h].z), fabsf(xa[j][h].w))));
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const bool fin = mx > 0.0f && mx <= 3.4028234e38f;
+                int ex = 0;
+                if (fin) (void)frexpf(mx, &ex);
+                const int sh = fin ? 14 - ex : 0;  // max |x'| in [2^13, 2^14)
+                const float scl = ldexpf(1.0f, sh);
+                // inverse scales of the planes of this lane's outputs (4g ..)
+                const float invs = ldexpf(1.0f, -sh);
+#pragma unroll
+                for (int v = 0; v < 4; v++) inv[v] = __shfl(invs, (4 * g + v) & 7, 64);
+                float ssum[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float vv[8] = {xa[j][0].x * scl, xa[j][0].y * scl, xa[j][0].z * scl, xa[j][0].w * scl,
+                                         xa[j][1].x * scl, xa[j][1].y * scl, xa[j][1].z * scl, xa[j][1].w * scl};
+                    float s = 0.0f;
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const _Float16 hu = (_Float16)vv[u];
+                        ax[j][u] = c16 < 8 ? hu : (_Float16)(vv[u] - (float)hu);
+                        s += vv[u];
+                    }
+                    ssum[j] = s;
+                }
+                // sub-block sums / 32 as the min-term operand: K 0..7 hi (g
+                // even), 8..15 lo (g odd); lanes g >= 2 meet zero weights
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    float s = ssum[j] + __shfl_xor(ssum[j], 16, 64);
+                    s += __shfl_xor(s, 32, 64);
+                    const float s32 = s * 0.03125f;
+                    const _Float16 hs = (_Float16)s32;
+                    am[j] = (g & 1) ? (_Float16)(s32 - (float)hs) : hs;
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                MfW<T_Q4K> wu;
+                mf_load<T_Q4K>(st + t * C::TILE + c16 * WP + sb * Q4K_BYTES, g, wu);
+                const uint4 hd = wu.hdr;
+                const uint32_t scw = hd.y & 0x3F3F3F3Fu, sch = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+                const uint2 sl = moe_b4_h(scw), shh = moe_b4_h(sch);
+                const mh2 scp[4] = {__builtin_bit_cast(mh2, sl.x), __builtin_bit_cast(mh2, sl.y),
+                                    __builtin_bit_cast(mh2, shh.x), __builtin_bit_cast(mh2, shh.y)};
+                // D[r][row]: rows r < 8 the planes' hi products, r >= 8 their
+                // lo products; two chains (even and odd sub-blocks)
+                mf4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int c = j >> 1, s4 = 4 * (j & 1);
+                    const uint32_t lo = (wu.q[c].x >> s4) & 0x0F0F0F0Fu, hi = (wu.q[c].y >> s4) & 0x0F0F0F0Fu;
+                    const _Float16 s1 = scp[j >> 1][j & 1];
+                    const mh2 sv = {s1, s1};
+                    const mh2 of = sv * (_Float16)(-1024.0f);
+                    const uint2 p0 = moe_nib4(lo, sv, of), p1 = moe_nib4(hi, sv, of);
+                    const mh8 bw = __builtin_bit_cast(mh8, make_uint4(p0.x, p0.y, p1.x, p1.y));
+                    if (j & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[j], bw, acc1, 0, 0, 0);
+                    else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[j], bw, acc0, 0, 0, 0);
+                }
+                // lane (g, c16), g < 2: plane 4g + v's hi sum here, its lo sum
+                // in lane (g + 2, c16)
+                const mf4 acc2 = acc0 + acc1;
+                mf4 acc;
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[v] = acc2[v] + __shfl_xor(acc2[v], 32, 64);
+                const float d = f16_to_f32(hd.x & 0xffffu), dmin = f16_to_f32(hd.x >> 16);
+                const uint32_t mnl = hd.z & 0x3F3F3F3Fu,
+                               mnh = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+                const uint2 ml = moe_b4_h(mnl), mh = moe_b4_h(mnh);
+                const mh8 bm = g < 2 ? __builtin_bit_cast(mh8, make_uint4(ml.x, ml.y, mh.x, mh.y)) : mh8{};
+                const mf4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const mf4 accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm, z, 0, 0, 0);
+                const float dm32 = 32.0f * dmin;
+                float o[4];
+#pragma unroll
+                for (int v = 0; v < 4; v++) o[v] = __builtin_fmaf(d, acc[v], -dm32 * accm[v]) * inv[v];
+                part[(sb * 2 + t) * 64 + lane] = make_float4(o[0], o[1], o[2], o[3]);
+            }
+            __syncthreads();
+            // add the NSB partials in superblock order; lane (g, c16) holds
+            // planes 4g .. 4g+3 of row c16 of the tile
+            constexpr int ITEMS = GLU ? 1 : 2;
+            for (int item = wave; item < ITEMS; item += NSB) {  // uniform
+                float4 sum[2];
+#pragma unroll
+                for (int u = 0; u < (GLU ? 2 : 1); u++) {
+                    const int t = GLU ? u : item;
+                    float4 a = part[t * 64 + lane];
+#pragma unroll
+                    for (int w = 1; w < NSB; w++) {
+                        const float4 p = part[(w * 2 + t) * 64 + lane];
+                        a.x += p.x;
+                        a.y += p.y;
+                        a.z += p.z;
+                        a.w += p.w;
+                    }
+                    sum[u] = a;
+                }
+                const int row = tp * ROWS + (GLU ? 0 : 16 * item) + c16;
+                const float s0[4] = {sum[0].x, sum[0].y, sum[0].z, sum[0].w};
+                const float s1[4] = {sum[1].x, sum[1].y, sum[1].z, sum[1].w};
+                float val[4];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    if constexpr (GLU) {
+                        const float y = s0[v], u = s1[v];
+                        val[v] = y / (1.0f + expf(-y)) * u;
+                    } else {
+                        val[v] = s0[v];
+                    }
+                }
+                if (np <= 8) {  // uniform: stored at the next iteration
+                    const int u = item >= NSB;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) pend[u][v] = val[v];
+                    prow[u] = row;
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int q = 4 * g + v;
+                        if (g < 2 && q < pg && row < n) Y[(int64_t)s_list[g0 + q] * n + row] = val[v];
+                    }
+                }
+            }
+            __syncthreads();  // part is rewritten by the next pass or pair
+        }
+    }
+    flush();
+    // no DMA (the repeated tail stages) may still be writing this
+    // workgroup's LDS when it exits
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+template <int NSB>
+static hipError_t moe_dma_nsb(const void* w, const float* x, float* y, const uint32_t* ids, int planes, int* ws,
+                              int* sticky, int E, int n, int in_dim1, int topk, const void* w2, float* y2, int mode,
+                              hipStream_t s) {
+    using C = MoedCfg<NSB>;
+    const bool glu = mode == MOE_GLU;
+    const int rows = glu ? 16 : 32;
+    const int ntp = (n + rows - 1) / rows;
+    // pairs a workgroup: about one round of workgroups over the CUs (as many
+    // a CU as the LDS holds), counting every expert as active
+    const int64_t per_cu = (160 * 1024) / C::LDS, slots = (int64_t)cu_count() * (per_cu > 0 ? per_cu : 1);
+    const int64_t layers = (int64_t)E * (mode == MOE_PAIR ? 2 : 1);
+    int tpw = (int)(((int64_t)ntp * layers + slots - 1) / slots);
+    tpw = tpw < 1 ? 1 : tpw > ntp ? ntp : tpw;
+    dim3 grid((ntp + tpw - 1) / tpw, E + 1, mode == MOE_PAIR ? 2 : 1);
+    const void* kern = glu ? (const void*)k_moe_dma<NSB, true> : (const void*)k_moe_dma<NSB, false>;
+    if (hipError_t e = set_lds_limit(kern, C::LDS)) return e;
+    if (glu)
+        hipLaunchKernelGGL((k_moe_dma<NSB, true>), grid, dim3(64 * NSB), C::LDS, s, (const uint8_t*)w, x, y, ids,
+                           planes, ws, sticky, E, n, in_dim1, topk, (const uint8_t*)w2, y2, tpw);
+    else
+        hipLaunchKernelGGL((k_moe_dma<NSB, false>), grid, dim3(64 * NSB), C::LDS, s, (const uint8_t*)w, x, y, ids,
+                           planes, ws, sticky, E, n, in_dim1, topk, (const uint8_t*)w2, y2, tpw);
+    return hipGetLastError();
+}
+
+// LLOOM_HIP_MOE_DMA (read once): 0 keeps decode-like Q4_K routing on
+// k_moe_lds; unset or 1 takes k_moe_dma where it fits.
+static bool moe_dma_on() {
+    static const bool v = [] {
+        const char* e = getenv("LLOOM_HIP_MOE_DMA");
+        return !e || atoi(e) != 0;
+    }();
+    return v;
+}
+
+// Rows of 2048 elements (8 superblocks, 8 waves) only: measured on C5's gate
+// and up calls 35.6 against 38.0 us for k_moe_lds, but on the down
+// projection (k = 768, 3 waves) 41.8 against 39.3.
+static bool moe_dma_fits(int type, int64_t n, int64_t k, int planes) {
+    return type == T_Q4K && k == 2048 && n >= 1 && planes <= MOEM_FUSE_MAX && moe_dma_on();
+}
+
+static hipError_t launch_moe_dma(const void* w, const float* x, float* y, const uint32_t* ids, int planes, int* ws,
+                                 int* sticky, int E, int n, int k, int in_dim1, int topk, const void* w2, float* y2,
+                                 int mode, hipStream_t s) {
+    if (k != 2048) return hipErrorInvalidValue;
+    return moe_dma_nsb<8>(w, x, y, ids, planes, ws, sticky, E, n, in_dim1, topk, w2, y2, mode, s);
+}
+
 template <int DEPTH, bool GLU>
 static hipError_t moe_mfma_cfg(const void* w, const float* x, float* y, const uint32_t* ids, int planes, int* ws,
                                int* sticky, int E, int n, int K, int in_dim1, int topk, int max_slots, int pgmax,
@@ -1023,6 +1404,11 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
     // Dense routing (prefill: many planes per expert) takes the fp16-MFMA
     // kernel, 16 planes a pass; decode-like routing keeps the VALU kernel
     // (C5, two planes an expert: 44 against 52 us for the MFMA kernel)
+    // Decode-like routing (fewer than MOE_MFMA_DENSITY planes an active
+    // expert) of Q4_K rows of 2048 elements: k_moe_dma, routed in-kernel
+    if (planes < MOE_MFMA_DENSITY * max_slots && moe_dma_fits(type, n, k, planes))
+        return launch_moe_dma(w, x, y, ids, planes, ws, sticky, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, w2,
+                              y2, mode, s);
     if (type == T_Q4K && moe_mfma_fits(k) && planes >= MOE_MFMA_DENSITY * max_slots) {
         int pgm = MOEM_LDS / moem_plane_bytes((int)k);
         pgm = pgm > 16 ? 16 : pgm < 1 ? 1 : pgm;

@@ -244,7 +244,7 @@ __global__ __launch_bounds__(64 * ST_WAVES) void k_mv_stream(const uint8_t* __re
 }
 
 // CUs of the current device, asked once per device.
-static int cu_count() {
+int cu_count() {
     static std::atomic<int> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
