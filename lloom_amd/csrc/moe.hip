@@ -15,6 +15,7 @@
 //     k_moe_rows (activations read from L2 per row) is kept for rows too long
 //     to stage.
 #include <cstdlib>
+#include <type_traits>
 
 #include "kq_common.hpp"
 #include "kq_mfma.hpp"
@@ -1037,24 +1038,29 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
     for (int i = 0; i < S - 1; i++) issue(i, i);
 
     const int sb = wave;
-    mh8 ax[8], am;
-    float inv[4];
-    // With one pass (at most 8 planes) a pair's outputs are stored at the
-    // start of the next iteration, before its DMAs: stores count in vmcnt,
-    // and a store issued after a stage's DMAs would make the counted wait
-    // for the stage before it wait for that stage too.
-    // (a wave adds one tile's partials, or both tiles' with one wave)
+    // the operands of up to two passes (16 planes) stay in registers for the
+    // run; past 16 planes every pass reloads its own into slot 0
+    mh8 ax[2][8], am[2];
+    float inv[2][4];
+    // With at most 16 planes a pair's outputs are stored at the start of the
+    // next iteration, before its DMAs: stores count in vmcnt, and a store
+    // issued after a stage's DMAs would make the counted wait for the stage
+    // before it wait for that stage too.  (A wave adds at most one item: NSB
+    // >= 2.)
+    static_assert(NSB >= 2, "one reduction item a wave");
     float pend[2][4];
     int prow[2] = {-1, -1};
     auto flush = [&]() {
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            if (prow[u] >= 0 && prow[u] < n) {
+        for (int ps = 0; ps < 2; ps++) {
+            if (prow[ps] >= 0 && prow[ps] < n) {
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    if (g < 2 && 4 * g + v < np) Y[(int64_t)s_list[4 * g + v] * n + prow[u]] = pend[u][v];
+                for (int v = 0; v < 4; v++) {
+                    const int q = 8 * ps + 4 * g + v;
+                    if (g < 2 && q < np) Y[(int64_t)s_list[q] * n + prow[ps]] = pend[ps][v];
+                }
             }
-            prow[u] = -1;
+            prow[ps] = -1;
         }
     };
     for (int it = 0; it < T; it++) {
@@ -1066,9 +1072,11 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
         flush();
         issue(it + S - 1, (it + S - 1) % S);
         const uint8_t* st = smem + slot * C::STAGE;
-        for (int g0 = 0; g0 < np; g0 += 8) {
+        // one pass of (up to) 8 planes from g0; PS: its operand slot
+        auto pass = [&](auto PSC, int g0, bool prep) {
+            constexpr int PS = decltype(PSC)::value;
             const int pg = min(8, np - g0);
-            if (it == 0 || np > 8) {  // uniform
+            if (prep) {  // uniform
                 // this lane's plane (c16 % 8: MFMA rows 0-7 take the planes'
                 // fp16 hi parts, rows 8-15 the lo parts) and its 64 elements
                 // of superblock sb; lanes past the pass's planes hold zeros
@@ -1105,7 +1113,7 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
                 // inverse scales of the planes of this lane's outputs (4g ..)
                 const float invs = ldexpf(1.0f, -sh);
 #pragma unroll
-                for (int v = 0; v < 4; v++) inv[v] = __shfl(invs, (4 * g + v) & 7, 64);
+                for (int v = 0; v < 4; v++) inv[PS][v] = __shfl(invs, (4 * g + v) & 7, 64);
                 float ssum[8];
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
@@ -1115,7 +1123,7 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
                         const _Float16 hu = (_Float16)vv[u];
-                        ax[j][u] = c16 < 8 ? hu : (_Float16)(vv[u] - (float)hu);
+                        ax[PS][j][u] = c16 < 8 ? hu : (_Float16)(vv[u] - (float)hu);
                         s += vv[u];
                     }
                     ssum[j] = s;
@@ -1128,7 +1136,7 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
                     s += __shfl_xor(s, 32, 64);
                     const float s32 = s * 0.03125f;
                     const _Float16 hs = (_Float16)s32;
-                    am[j] = (g & 1) ? (_Float16)(s32 - (float)hs) : hs;
+                    am[PS][j] = (g & 1) ? (_Float16)(s32 - (float)hs) : hs;
                 }
             }
 #pragma unroll
@@ -1152,8 +1160,8 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
                     const mh2 of = sv * (_Float16)(-1024.0f);
                     const uint2 p0 = moe_nib4(lo, sv, of), p1 = moe_nib4(hi, sv, of);
                     const mh8 bw = __builtin_bit_cast(mh8, make_uint4(p0.x, p0.y, p1.x, p1.y));
-                    if (j & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[j], bw, acc1, 0, 0, 0);
-                    else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[j], bw, acc0, 0, 0, 0);
+                    if (j & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[PS][j], bw, acc1, 0, 0, 0);
+                    else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[PS][j], bw, acc0, 0, 0, 0);
                 }
                 // lane (g, c16), g < 2: plane 4g + v's hi sum here, its lo sum
                 // in lane (g + 2, c16)
@@ -1167,11 +1175,11 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
                 const uint2 ml = moe_b4_h(mnl), mh = moe_b4_h(mnh);
                 const mh8 bm = g < 2 ? __builtin_bit_cast(mh8, make_uint4(ml.x, ml.y, mh.x, mh.y)) : mh8{};
                 const mf4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                const mf4 accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm, z, 0, 0, 0);
+                const mf4 accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[PS], bm, z, 0, 0, 0);
                 const float dm32 = 32.0f * dmin;
                 float o[4];
 #pragma unroll
-                for (int v = 0; v < 4; v++) o[v] = __builtin_fmaf(d, acc[v], -dm32 * accm[v]) * inv[v];
+                for (int v = 0; v < 4; v++) o[v] = __builtin_fmaf(d, acc[v], -dm32 * accm[v]) * inv[PS][v];
                 part[(sb * 2 + t) * 64 + lane] = make_float4(o[0], o[1], o[2], o[3]);
             }
             __syncthreads();
@@ -1207,11 +1215,10 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
                         val[v] = s0[v];
                     }
                 }
-                if (np <= 8) {  // uniform: stored at the next iteration
-                    const int u = item >= NSB;
+                if (np <= 16) {  // uniform: stored at the next iteration
 #pragma unroll
-                    for (int v = 0; v < 4; v++) pend[u][v] = val[v];
-                    prow[u] = row;
+                    for (int v = 0; v < 4; v++) pend[PS][v] = val[v];
+                    prow[PS] = row;
                 } else {
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
@@ -1221,6 +1228,12 @@ __global__ __launch_bounds__(64 * NSB) void k_moe_dma(const uint8_t* __restrict_
                 }
             }
             __syncthreads();  // part is rewritten by the next pass or pair
+        };
+        if (np <= 16) {  // uniform
+            pass(std::integral_constant<int, 0>{}, 0, it == 0);
+            if (np > 8) pass(std::integral_constant<int, 1>{}, 8, it == 0);
+        } else {
+            for (int g0 = 0; g0 < np; g0 += 8) pass(std::integral_constant<int, 0>{}, g0, true);
         }
     }
     flush();
@@ -1237,8 +1250,9 @@ static hipError_t moe_dma_nsb(const void* w, const float* x, float* y, const uin
     const bool glu = mode == MOE_GLU;
     const int rows = glu ? 16 : 32;
     const int ntp = (n + rows - 1) / rows;
-    // pairs a workgroup: about one round of workgroups over the CUs (as many
-    // a CU as the LDS holds), counting every expert as active
+    // pairs a workgroup: one round of workgroups over the CUs (as many a CU
+    // as the LDS holds) for every expert's runs (the routing density this
+    // kernel takes leaves few experts without planes)
     const int64_t per_cu = (160 * 1024) / C::LDS, slots = (int64_t)cu_count() * (per_cu > 0 ? per_cu : 1);
     const int64_t layers = (int64_t)E * (mode == MOE_PAIR ? 2 : 1);
     int tpw = (int)(((int64_t)ntp * layers + slots - 1) / slots);
@@ -1265,11 +1279,22 @@ static bool moe_dma_on() {
     return v;
 }
 
-// Rows of 2048 elements (8 superblocks, 8 waves) only: measured on C5's gate
-// and up calls 35.6 against 38.0 us for k_moe_lds, but on the down
-// projection (k = 768, 3 waves) 41.8 against 39.3.
-static bool moe_dma_fits(int type, int64_t n, int64_t k, int planes) {
-    return type == T_Q4K && k == 2048 && n >= 1 && planes <= MOEM_FUSE_MAX && moe_dma_on();
+// Rows of 2048 elements (8 superblocks, 8 waves) at 1.75 to 2.5 planes an
+// expert on average (7 E <= 4 planes < 10 E): where it measured faster.
+// C5's gate weight ([128, 768, 2048] Q4_K), T tokens top-8 (random experts),
+// graph replays on rotating copies, this kernel against k_moe_lds:
+//   T = 1, 8, 16, 24:   17, 37, 34, 34 us against 9.2, 17.4, 26.5, 30.8
+//                       (few planes leave most of this kernel's one-round
+//                       grid idle, and k_moe_lds's cost grows with planes)
+//   T = 28 .. 38:       33.4 - 36 us against 36.7 - 47
+//   T = 40, 48, 64:     57, 58, 58 us against 50, 50, 61 (some expert gets
+//                       more than 8 planes: two passes, and that expert's
+//                       two workgroups set the time)
+// At k = 768 (3 waves) it lost on C5's down projection (41.8 against 39.3).
+static bool moe_dma_fits(int type, int64_t n, int64_t k, int64_t E, int planes) {
+    const int64_t p4 = 4 * (int64_t)planes;
+    return type == T_Q4K && k == 2048 && n >= 1 && planes <= MOEM_FUSE_MAX && p4 >= 7 * E && p4 < 10 * E &&
+           moe_dma_on();
 }
 
 static hipError_t launch_moe_dma(const void* w, const float* x, float* y, const uint32_t* ids, int planes, int* ws,
@@ -1406,7 +1431,7 @@ hipError_t launch_moe(int type, const void* w, int64_t E, int64_t n, int64_t k, 
     // (C5, two planes an expert: 44 against 52 us for the MFMA kernel)
     // Decode-like routing (fewer than MOE_MFMA_DENSITY planes an active
     // expert) of Q4_K rows of 2048 elements: k_moe_dma, routed in-kernel
-    if (planes < MOE_MFMA_DENSITY * max_slots && moe_dma_fits(type, n, k, planes))
+    if (planes < MOE_MFMA_DENSITY * max_slots && moe_dma_fits(type, n, k, E, planes))
         return launch_moe_dma(w, x, y, ids, planes, ws, sticky, (int)E, (int)n, (int)k, (int)in_dim1, (int)topk, w2,
                               y2, mode, s);
     if (type == T_Q4K && moe_mfma_fits(k) && planes >= MOE_MFMA_DENSITY * max_slots) {

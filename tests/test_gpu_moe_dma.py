@@ -1,5 +1,5 @@
-"""GPU parity of the decode-routing Q4_K expert kernel (k_moe_dma: fewer
-than 8 planes an active expert, rows of 2048 elements) against the CPU
+"""GPU parity of the decode-routing Q4_K expert kernel (k_moe_dma: 1.75 to
+2.5 planes an expert on average, rows of 2048 elements) against the CPU
 oracle (matmul_indexed, the reference's matmul_t_indexed arithmetic,
 mod.rs:766-810) and a float64 dense reference, through the C ABI.
 
@@ -60,15 +60,16 @@ def _skewed_ids(rng, E, batch, topk, hot, hot_planes):
 
 
 # (E, n, k, batch, topk, in_dim1 is topk, planes on the hot expert)
-CASES = [(16, 200, 2048, 12, 8, False, 40), (16, 37, 2048, 12, 8, True, 20), (12, 64, 2048, 10, 6, False, 9),
-         (9, 8, 2048, 7, 4, True, 5), (20, 96, 2048, 16, 8, False, 17), (24, 48, 2048, 6, 8, True, 1),
-         (10, 2048, 2048, 8, 4, False, 3)]
+CASES = [(16, 200, 2048, 4, 8, False, 20), (16, 37, 2048, 4, 8, True, 12), (12, 64, 2048, 4, 6, False, 9),
+         (9, 8, 2048, 4, 4, True, 5), (20, 96, 2048, 5, 8, False, 17), (24, 48, 2048, 6, 8, True, 1),
+         (10, 2048, 2048, 5, 4, False, 3)]
 
 
 @pytest.mark.parametrize("E,n,k,batch,topk,per_slot,hot", CASES)
 def test_moe_dma_matches_oracle(L, E, n, k, batch, topk, per_slot, hot):
     rng = np.random.default_rng(E * 1000 + k + n)
-    assert batch * topk < 8 * min(E, batch * topk)  # decode-like routing
+    planes = batch * topk
+    assert 7 * E <= 4 * planes < 10 * E  # the routing density k_moe_dma takes
     w = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
     in_dim1 = topk if per_slot else 1
     x = rng.standard_normal((batch, in_dim1, k)).astype(np.float32)
@@ -89,7 +90,7 @@ def test_moe_dma_pair_glu_bits(L):
     """The pair launch is the two single calls bit for bit; the SwiGLU launch
     is silu(gate) * up of them (mod.rs:1365-1531)."""
     rng = np.random.default_rng(77)
-    E, n, k, batch, topk = 16, 100, 2048, 9, 8
+    E, n, k, batch, topk = 16, 100, 2048, 4, 8
     wg = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
     wu = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
     x = _cuda(rng.standard_normal((batch, 1, k)).astype(np.float32))
@@ -109,7 +110,7 @@ def test_moe_dma_pair_glu_bits(L):
 
 def test_moe_dma_bad_id(L):
     rng = np.random.default_rng(5)
-    E, n, k, batch, topk = 8, 40, 2048, 5, 4
+    E, n, k, batch, topk = 8, 40, 2048, 4, 4
     w = (rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)
     qt = L.QTensor.quantize(_cuda(w), O.Q4K)
     x = _cuda(rng.standard_normal((batch, 1, k)).astype(np.float32))
