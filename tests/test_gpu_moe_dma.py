@@ -130,3 +130,37 @@ def test_moe_dma_bad_id(L):
     got = qt.indexed_moe_forward(x, _cuda(good)).cpu().numpy()
     _rows_close(got, O.matmul_indexed(O.Q4K, qt.data(), E, n, k, x.cpu().numpy(), good.astype(np.uint32)),
                 "after a bad id")
+
+
+def test_moe_dma_graph_replays(L):
+    """The routed call and the SwiGLU launch captured in a graph: every
+    replay (eager calls of the other kernels in between) equals the eager
+    result bit for bit; the kernel clears its own LDS counters, so nothing
+    carries over from one replay to the next."""
+    rng = np.random.default_rng(91)
+    E, n, k, batch, topk = 16, 96, 2048, 4, 8
+    qg = L.QTensor.quantize(_cuda((rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)), O.Q4K)
+    qu = L.QTensor.quantize(_cuda((rng.standard_normal((E, n, k)) * 0.05).astype(np.float32)), O.Q4K)
+    x = _cuda(rng.standard_normal((batch, 1, k)).astype(np.float32))
+    ids = _cuda(_skewed_ids(rng, E, batch, topk, hot=2, hot_planes=10).astype(np.int32))
+    y = torch.empty((batch, topk, n), device="cuda")
+    yg = torch.empty_like(y)
+    eager = qg.indexed_moe_forward_into(x, ids, y).clone()
+    eager_glu = qg.indexed_moe_forward_glu_into(qu, x, ids, yg).clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            qg.indexed_moe_forward_into(x, ids, y)
+            qg.indexed_moe_forward_glu_into(qu, x, ids, yg)
+    torch.cuda.current_stream().wait_stream(s)
+    other_ids = _cuda(rng.integers(0, E, (1, topk)).astype(np.int32))
+    for i in range(3):
+        y.fill_(float("nan"))
+        yg.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager) and torch.equal(yg, eager_glu), i
+        qu.indexed_moe_forward(x[:1], other_ids)  # eager work on the other routed kernel
+        torch.cuda.synchronize()

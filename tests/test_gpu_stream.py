@@ -102,3 +102,29 @@ def test_stream_epilogues(L):
     g = torch.from_numpy(gate).cuda()
     mm.forward_mul_into(x, g)
     assert np.array_equal(g.cpu().numpy().view(np.uint32), (gate * plain).astype(np.float32).view(np.uint32))
+
+
+def test_stream_graph_replays(L):
+    """The streaming decode call captured in a graph: every replay (eager
+    calls of other shapes in between) equals the eager result bit for bit;
+    the kernel's LDS counters are cleared by the kernel itself."""
+    n, k, m = 12301, 4096, 8
+    qt = L.QTensor.quantize(torch.from_numpy(_weights(21, n, k)).cuda(), L.GgmlDType.Q4K)
+    mm = L.QMatMul.from_qtensor(qt)
+    x = torch.from_numpy(_x(22, m, k)).cuda()
+    y = torch.empty((m, n), device="cuda")
+    eager = mm.forward_into(x, y).clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            mm.forward_into(x, y)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), i
+        mm.forward(x[: 2 + i])  # eager calls on the other decode kernels
+        torch.cuda.synchronize()
