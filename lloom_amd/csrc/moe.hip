@@ -918,14 +918,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MOEM_WAVES_
 //    exact) and splits it into fp16 hi + lo, with the 32-element sums / 32
 //    for the min term.  The hi parts of 8 planes fill MFMA rows 0-7 and
 //    their lo parts rows 8-15, so one 16x16x32 MFMA a sub-block gives both
-//    (decode routes fewer than 8 planes to most experts); with at most 8
-//    planes these operands stay in registers for the whole run;
+//    (decode routes fewer than 8 planes to most experts); with at most 16
+//    planes (two passes) these operands stay in registers for the whole run;
 //  * per tile: sum_j sc_j S_j as 8 MFMAs (sc_j q exact fp16 integers), hi
 //    and lo rows added, and the min term as one more MFMA, then
 //    (d acc - 32 dmin accm) 2^-s; the K/256 partial sums meet in LDS and are
 //    added in superblock order.
-// More than 8 planes an expert take further passes over each staged pair.
-// Served for rows of 2048 elements (8 waves); see moe_dma_fits.
+// More than 8 planes an expert take further passes over each staged pair
+// (past 16, each reloading its operands).  Served for rows of 2048 elements
+// (8 waves); see moe_dma_fits.
 
 // LDS pitch of a row of `bytes` (a multiple of 16): its dword count 4 mod 8,
 // so a 16-row b128 read takes two passes over the 32 banks, not sixteen.
